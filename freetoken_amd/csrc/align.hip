@@ -1,0 +1,285 @@
+// Deterministic token -> expert permutation (moe_align_block_size) with an
+// optional expert-cache slot lookup in front of it.
+//
+// Contract (reference moe/fused.py:88-158, kernel/triton/moe_align.py:1-44):
+//   effective_E = num_experts + 1, ids outside [0, effective_E) ignored;
+//   counts padded to block_size, exclusive prefix sum -> region starts;
+//   expert_ids per block; num_tokens_post_pad; sorted_ids filled with the
+//   sentinel numel.  The reference ranks routes inside an expert with atomics;
+//   here the order is the canonical stable one: ascending flat route index.
+//
+// One workgroup of 16 waves does everything.  The routes are cut into 16
+// contiguous chunks, one per wave.  Pass 1 counts per (wave, expert) with LDS
+// atomics (order-free).  A scan over waves turns the counts into per-wave
+// bases, a scan over experts gives the padded region starts.  Pass 2 walks each
+// chunk in 64-route batches in order; a 64-key bitonic sort of
+// (expert << 6 | lane) inside the wave yields, for every route, its rank among
+// the equal-expert routes of the batch, so the final position is
+// region_start[e] + wave_base[w][e] + rank -- no atomics, fully deterministic.
+#include "kernels.h"
+
+namespace ftmoe {
+
+constexpr int kAlignWaves = 16;
+constexpr int kAlignThreads = kAlignWaves * kWave;
+
+
+// Block-wide exclusive scan of v over all threads (returns prefix, total in *tot).
+__device__ int block_exclusive_scan(int v, int* s_tmp, int* tot) {
+  const int lane = lane_id();
+  const int w = threadIdx.x / kWave;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  if (lane == kWave - 1) s_tmp[w] = x;
+  __syncthreads();
+  if (w == 0) {
+    int s = (lane < kAlignWaves) ? s_tmp[lane] : 0;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int y = __shfl_up(s, off, kWave);
+      if (lane >= off) s += y;
+    }
+    if (lane < kAlignWaves) s_tmp[kAlignWaves + lane] = s;  // inclusive per wave
+  }
+  __syncthreads();
+  const int wave_prefix = (w == 0) ? 0 : s_tmp[kAlignWaves + w - 1];
+  *tot = s_tmp[2 * kAlignWaves - 1];
+  __syncthreads();
+  return wave_prefix + x - v;
+}
+
+__global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
+  extern __shared__ int lds[];
+  const int eff = a.num_experts + 1;
+  int* wcount = lds;                          // [kAlignWaves][eff]
+  int* cum = wcount + kAlignWaves * eff;      // [eff + 1]
+  int* cnt = cum + eff + 1;                   // [eff]
+  int* seen = cnt + eff;                      // [table_size] (stats only)
+  __shared__ int s_tmp[2 * kAlignWaves];
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int w = tid / kWave;
+  const int chunk = ((a.numel + kAlignWaves - 1) / kAlignWaves + kWave - 1) / kWave * kWave;
+  const int c0 = w * chunk;
+  const int c1 = min(a.numel, c0 + chunk);
+
+  for (int i = tid; i < kAlignWaves * eff; i += kAlignThreads) wcount[i] = 0;
+  if (a.stats)
+    for (int i = tid; i < a.table_size; i += kAlignThreads) seen[i] = 0;
+  __syncthreads();
+
+  // ---- pass 0: optional slot lookup; pass 1: per-wave counts
+  long long missed = 0;
+  for (int i = c0 + lane; i < c1; i += kWave) {
+    int e = a.ids[i];
+    if (a.slot_for_id) {
+      const bool valid = e >= 0 && e < a.table_size;
+      const int s = valid ? a.slot_for_id[e] : -1;
+      if (a.slot_ids) a.slot_ids[i] = s;
+      if (a.miss_mask) a.miss_mask[i] = (valid && s < 0) ? 1 : 0;
+      if (a.stats && valid) seen[e] = 1;
+      if (valid && s < 0) ++missed;
+      e = s;
+    }
+    if (e >= 0 && e < eff) atomicAdd(&wcount[w * eff + e], 1);
+  }
+  __syncthreads();
+
+  // ---- scan over waves (per expert) and padded scan over experts
+  const int per = (eff + kAlignThreads - 1) / kAlignThreads;
+  int local = 0, local_seg = 0;
+  for (int q = 0; q < per; ++q) {
+    const int e = tid * per + q;
+    if (e < eff) {
+      int acc = 0;
+      for (int v = 0; v < kAlignWaves; ++v) {
+        const int t = wcount[v * eff + e];
+        wcount[v * eff + e] = acc;
+        acc += t;
+      }
+      cnt[e] = acc;
+      local += (acc + a.block_size - 1) / a.block_size * a.block_size;
+      local_seg += (e < a.num_experts && acc > 0) ? 1 : 0;
+    }
+  }
+  int total = 0, total_seg = 0;
+  int pre = block_exclusive_scan(local, s_tmp, &total);
+  int pre_seg = block_exclusive_scan(local_seg, s_tmp, &total_seg);
+  for (int q = 0; q < per; ++q) {
+    const int e = tid * per + q;
+    if (e < eff) {
+      cum[e] = pre;
+      const int c = cnt[e];
+      if (a.seg_expert && e < a.num_experts && c > 0) {
+        a.seg_expert[pre_seg] = e;
+        a.seg_start[pre_seg] = pre;
+        a.seg_count[pre_seg] = c;
+        ++pre_seg;
+      }
+      pre += (c + a.block_size - 1) / a.block_size * a.block_size;
+    }
+  }
+  if (tid == 0) {
+    cum[eff] = total;
+    a.ntpp[0] = total;
+    if (a.n_seg) a.n_seg[0] = total_seg;
+  }
+  // sentinel fill (ordered before the scatter by the barrier below)
+  for (int i = tid; i < a.max_padded; i += kAlignThreads) a.sorted_ids[i] = a.numel;
+  __syncthreads();
+  // expert id of every used block; -1 for unused blocks
+  for (int b = tid; b < a.max_blocks; b += kAlignThreads) {
+    int e = -1;
+    if (b * a.block_size < total) {
+      int lo = 0, hi = eff;  // largest e with cum[e] <= b*bs and cnt[e] > 0
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (cum[mid] <= b * a.block_size) lo = mid; else hi = mid;
+      }
+      e = lo;
+    }
+    a.expert_ids[b] = e;
+  }
+  if (a.stats && tid == 0) {
+    long long act = 0, miss = 0;
+    for (int e = 0; e < a.table_size; ++e)
+      if (seen[e]) {
+        ++act;
+        miss += (a.slot_for_id[e] < 0) ? 1 : 0;
+      }
+    a.stats[0] += act;
+    a.stats[1] += miss;
+    a.stats[2] += 1;
+  }
+
+  // ---- pass 2: stable scatter, 64 routes at a time per wave
+  for (int base = c0; base < c1; base += kWave) {
+    const int i = base + lane;
+    int e = -1;
+    if (i < c1) {
+      if (a.slot_for_id && a.slot_ids) {
+        e = a.slot_ids[i];  // written by this lane in pass 1 (may alias ids)
+      } else {
+        e = a.ids[i];
+        if (a.slot_for_id) e = (e >= 0 && e < a.table_size) ? a.slot_for_id[e] : -1;
+      }
+    }
+    const bool valid = e >= 0 && e < eff;
+    uint32_t key = (static_cast<uint32_t>(valid ? e : 0xFFFFF) << 6) | static_cast<uint32_t>(lane);
+#pragma unroll
+    for (int k = 2; k <= kWave; k <<= 1) {
+#pragma unroll
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const uint32_t other = __shfl_xor(key, j, kWave);
+        const bool up = (lane & k) == 0;
+        const bool lower = (lane & j) == 0;
+        key = (lower == up) ? min(key, other) : max(key, other);
+      }
+    }
+    const int se = static_cast<int>(key >> 6);
+    const int prev = __shfl(se, lane == 0 ? 0 : lane - 1, kWave);
+    const int next = __shfl(se, lane == kWave - 1 ? lane : lane + 1, kWave);
+    const bool head = lane == 0 || prev != se;
+    const bool tail = lane == kWave - 1 || next != se;
+    const unsigned long long heads = __ballot(head);
+    const unsigned long long upto = (lane == kWave - 1) ? ~0ull : ((2ull << lane) - 1ull);
+    const int run_start = kWave - 1 - __clzll(heads & upto);
+    const int rank = lane - run_start;
+    if (se < eff) {
+      const int src_lane = static_cast<int>(key & 63u);
+      const int pos = cum[se] + wcount[w * eff + se] + rank;
+      a.sorted_ids[pos] = base + src_lane;
+    }
+    // A wave issues its LDS reads (above) before this write, so every lane saw
+    // the base from before this batch.
+    if (se < eff && tail) wcount[w * eff + se] += rank + 1;
+  }
+  if (a.stats) {
+    // routes that missed, summed over the workgroup
+    __shared__ long long s_missed;
+    if (tid == 0) s_missed = 0;
+    __syncthreads();
+    if (missed) atomicAdd(reinterpret_cast<unsigned long long*>(&s_missed), static_cast<unsigned long long>(missed));
+    __syncthreads();
+    if (tid == 0) a.stats[3] += s_missed;
+  }
+}
+
+size_t align_lds_bytes(int num_experts, int table_size, bool stats) {
+  const int eff = num_experts + 1;
+  return sizeof(int) * (static_cast<size_t>(kAlignWaves) * eff + (eff + 1) + eff + (stats ? table_size : 0));
+}
+
+hipError_t launch_align(const AlignArgs& a, hipStream_t stream) {
+  const size_t lds = align_lds_bytes(a.num_experts, a.table_size, a.stats != nullptr);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(align_kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
+    if (err != hipSuccess) return err;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(align_kernel, dim3(1), dim3(kAlignThreads), lds, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace ftmoe
+
+namespace ftmoe {
+
+// Standalone expert-cache lookup: slot_ids[i] = slot_for_id[ids[i]] (-1 when
+// absent or out of range) with the accumulated counters of the reference's
+// decode statistics (distinct active / distinct missing experts, calls, missed
+// routes).  One workgroup; slot_ids may alias ids.
+__global__ void __launch_bounds__(1024) slot_map_kernel(const int32_t* ids, int numel, const int32_t* slot_for_id,
+                                                        int table_size, int32_t* slot_ids, uint8_t* miss_mask,
+                                                        long long* stats) {
+  extern __shared__ int seen[];
+  __shared__ unsigned long long s_missed;
+  const int tid = threadIdx.x;
+  if (stats) {
+    for (int i = tid; i < table_size; i += blockDim.x) seen[i] = 0;
+    if (tid == 0) s_missed = 0;
+    __syncthreads();
+  }
+  unsigned long long missed = 0;
+  for (int i = tid; i < numel; i += blockDim.x) {
+    const int e = ids[i];
+    const bool valid = e >= 0 && e < table_size;
+    const int s = valid ? slot_for_id[e] : -1;
+    slot_ids[i] = s;
+    if (miss_mask) miss_mask[i] = (valid && s < 0) ? 1 : 0;
+    if (stats && valid) seen[e] = 1;
+    missed += (valid && s < 0) ? 1 : 0;
+  }
+  if (!stats) return;
+  if (missed) atomicAdd(&s_missed, missed);
+  __syncthreads();
+  if (tid == 0) {
+    long long act = 0, miss = 0;
+    for (int e = 0; e < table_size; ++e)
+      if (seen[e]) {
+        ++act;
+        miss += slot_for_id[e] < 0 ? 1 : 0;
+      }
+    stats[0] += act;
+    stats[1] += miss;
+    stats[2] += 1;
+    stats[3] += static_cast<long long>(s_missed);
+  }
+}
+
+hipError_t launch_slot_map(const int32_t* ids, int numel, const int32_t* slot_for_id, int table_size,
+                           int32_t* slot_ids, uint8_t* miss_mask, long long* stats, hipStream_t stream) {
+  const size_t lds = stats ? sizeof(int) * static_cast<size_t>(table_size) : 0;
+  hipLaunchKernelGGL(slot_map_kernel, dim3(1), dim3(1024), lds, stream, ids, numel, slot_for_id, table_size,
+                     slot_ids, miss_mask, stats);
+  return hipGetLastError();
+}
+
+}  // namespace ftmoe

@@ -1,0 +1,249 @@
+// C ABI of the MoE-layer hot path (declarations and contracts: include/ftmoe.h).
+// Validates arguments on the host, carves the caller's workspace and launches
+// the kernels of route.hip, align.hip and decode.hip on the caller's stream.
+#include <cstdarg>
+#include <cstdio>
+#include <algorithm>
+#include <string>
+
+#include "../../include/ftmoe.h"
+
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_hip(hipError_t err, const char* what) {
+  if (err != hipSuccess) return fail(FTMOE_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
+  return FTMOE_OK;
+}
+
+constexpr size_t kAlignBytes = 256;
+
+size_t round_up(size_t v) { return (v + kAlignBytes - 1) / kAlignBytes * kAlignBytes; }
+
+// Sequential carve-out of a workspace buffer.
+struct Carver {
+  uint8_t* base;
+  size_t off = 0;
+  template <typename T>
+  T* take(size_t n) {
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off += round_up(n * sizeof(T));
+    return p;
+  }
+};
+
+int check_bank(const ftmoe_bank* b, const char* name, bool shared) {
+  if (!b) return fail(FTMOE_ERR_INVALID, "%s bank is NULL", name);
+  if (b->format < FTMOE_FMT_BF16 || b->format > FTMOE_FMT_MXFP4)
+    return fail(FTMOE_ERR_UNSUPPORTED, "%s bank: unknown format %d", name, b->format);
+  if (b->hidden <= 0 || b->inter <= 0 || b->hidden % 128 || b->inter % 128)
+    return fail(FTMOE_ERR_UNSUPPORTED, "%s bank: hidden %d / inter %d must be positive multiples of 128", name,
+                b->hidden, b->inter);
+  if (b->num_rows <= 0 || (shared && b->num_rows != 1))
+    return fail(FTMOE_ERR_INVALID, "%s bank: num_rows %d", name, b->num_rows);
+  if (!b->gate_up || !b->down) return fail(FTMOE_ERR_INVALID, "%s bank: NULL weights", name);
+  if (b->format != FTMOE_FMT_BF16 && (!b->gate_up_scale || !b->down_scale))
+    return fail(FTMOE_ERR_INVALID, "%s bank: NULL scales for a quantized format", name);
+  return FTMOE_OK;
+}
+
+struct DecodeLayout {
+  int32_t* sorted;
+  int32_t* expert_ids;
+  int32_t* ntpp;
+  int32_t* seg_expert;
+  int32_t* seg_start;
+  int32_t* seg_count;
+  int32_t* n_seg;
+  uint16_t* act;
+  uint16_t* ic3;
+  uint16_t* sh_out;
+  int act_stride;
+  size_t bytes;
+};
+
+DecodeLayout decode_layout(void* ws, int M, int k, const ftmoe_bank* bank, const ftmoe_bank* shared) {
+  DecodeLayout L{};
+  Carver c{static_cast<uint8_t*>(ws)};
+  const int numel = M * k;
+  L.sorted = c.take<int32_t>(numel);
+  L.expert_ids = c.take<int32_t>(numel);
+  L.ntpp = c.take<int32_t>(1);
+  L.seg_expert = c.take<int32_t>(bank->num_rows);
+  L.seg_start = c.take<int32_t>(bank->num_rows);
+  L.seg_count = c.take<int32_t>(bank->num_rows);
+  L.n_seg = c.take<int32_t>(1);
+  L.act_stride = shared ? std::max(bank->inter, shared->inter) : bank->inter;
+  L.act = c.take<uint16_t>(static_cast<size_t>(numel + M) * L.act_stride);
+  L.ic3 = c.take<uint16_t>(static_cast<size_t>(numel) * bank->hidden);
+  L.sh_out = shared ? c.take<uint16_t>(static_cast<size_t>(M) * bank->hidden) : nullptr;
+  L.bytes = c.off;
+  return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ftmoe_last_error(void) { return g_last_error.c_str(); }
+
+int ftmoe_version(void) { return 1; }
+
+int ftmoe_route_softmax_topk(const void* logits, int logits_dtype, int M, int E, int k, int renormalize,
+                             float* topk_w, int32_t* topk_ids, ftmoe_stream_t stream) {
+  if (!logits || !topk_w || !topk_ids) return fail(FTMOE_ERR_INVALID, "route_softmax_topk: NULL pointer");
+  if (logits_dtype != FTMOE_DTYPE_F32 && logits_dtype != FTMOE_DTYPE_BF16)
+    return fail(FTMOE_ERR_UNSUPPORTED, "route_softmax_topk: logits dtype %d", logits_dtype);
+  if (M < 0 || E <= 0 || E > 1024 || k <= 0 || k > E || k > 64)
+    return fail(FTMOE_ERR_UNSUPPORTED, "route_softmax_topk: M=%d E=%d k=%d (need E<=1024, 0<k<=min(E,64))", M, E, k);
+  if (M == 0) return FTMOE_OK;
+  return check_hip(ftmoe::launch_softmax_topk(logits, logits_dtype == FTMOE_DTYPE_BF16, M, E, k, renormalize,
+                                              topk_w, topk_ids, stream),
+                   "route_softmax_topk launch");
+}
+
+int ftmoe_route_grouped_sigmoid(const float* logits, const float* bias, int M, int E, int n_group, int topk_group,
+                                int k, int renormalize, float routed_scaling_factor, float* topk_w,
+                                int32_t* topk_ids, ftmoe_stream_t stream) {
+  if (!logits || !topk_w || !topk_ids) return fail(FTMOE_ERR_INVALID, "route_grouped_sigmoid: NULL pointer");
+  if (M < 0 || E <= 0 || E > 1024 || n_group <= 0 || n_group > 64 || E % n_group || topk_group <= 0 ||
+      topk_group > n_group || k <= 0 || k > 64 || k > E / n_group * topk_group)
+    return fail(FTMOE_ERR_UNSUPPORTED, "route_grouped_sigmoid: M=%d E=%d n_group=%d topk_group=%d k=%d", M, E,
+                n_group, topk_group, k);
+  if (n_group > 1 && E / n_group < 2)
+    return fail(FTMOE_ERR_UNSUPPORTED, "route_grouped_sigmoid: groups need >= 2 experts");
+  if (M == 0) return FTMOE_OK;
+  return check_hip(ftmoe::launch_grouped_sigmoid(logits, bias, M, E, n_group, topk_group, k, renormalize,
+                                                 routed_scaling_factor, topk_w, topk_ids, stream),
+                   "route_grouped_sigmoid launch");
+}
+
+void ftmoe_align_sizes(int numel, int num_experts, int block_size, int* max_padded, int* max_blocks) {
+  const long long mp = numel < num_experts + 1 ? static_cast<long long>(numel) * block_size
+                                               : numel + static_cast<long long>(num_experts + 1) * (block_size - 1);
+  if (max_padded) *max_padded = static_cast<int>(mp);
+  if (max_blocks) *max_blocks = static_cast<int>((mp + block_size - 1) / block_size);
+}
+
+int ftmoe_align(const int32_t* topk_ids, int numel, int num_experts, int block_size, int32_t* sorted_ids,
+                int32_t* expert_ids, int32_t* num_tokens_post_pad, ftmoe_stream_t stream) {
+  if (numel < 0 || num_experts <= 0 || num_experts > 1023 || block_size <= 0)
+    return fail(FTMOE_ERR_UNSUPPORTED, "align: numel=%d num_experts=%d block_size=%d", numel, num_experts,
+                block_size);
+  int max_padded = 0, max_blocks = 0;
+  ftmoe_align_sizes(numel, num_experts, block_size, &max_padded, &max_blocks);
+  if ((!topk_ids && numel) || (!sorted_ids && max_padded) || (!expert_ids && max_blocks) || !num_tokens_post_pad)
+    return fail(FTMOE_ERR_INVALID, "align: NULL pointer");
+  ftmoe::AlignArgs a{};
+  a.ids = topk_ids;
+  a.numel = numel;
+  a.num_experts = num_experts;
+  a.block_size = block_size;
+  a.sorted_ids = sorted_ids;
+  ftmoe_align_sizes(numel, num_experts, block_size, &a.max_padded, &a.max_blocks);
+  a.expert_ids = expert_ids;
+  a.ntpp = num_tokens_post_pad;
+  return check_hip(ftmoe::launch_align(a, stream), "align launch");
+}
+
+int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_id, int num_experts,
+                   int32_t* slot_ids, uint8_t* miss_mask, int64_t* stats, ftmoe_stream_t stream) {
+  if ((!topk_ids && numel) || !slot_for_id || !slot_ids) return fail(FTMOE_ERR_INVALID, "slot_map: NULL pointer");
+  if (numel < 0 || num_experts <= 0 || num_experts > 4096)
+    return fail(FTMOE_ERR_UNSUPPORTED, "slot_map: numel=%d num_experts=%d", numel, num_experts);
+  return check_hip(ftmoe::launch_slot_map(topk_ids, numel, slot_for_id, num_experts, slot_ids, miss_mask,
+                                          reinterpret_cast<long long*>(stats), stream),
+                   "slot_map launch");
+}
+
+size_t ftmoe_experts_decode_workspace(int M, int top_k, const ftmoe_bank* bank, const ftmoe_bank* shared) {
+  if (!bank || M <= 0 || top_k <= 0) return 0;
+  return decode_layout(nullptr, M, top_k, bank, shared).bytes;
+}
+
+int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
+                         const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
+                         int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
+                         ftmoe_stream_t stream) {
+  int rc = check_bank(bank, "routed", false);
+  if (rc) return rc;
+  if (shared) {
+    rc = check_bank(shared, "shared", true);
+    if (rc) return rc;
+    if (shared->hidden != bank->hidden) return fail(FTMOE_ERR_INVALID, "shared hidden %d != %d", shared->hidden, bank->hidden);
+  }
+  if (!x || !topk_w || !topk_ids || !y) return fail(FTMOE_ERR_INVALID, "experts_decode: NULL pointer");
+  if (M <= 0 || top_k <= 0) return fail(FTMOE_ERR_INVALID, "experts_decode: M=%d top_k=%d", M, top_k);
+  if (bank->num_rows > 1023) return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode: num_rows %d > 1023", bank->num_rows);
+  if (activation < FTMOE_ACT_SILU || activation > FTMOE_ACT_GELU_TANH)
+    return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode: activation %d", activation);
+  const DecodeLayout need = decode_layout(nullptr, M, top_k, bank, shared);
+  if (!workspace || workspace_bytes < need.bytes)
+    return fail(FTMOE_ERR_WORKSPACE, "experts_decode: workspace %zu < %zu bytes", workspace_bytes, need.bytes);
+  const DecodeLayout L = decode_layout(workspace, M, top_k, bank, shared);
+  const int numel = M * top_k;
+
+  ftmoe::AlignArgs al{};
+  al.ids = topk_ids;
+  al.numel = numel;
+  al.num_experts = bank->num_rows;
+  al.block_size = 1;
+  al.sorted_ids = L.sorted;
+  ftmoe_align_sizes(numel, bank->num_rows, 1, &al.max_padded, &al.max_blocks);
+  al.expert_ids = L.expert_ids;
+  al.ntpp = L.ntpp;
+  al.seg_expert = L.seg_expert;
+  al.seg_start = L.seg_start;
+  al.seg_count = L.seg_count;
+  al.n_seg = L.n_seg;
+  rc = check_hip(ftmoe::launch_align(al, stream), "experts_decode align");
+  if (rc) return rc;
+
+  ftmoe::DecodeArgs d{};
+  d.x = static_cast<const uint16_t*>(x);
+  d.topk_w = topk_w;
+  d.sorted = L.sorted;
+  d.seg_expert = L.seg_expert;
+  d.seg_start = L.seg_start;
+  d.seg_count = L.seg_count;
+  d.n_seg = L.n_seg;
+  d.M = M;
+  d.k = top_k;
+  d.H = bank->hidden;
+  d.I = bank->inter;
+  d.Is = shared ? shared->inter : 0;
+  d.max_seg = std::min(numel, bank->num_rows);
+  d.gate_up = {static_cast<const uint8_t*>(bank->gate_up), bank->gate_up_scale};
+  d.down = {static_cast<const uint8_t*>(bank->down), bank->down_scale};
+  if (shared) {
+    d.sh_gate_up = {static_cast<const uint8_t*>(shared->gate_up), shared->gate_up_scale};
+    d.sh_down = {static_cast<const uint8_t*>(shared->down), shared->down_scale};
+  }
+  d.act = L.act;
+  d.act_stride = L.act_stride;
+  d.ic3 = L.ic3;
+  d.sh_out = L.sh_out;
+  d.act_kind = activation;
+  d.weight_on_input = apply_router_weight_on_input;
+  rc = check_hip(ftmoe::launch_decode_stages(bank->format, shared ? shared->format : FTMOE_FMT_NONE, d, stream),
+                 "experts_decode stages");
+  if (rc) return rc;
+  return check_hip(ftmoe::launch_combine(L.ic3, topk_ids, bank->num_rows, L.sh_out, M, top_k, bank->hidden,
+                                         static_cast<uint16_t*>(y), stream),
+                   "experts_decode combine");
+}
+
+}  // extern "C"

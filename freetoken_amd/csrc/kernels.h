@@ -1,0 +1,68 @@
+// Argument structs and launch entry points shared by the kernels and the C ABI.
+#pragma once
+
+#include "ftmoe_common.h"
+
+namespace ftmoe {
+
+enum WFmt : int { FMT_BF16 = 0, FMT_FP8 = 1, FMT_MXFP4 = 2, FMT_NONE = -1 };
+
+struct AlignArgs {
+  const int32_t* ids;          // [numel] expert ids (or expert ids to map)
+  const int32_t* slot_for_id;  // nullable: [table_size] expert -> slot (-1 absent)
+  int table_size;
+  int32_t* slot_ids;           // nullable: mapped ids out [numel] (may alias ids)
+  uint8_t* miss_mask;          // nullable: [numel]
+  long long* stats;            // nullable: [4] accumulated counters
+  int numel;
+  int num_experts;             // experts of the aligned id space (slots if mapped)
+  int block_size;
+  int32_t* sorted_ids;         // [max_padded]
+  int max_padded;
+  int32_t* expert_ids;         // [max_blocks]
+  int max_blocks;
+  int32_t* ntpp;               // [1]
+  int32_t* seg_expert;         // nullable: [num_experts] compact segments
+  int32_t* seg_start;
+  int32_t* seg_count;
+  int32_t* n_seg;              // [1]
+};
+
+struct BankView {
+  const uint8_t* w;  // weights, [S, N, K] elements of the format
+  const void* s;     // fp8: float [S, N/128, K/128]; mxfp4: uint8 [S, N, K/32]; bf16: null
+};
+
+struct DecodeArgs {
+  const uint16_t* x;        // [M, H] bf16
+  const float* topk_w;      // [M*k]
+  const int32_t* sorted;    // route indices grouped by segment
+  const int32_t* seg_expert;
+  const int32_t* seg_start;
+  const int32_t* seg_count;
+  const int32_t* n_seg;
+  int M, k, H, I, Is;       // Is: shared expert intermediate size (0: none)
+  int max_seg;              // routed segments of the grid (the shared one follows)
+  BankView gate_up, down;   // routed bank
+  BankView sh_gate_up, sh_down;
+  uint16_t* act;            // [M*k + M, act_stride] bf16
+  int act_stride;
+  uint16_t* ic3;            // [M*k, H] bf16
+  uint16_t* sh_out;         // [M, H] bf16
+  int act_kind;
+  int weight_on_input;
+};
+
+hipError_t launch_softmax_topk(const void* logits, int logits_bf16, int M, int E, int k, int renorm, float* w,
+                               int32_t* ids, hipStream_t stream);
+hipError_t launch_grouped_sigmoid(const float* logits, const float* bias, int M, int E, int n_group,
+                                  int topk_group, int k, int renorm, float scale, float* w, int32_t* ids,
+                                  hipStream_t stream);
+hipError_t launch_align(const AlignArgs& a, hipStream_t stream);
+hipError_t launch_slot_map(const int32_t* ids, int numel, const int32_t* slot_for_id, int table_size,
+                           int32_t* slot_ids, uint8_t* miss_mask, long long* stats, hipStream_t stream);
+hipError_t launch_decode_stages(int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_combine(const uint16_t* ic3, const int32_t* ids, int num_rows, const uint16_t* sh_out, int M,
+                          int k, int H, uint16_t* y, hipStream_t stream);
+
+}  // namespace ftmoe

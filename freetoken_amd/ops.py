@@ -1,0 +1,229 @@
+"""Torch-tensor wrappers over the C ABI (device memory and streams only).
+
+Each wrapper validates dtypes/shapes like the reference's asserts, hands raw
+device pointers and the current HIP stream to ``libftmoe.so`` and returns
+torch tensors.  There is no CPU path: tensors must live on a ROCm device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("ftmoe ops take device (ROCm) tensors; no CPU fallback exists")
+        if t is not None and not t.is_contiguous():
+            raise ValueError("ftmoe ops take contiguous tensors")
+
+
+# --------------------------------------------------------------------------- routing
+
+
+def route_softmax_topk(logits: torch.Tensor, topk: int, renormalize: bool):
+    """Softmax top-k router (``fused_topk`` contract): returns (w fp32, ids int32)."""
+    _require_gpu(logits)
+    if logits.dtype == torch.float32:
+        dt = _lib.DTYPE_F32
+    elif logits.dtype == torch.bfloat16:
+        dt = _lib.DTYPE_BF16
+    else:
+        logits = logits.float()
+        dt = _lib.DTYPE_F32
+    m, e = logits.shape
+    w = torch.empty((m, topk), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((m, topk), dtype=torch.int32, device=logits.device)
+    check(
+        lib().ftmoe_route_softmax_topk(_ptr(logits), dt, m, e, topk, int(renormalize), _ptr(w), _ptr(ids),
+                                       _stream(logits.device)),
+        "route_softmax_topk",
+    )
+    return w, ids
+
+
+def route_grouped_sigmoid(logits: torch.Tensor, bias: torch.Tensor | None, n_group: int, topk_group: int,
+                          topk: int, renormalize: bool, scale: float):
+    """DeepSeek-V3 grouped sigmoid router: returns (w fp32, ids int32)."""
+    logits = logits.float().contiguous()
+    if bias is not None:
+        bias = bias.float().contiguous()
+    _require_gpu(logits, bias)
+    m, e = logits.shape
+    w = torch.empty((m, topk), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((m, topk), dtype=torch.int32, device=logits.device)
+    check(
+        lib().ftmoe_route_grouped_sigmoid(_ptr(logits), _ptr(bias), m, e, n_group, topk_group, topk,
+                                          int(renormalize), float(scale), _ptr(w), _ptr(ids),
+                                          _stream(logits.device)),
+        "route_grouped_sigmoid",
+    )
+    return w, ids
+
+
+# --------------------------------------------------------------------------- align / slots
+
+
+def align_sizes(numel: int, num_experts: int, block_size: int) -> tuple[int, int]:
+    mp, mb = ctypes.c_int(), ctypes.c_int()
+    lib().ftmoe_align_sizes(numel, num_experts, block_size, ctypes.byref(mp), ctypes.byref(mb))
+    return mp.value, mb.value
+
+
+def align(topk_ids: torch.Tensor, block_size: int, num_experts: int):
+    """moe_align_block_size with the canonical stable order."""
+    if topk_ids.dtype != torch.int32:
+        raise ValueError("topk_ids must be int32")
+    _require_gpu(topk_ids)
+    numel = topk_ids.numel()
+    mp, mb = align_sizes(numel, num_experts, block_size)
+    dev = topk_ids.device
+    sorted_ids = torch.empty((mp,), dtype=torch.int32, device=dev)
+    expert_ids = torch.empty((mb,), dtype=torch.int32, device=dev)
+    ntpp = torch.empty((1,), dtype=torch.int32, device=dev)
+    check(
+        lib().ftmoe_align(_ptr(topk_ids), numel, num_experts, block_size, _ptr(sorted_ids), _ptr(expert_ids),
+                          _ptr(ntpp), _stream(dev)),
+        "align",
+    )
+    return sorted_ids, expert_ids, ntpp
+
+
+def slot_map(topk_ids: torch.Tensor, slot_for_id: torch.Tensor, out: torch.Tensor | None = None,
+             miss_mask: torch.Tensor | None = None, stats: torch.Tensor | None = None) -> torch.Tensor:
+    """Expert id -> cache slot (-1 = not resident); ``out`` may be ``topk_ids``."""
+    if topk_ids.dtype != torch.int32 or slot_for_id.dtype != torch.int32:
+        raise ValueError("topk_ids and slot_for_id must be int32")
+    _require_gpu(topk_ids, slot_for_id, out, miss_mask, stats)
+    if out is None:
+        out = torch.empty_like(topk_ids)
+    if stats is not None and stats.dtype != torch.int64:
+        raise ValueError("stats must be int64[4]")
+    check(
+        lib().ftmoe_slot_map(_ptr(topk_ids), topk_ids.numel(), _ptr(slot_for_id), slot_for_id.numel(), _ptr(out),
+                             _ptr(miss_mask), _ptr(stats), _stream(topk_ids.device)),
+        "slot_map",
+    )
+    return out
+
+
+# --------------------------------------------------------------------------- expert banks
+
+_FORMATS = {"bf16": _lib.FMT_BF16, "fp8_block": _lib.FMT_FP8_B128, "mxfp4": _lib.FMT_MXFP4}
+
+
+@dataclass
+class ExpertBank:
+    """Device tensors of one expert bank (see ftmoe_bank in include/ftmoe.h).
+
+    fmt "bf16": gate_up [S,2I,H] bf16, down [S,H,I] bf16.
+    fmt "fp8_block": e4m3 (float8_e4m3fn or uint8) gate_up/down with float32
+    (or bf16, converted once) 128x128 block scales.
+    fmt "mxfp4": uint8 packed [S,2I,H/2] / [S,H,I/2] with uint8 e8m0 scales
+    [S,2I,H/32] / [S,H,I/32].
+    """
+
+    fmt: str
+    gate_up: torch.Tensor
+    down: torch.Tensor
+    gate_up_scale: torch.Tensor | None = None
+    down_scale: torch.Tensor | None = None
+
+    def __post_init__(self):
+        if self.fmt not in _FORMATS:
+            raise ValueError(f"unknown expert format {self.fmt!r}")
+        if self.fmt == "fp8_block":
+            for name in ("gate_up_scale", "down_scale"):
+                s = getattr(self, name)
+                if s is None:
+                    raise ValueError(f"fp8_block bank needs {name}")
+                if s.dtype != torch.float32:
+                    setattr(self, name, s.float().contiguous())
+        if self.fmt == "bf16" and self.gate_up.dtype != torch.bfloat16:
+            raise ValueError("bf16 bank weights must be torch.bfloat16")
+
+    @property
+    def num_rows(self) -> int:
+        return self.gate_up.shape[0]
+
+    @property
+    def hidden(self) -> int:
+        return self.down.shape[1]
+
+    @property
+    def inter(self) -> int:
+        return self.gate_up.shape[1] // 2
+
+    def cstruct(self) -> _lib.FtmoeBank:
+        _require_gpu(self.gate_up, self.down, self.gate_up_scale, self.down_scale)
+        return _lib.FtmoeBank(
+            _FORMATS[self.fmt], self.num_rows, self.hidden, self.inter,
+            _ptr(self.gate_up), _ptr(self.gate_up_scale), _ptr(self.down), _ptr(self.down_scale),
+        )
+
+
+class _Workspace:
+    """Per-device scratch buffer, grown on demand (never during graph capture:
+    size it with a warm-up call at the largest batch first)."""
+
+    def __init__(self):
+        self.buf: dict[int, torch.Tensor] = {}
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        cur = self.buf.get(idx)
+        if cur is None or cur.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("ftmoe workspace must be sized before graph capture (run one eager call)")
+            cur = torch.empty((max(nbytes, 1 << 20),), dtype=torch.uint8, device=device)
+            self.buf[idx] = cur
+        return cur
+
+
+_WS = _Workspace()
+
+
+def experts_decode(x: torch.Tensor, topk_w: torch.Tensor, topk_ids: torch.Tensor, bank: ExpertBank,
+                   shared: ExpertBank | None = None, activation: str = "silu",
+                   apply_router_weight_on_input: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode-regime experts (+ optional shared expert) for a precomputed routing."""
+    if x.dtype != torch.bfloat16:
+        raise ValueError("hidden_states must be bfloat16")
+    if topk_w.dtype != torch.float32 or topk_ids.dtype != torch.int32:
+        raise ValueError("topk_weights must be float32 and topk_ids int32")
+    if topk_w.shape != topk_ids.shape:
+        raise ValueError("topk shape mismatch")
+    if activation not in _lib.ACT:
+        raise ValueError(f"Unsupported activation: {activation}")
+    _require_gpu(x, topk_w, topk_ids)
+    m, k = topk_ids.shape
+    if x.shape[0] != m:
+        raise ValueError("Number of tokens mismatch")
+    b = bank.cstruct()
+    sb = shared.cstruct() if shared is not None else None
+    bp = ctypes.byref(b)
+    sp = ctypes.byref(sb) if sb is not None else None
+    nbytes = lib().ftmoe_experts_decode_workspace(m, k, bp, sp)
+    ws = _WS.get(x.device, nbytes)
+    y = out if out is not None else torch.empty_like(x)
+    check(
+        lib().ftmoe_experts_decode(_ptr(x), m, k, _ptr(topk_w), _ptr(topk_ids), bp, sp, _lib.ACT[activation],
+                                   int(apply_router_weight_on_input), _ptr(y), _ptr(ws), ws.numel(),
+                                   _stream(x.device)),
+        "experts_decode",
+    )
+    return y

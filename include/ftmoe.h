@@ -1,0 +1,137 @@
+/*
+ * ftmoe -- C ABI of the MI355X (gfx950) fused MoE-layer hot path.
+ *
+ * Every entry point:
+ *   - is extern "C", takes plain pointers and sizes (device pointers unless
+ *     stated), and runs asynchronously on the given HIP stream (NULL = the
+ *     default stream); none synchronises the host and none allocates device
+ *     memory -- scratch comes from a caller-provided workspace whose size is
+ *     reported by the matching *_workspace() query;
+ *   - returns FTMOE_OK (0) or a negative ftmoe_status; the message of the last
+ *     failure on the calling thread is available from ftmoe_last_error();
+ *   - uses fixed shapes and no host reads of device data, so it can be captured
+ *     in a HIP graph.
+ *
+ * Number formats: bf16 is passed as uint16 bit patterns; fp8 is OCP e4m3fn;
+ * fp4 is OCP e2m1 packed two per byte, low nibble = even k; e8m0 scale codes
+ * decode to 2^(code-127).
+ *
+ * Reference interfaces (paths relative to python/freetoken/ of FreeToken) are
+ * cited on each declaration.
+ */
+#ifndef FTMOE_H
+#define FTMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* ftmoe_stream_t; /* == hipStream_t */
+
+enum ftmoe_status {
+  FTMOE_OK = 0,
+  FTMOE_ERR_INVALID = -1,     /* bad argument (null pointer, shape mismatch) */
+  FTMOE_ERR_UNSUPPORTED = -2, /* valid but unsupported shape or format */
+  FTMOE_ERR_HIP = -3,         /* a HIP runtime call failed */
+  FTMOE_ERR_WORKSPACE = -4    /* workspace smaller than *_workspace() */
+};
+
+enum ftmoe_dtype { FTMOE_DTYPE_F32 = 0, FTMOE_DTYPE_BF16 = 1 };
+
+enum ftmoe_format {
+  FTMOE_FMT_NONE = -1,
+  FTMOE_FMT_BF16 = 0,     /* bf16 weights */
+  FTMOE_FMT_FP8_B128 = 1, /* e4m3 weights + float32 128x128 block scales */
+  FTMOE_FMT_MXFP4 = 2     /* e2m1 weights + e8m0 scale per 32 K (row-major "ds_fp4" layout) */
+};
+
+enum ftmoe_activation { FTMOE_ACT_SILU = 0, FTMOE_ACT_GELU = 1, FTMOE_ACT_GELU_TANH = 2 };
+
+/* Indices of the int64 counters accumulated by ftmoe_slot_map (moe/offload_cache.py:205-229). */
+enum ftmoe_stat { FTMOE_STAT_ACTIVE = 0, FTMOE_STAT_MISS = 1, FTMOE_STAT_CALLS = 2, FTMOE_STAT_MISSED_ROUTES = 3 };
+
+/* One expert bank: S rows (experts, or expert-cache slots), each a SwiGLU MLP.
+ * Layouts follow layers/moe.py:60-92 and kernel/triton/dsv4/fused_moe.py:10-14:
+ *   gate_up [S, 2I, H] (gate rows [0,I), up rows [I,2I)), down [S, H, I];
+ *   FP8_B128: gate_up_scale float [S, 2I/128, H/128], down_scale float [S, H/128, I/128];
+ *   MXFP4:    gate_up [S, 2I, H/2] bytes, gate_up_scale uint8 [S, 2I, H/32],
+ *             down [S, H, I/2] bytes, down_scale uint8 [S, H, I/32];
+ *   BF16:     scales NULL.
+ * H and I must be multiples of 128. */
+typedef struct ftmoe_bank {
+  int format;
+  int num_rows;
+  int hidden;
+  int inter;
+  const void* gate_up;
+  const void* gate_up_scale;
+  const void* down;
+  const void* down_scale;
+} ftmoe_bank;
+
+const char* ftmoe_last_error(void);
+int ftmoe_version(void);
+
+/* Softmax top-k router; replaces fused_topk (moe/fused.py:38-85, torch fallback
+ * :16-35).  logits [M,E] float32 or bf16 (logits_dtype); selection on the fp32
+ * logits, ties to the lower expert index; with renormalize the k weights are
+ * the softmax over the selected logits, else the softmax over all E.
+ * Writes topk_w float32 [M,k] and topk_ids int32 [M,k] in rank order.
+ * E <= 1024, k <= min(E, 64). */
+int ftmoe_route_softmax_topk(const void* logits, int logits_dtype, int M, int E, int k, int renormalize,
+                             float* topk_w, int32_t* topk_ids, ftmoe_stream_t stream);
+
+/* DeepSeek-V3 grouped sigmoid router; replaces Glm4MoeSparseBlock._route /
+ * _group_limited (models/glm4_moe/moe.py:53-75).  logits float32 [M,E]; bias
+ * float32 [E] or NULL; E % n_group == 0, n_group <= 64, E <= 1024. */
+int ftmoe_route_grouped_sigmoid(const float* logits, const float* bias, int M, int E, int n_group, int topk_group,
+                                int k, int renormalize, float routed_scaling_factor, float* topk_w,
+                                int32_t* topk_ids, ftmoe_stream_t stream);
+
+/* Buffer sizes of ftmoe_align (moe/fused.py:139-147). */
+void ftmoe_align_sizes(int numel, int num_experts, int block_size, int* max_num_tokens_padded,
+                       int* max_num_m_blocks);
+
+/* moe_align_block_size (moe/fused.py:88-158; kernel/triton/moe_align.py:216-325)
+ * with the canonical stable order (ascending flat route index inside each
+ * expert).  sorted_ids [max_num_tokens_padded] (sentinel numel in unused
+ * slots), expert_ids [max_num_m_blocks] (-1 for unused blocks),
+ * num_tokens_post_pad [1].  num_experts <= 1023. */
+int ftmoe_align(const int32_t* topk_ids, int numel, int num_experts, int block_size, int32_t* sorted_ids,
+                int32_t* expert_ids, int32_t* num_tokens_post_pad, ftmoe_stream_t stream);
+
+/* Expert-cache indirection: slot_ids[i] = slot_for_id[topk_ids[i]] (-1 when the
+ * expert is not resident or the id is out of range); replaces the id -> slot
+ * rewrite of OffloadMoeCache.ensure_experts (moe/offload_cache.py:800-810,
+ * moe/offload_kernels.py:185-188) without admission.  slot_ids may alias
+ * topk_ids (in-place rewrite).  miss_mask (nullable) [numel] = 1 where the
+ * route missed.  stats (nullable) int64 [4] is ACCUMULATED:
+ * active distinct experts, missing distinct experts, calls, missed routes. */
+int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_id, int num_experts,
+                   int32_t* slot_ids, uint8_t* miss_mask, int64_t* stats, ftmoe_stream_t stream);
+
+/* Decode (W8A16 / W4A16 / bf16) expert computation for a precomputed routing;
+ * replaces fused_experts_decode_impl (moe/fused.py:340-423),
+ * fused_experts_decode_fp8_block (moe/fused_fp8_block.py:32-44) and
+ * routed_experts_fp4 (moe/fused_ds_fp4.py:97-132, without the DSV4 FP8
+ * activation round trip), plus the shared-expert add of the model block
+ * (models/glm4_moe/moe.py:81-82).
+ *   x bf16 [M,H]; topk_w float32 [M,k]; topk_ids int32 [M,k] index bank rows
+ *   (ids outside [0, num_rows) are skipped); shared: nullable bank with
+ *   num_rows == 1 whose output is added; y bf16 [M,H] (may not alias x).
+ * apply_router_weight_on_input scales the gate_up outputs instead of the
+ * down outputs (moe/fused.py:240). */
+size_t ftmoe_experts_decode_workspace(int M, int top_k, const ftmoe_bank* bank, const ftmoe_bank* shared);
+int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
+                         const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
+                         int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
+                         ftmoe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FTMOE_H */

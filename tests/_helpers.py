@@ -1,0 +1,47 @@
+"""Shared helpers of the GPU parity tests: upload oracle banks, run layers."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from freetoken_amd.ops import ExpertBank
+from oracle.experts import Bank
+
+_FMT = {"bf16": "bf16", "fp8": "fp8_block", "mxfp4": "mxfp4"}
+
+
+def to_device_bank(bank: Bank, dev, rows=None) -> ExpertBank:
+    sl = slice(None) if rows is None else rows
+
+    def t(a, dtype=None):
+        x = torch.from_numpy(np.ascontiguousarray(a[sl])).to(dev)
+        return x.to(dtype) if dtype is not None else x
+
+    if bank.fmt == "bf16":
+        return ExpertBank("bf16", t(bank.gate_up, torch.bfloat16), t(bank.down, torch.bfloat16))
+    if bank.fmt == "fp8":
+        return ExpertBank(
+            "fp8_block",
+            t(bank.gate_up).view(torch.float8_e4m3fn),
+            t(bank.down).view(torch.float8_e4m3fn),
+            t(bank.gate_up_scale),
+            t(bank.down_scale),
+        )
+    return ExpertBank("mxfp4", t(bank.gate_up), t(bank.down), t(bank.gate_up_scale), t(bank.down_scale))
+
+
+def bf16_dev(a, dev) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev).to(torch.bfloat16)
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    if t.dtype == torch.bfloat16:
+        t = t.float()
+    return t.detach().cpu().numpy()
+
+
+def sub_bank(bank: Bank, rows) -> Bank:
+    """Rows of a bank (e.g. the resident experts of a slot cache)."""
+    f = (lambda a: None if a is None else np.ascontiguousarray(a[rows]))
+    return Bank(bank.fmt, f(bank.gate_up), f(bank.down), f(bank.gate_up_scale), f(bank.down_scale))

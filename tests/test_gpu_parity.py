@@ -1,0 +1,225 @@
+"""GPU parity of the HIP path against the CPU oracle (bit-exact routing and
+permutation; bf16 outputs within max-rel 2e-2 and cosine >= 0.9995)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import synth
+from oracle.numerics import bf16_round
+from freetoken_amd import ops
+
+from _helpers import bf16_dev, sub_bank, to_device_bank, to_np
+from conftest import COS_TOL, MAX_REL_TOL, cosine, max_rel
+
+pytestmark = pytest.mark.gpu
+
+
+# ----------------------------------------------------------------- routing
+
+
+@pytest.mark.parametrize("E,k", [(16, 2), (128, 8), (160, 8), (256, 8), (1024, 6)])
+@pytest.mark.parametrize("renorm", [True, False])
+@pytest.mark.parametrize("bf16", [True, False])
+def test_softmax_topk_exact(dev, E, k, renorm, bf16):
+    rng = np.random.default_rng(E * 10 + k)
+    lg = synth.tied_logits(rng, 67, E, bf16=bf16)
+    w_ref, ids_ref = oracle.routing.softmax_topk(lg, k, renorm)
+    t = torch.from_numpy(lg).to(dev)
+    t = t.to(torch.bfloat16) if bf16 else t
+    w, ids = ops.route_softmax_topk(t, k, renorm)
+    np.testing.assert_array_equal(to_np(ids), ids_ref)
+    np.testing.assert_allclose(to_np(w), w_ref, rtol=2e-6, atol=1e-7)
+
+
+def test_softmax_topk_reference_kat(dev):
+    # tests/moe/test_fused_moe.py:42-58 of the reference
+    lg = torch.tensor([[4.0, 1.0, -1.0, 2.0], [0.5, 3.0, 2.0, -2.0]], device=dev, dtype=torch.bfloat16)
+    w, ids = ops.route_softmax_topk(lg, 2, True)
+    ref_l, ref_i = torch.topk(lg.float().cpu(), 2, dim=-1)
+    np.testing.assert_array_equal(to_np(ids), ref_i.numpy())
+    np.testing.assert_allclose(to_np(w), torch.softmax(ref_l, -1).numpy(), rtol=2e-4, atol=2e-4)
+
+
+@pytest.mark.parametrize("M", [1, 7, 64, 256, 8192])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_grouped_sigmoid_exact(dev, M, with_bias):
+    rng = np.random.default_rng(M + (7 if with_bias else 0))
+    E = 256
+    lg = synth.tied_logits(rng, M, E, bf16=False) + synth.zipf_bias(rng, E)[None, :]
+    bias = synth.normal(rng, (E,), 0.1) if with_bias else None
+    w_ref, ids_ref = oracle.routing.grouped_sigmoid_topk(lg, bias, 8, 4, 8, True, 2.5)
+    tb = None if bias is None else torch.from_numpy(bias).to(dev)
+    w, ids = ops.route_grouped_sigmoid(torch.from_numpy(lg).to(dev), tb, 8, 4, 8, True, 2.5)
+    np.testing.assert_array_equal(to_np(ids), ids_ref)
+    np.testing.assert_allclose(to_np(w), w_ref, rtol=1e-6, atol=1e-7)
+
+
+def test_grouped_sigmoid_ties_and_flips(dev):
+    E, G = 64, 8
+    lg = np.zeros((4, E), dtype=np.float32)  # all equal: lowest groups, lowest experts
+    lg[1, :] = 1.0
+    lg[1, 40:48] = 3.0  # group 5 dominates
+    lg[2] = np.tile(np.arange(8, dtype=np.float32), 8)  # every group ties
+    bias = np.zeros(E, dtype=np.float32)
+    bias[63] = 5.0  # flips selection to expert 63 in row 3
+    for b in (None, bias):
+        w_ref, ids_ref = oracle.routing.grouped_sigmoid_topk(lg, b, G, 4, 8, True, 2.5)
+        tb = None if b is None else torch.from_numpy(b).to(dev)
+        w, ids = ops.route_grouped_sigmoid(torch.from_numpy(lg).to(dev), tb, G, 4, 8, True, 2.5)
+        np.testing.assert_array_equal(to_np(ids), ids_ref)
+        np.testing.assert_allclose(to_np(w), w_ref, rtol=1e-6, atol=1e-7)
+
+
+# ----------------------------------------------------------------- align / slots
+
+
+@pytest.mark.parametrize(
+    "numel,E,bs",
+    [(0, 8, 4), (12, 4, 4), (8, 256, 1), (64, 128, 16), (512, 256, 64), (2048, 256, 16), (1000, 1023, 8),
+     (65536, 256, 64), (73728, 257, 128)],
+)
+def test_align_exact(dev, numel, E, bs):
+    rng = np.random.default_rng(numel + E)
+    ids = rng.integers(-1, E + 2, size=numel).astype(np.int32)  # includes skips, the sentinel bucket, junk
+    s_ref, e_ref, n_ref = oracle.align.moe_align_block_size(ids, bs, E)
+    s, e, n = ops.align(torch.from_numpy(ids).to(dev), bs, E)
+    np.testing.assert_array_equal(to_np(n), n_ref)
+    np.testing.assert_array_equal(to_np(s), s_ref)
+    np.testing.assert_array_equal(to_np(e), e_ref)
+
+
+def test_align_docstring_kat(dev):
+    ids = torch.tensor([[2, 3, 4], [1, 2, 4], [1, 3, 4], [1, 2, 3]], dtype=torch.int32, device=dev)
+    s, e, n = ops.align(ids, 4, 4)
+    assert to_np(s)[:16].tolist() == [3, 6, 9, 12, 0, 4, 10, 12, 1, 7, 11, 12, 2, 5, 8, 12]
+    assert int(to_np(n)[0]) == 16
+    assert to_np(e)[:4].tolist() == [1, 2, 3, 4]
+
+
+def test_slot_map_exact(dev):
+    rng = np.random.default_rng(3)
+    E, S = 256, 64
+    table = np.full(E, -1, dtype=np.int32)
+    res = rng.choice(E, S, replace=False)
+    table[res] = rng.permutation(S)
+    ids = rng.integers(-2, E + 3, size=(64, 8)).astype(np.int32)
+    slots_ref, miss_ref, stats_ref = oracle.slots.slot_map(ids, table)
+    t_ids = torch.from_numpy(ids).to(dev)
+    miss = torch.empty(ids.shape, dtype=torch.uint8, device=dev)
+    stats = torch.zeros(4, dtype=torch.int64, device=dev)
+    out = ops.slot_map(t_ids, torch.from_numpy(table).to(dev), miss_mask=miss, stats=stats)
+    np.testing.assert_array_equal(to_np(out), slots_ref)
+    np.testing.assert_array_equal(to_np(miss), miss_ref)
+    np.testing.assert_array_equal(to_np(stats), stats_ref)
+    ops.slot_map(t_ids, torch.from_numpy(table).to(dev), out=t_ids, stats=stats)  # in place, accumulate
+    np.testing.assert_array_equal(to_np(t_ids), slots_ref)
+    np.testing.assert_array_equal(to_np(stats), 2 * stats_ref)
+
+
+# ----------------------------------------------------------------- decode experts
+
+# (name, routed fmt, rows, H, I, k, shared fmt or None, shared I)
+DECODE_CASES = [
+    ("c1_bf16", "bf16", 16, 1024, 512, 2, None, 0),
+    ("c2_fp8_reduced", "fp8", 24, 2048, 768, 8, None, 0),
+    ("c3_mxfp4_reduced", "mxfp4", 20, 1280, 384, 8, "bf16", 384),
+    ("c4_fp8_reduced", "fp8", 16, 1024, 256, 8, "fp8", 256),
+]
+
+
+def _decode_case(name, fmt, rows, H, I, k, sfmt, sI, M, seed=0):
+    rng = np.random.default_rng(seed + M)
+    bank = synth.make_bank(fmt, rows, H, I, rng)
+    shared = synth.make_bank(sfmt, 1, H, sI, rng) if sfmt else None
+    x = synth.activations(rng, M, H)
+    ids = np.stack([rng.choice(rows, k, replace=False) for _ in range(M)]).astype(np.int32)
+    w = rng.random((M, k), dtype=np.float32)
+    w = (w / w.sum(1, keepdims=True)).astype(np.float32)
+    return bank, shared, x, w, ids
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=[c[0] for c in DECODE_CASES])
+@pytest.mark.parametrize("M", [1, 4, 33, 64])
+def test_decode_parity(dev, case, M):
+    name, fmt, rows, H, I, k, sfmt, sI = case
+    bank, shared, x, w, ids = _decode_case(*case, M)
+    y_ref = oracle.experts.moe_layer("decode", x, w, ids, bank, shared)
+    y = ops.experts_decode(bf16_dev(x, dev), torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev),
+                           to_device_bank(bank, dev), to_device_bank(shared, dev) if shared else None)
+    got = to_np(y)
+    assert max_rel(got, y_ref) <= MAX_REL_TOL, (name, M, max_rel(got, y_ref))
+    assert cosine(got, y_ref) >= COS_TOL, (name, M, cosine(got, y_ref))
+
+
+def test_decode_skips_and_weight_on_input(dev):
+    bank, shared, x, w, ids = _decode_case(*DECODE_CASES[0], 8, seed=5)
+    ids[0, 1] = -1
+    ids[3, 0] = 99  # out of range: skipped
+    for on_input in (False, True):
+        y_ref = oracle.experts.moe_layer("decode", x, w, ids, bank, None, weight_on_input=on_input)
+        y = ops.experts_decode(bf16_dev(x, dev), torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev),
+                               to_device_bank(bank, dev), None, apply_router_weight_on_input=on_input)
+        got = to_np(y)
+        assert max_rel(got, y_ref) <= MAX_REL_TOL
+        assert cosine(got, y_ref) >= COS_TOL
+
+
+@pytest.mark.parametrize("batch_size", [1, 2, 4, 8, 16, 24])
+def test_decode_noncontiguous_slots_recipe(dev, batch_size):
+    """Recipe of the reference's tests/moe/test_fused_moe.py:61-98 (37 cache
+    slots, fixed non-contiguous slot ids, top-8), at a 128-multiple geometry."""
+    rng = np.random.default_rng(42 + batch_size)
+    bank = synth.make_bank("bf16", 37, 256, 128, rng, std=0.5)
+    x = bf16_round(0.5 * rng.standard_normal((batch_size, 256)).astype(np.float32))
+    w = rng.random((batch_size, 8), dtype=np.float32)
+    w = (w / w.sum(1, keepdims=True)).astype(np.float32)
+    ids = np.tile(np.array([31, 4, 18, 0, 29, 7, 35, 12], dtype=np.int32), (batch_size, 1))
+    y_ref = oracle.experts.moe_layer("decode", x, w, ids, bank)
+    y = ops.experts_decode(bf16_dev(x, dev), torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev),
+                           to_device_bank(bank, dev))
+    got = to_np(y)
+    assert max_rel(got, y_ref) <= MAX_REL_TOL
+    assert cosine(got, y_ref) >= COS_TOL
+
+
+def test_decode_deterministic(dev):
+    bank, shared, x, w, ids = _decode_case(*DECODE_CASES[3], 64, seed=9)
+    args = (bf16_dev(x, dev), torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev),
+            to_device_bank(bank, dev), to_device_bank(shared, dev))
+    a = ops.experts_decode(*args).clone()
+    b = ops.experts_decode(*args)
+    assert torch.equal(a, b)
+
+
+def test_decode_slot_cache_misses(dev):
+    """C4-style expert cache: routing over 64 experts, 16 resident slots; the
+    non-resident routes are reported and excluded."""
+    rng = np.random.default_rng(11)
+    E, S, H, I, M = 64, 16, 1024, 256, 16
+    full = synth.make_bank("fp8", E, H, I, rng)
+    shared = synth.make_bank("fp8", 1, H, I, rng)
+    resident = np.sort(rng.choice(E, S, replace=False))
+    table = np.full(E, -1, dtype=np.int32)
+    table[resident] = np.arange(S, dtype=np.int32)
+    lg = synth.normal(rng, (M, E))
+    bias = synth.normal(rng, (E,), 0.05)
+    w_ref, ids_ref = oracle.routing.grouped_sigmoid_topk(lg, bias, 8, 4, 8, True, 2.5)
+    slots_ref, miss_ref, stats_ref = oracle.slots.slot_map(ids_ref, table)
+    x = synth.activations(rng, M, H)
+    y_ref = oracle.experts.moe_layer("decode", x, w_ref, slots_ref, sub_bank(full, resident), shared)
+
+    w, ids = ops.route_grouped_sigmoid(torch.from_numpy(lg).to(dev), torch.from_numpy(bias).to(dev), 8, 4, 8,
+                                       True, 2.5)
+    stats = torch.zeros(4, dtype=torch.int64, device=dev)
+    slots = ops.slot_map(ids, torch.from_numpy(table).to(dev), stats=stats)
+    y = ops.experts_decode(bf16_dev(x, dev), w, slots, to_device_bank(full, dev, resident),
+                           to_device_bank(shared, dev))
+    np.testing.assert_array_equal(to_np(slots), slots_ref)
+    np.testing.assert_array_equal(to_np(stats), stats_ref)
+    got = to_np(y)
+    assert max_rel(got, y_ref) <= MAX_REL_TOL
+    assert cosine(got, y_ref) >= COS_TOL
