@@ -1,0 +1,440 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X fused MoE-layer hot path.
+
+Headline workload (one JSON line on stdout): the DeepSeek-V3-shaped FP8 MoE
+layer in decode -- hidden 7168, 256 routed experts with grouped sigmoid routing
+(8 groups, top-4 groups, top-8, bias, scale 2.5), intermediate 2048, one FP8
+shared expert, 64 experts resident in cache slots behind the slot table -- at
+batch 64.  One step = one layer call: router -> slot lookup -> experts ->
+combine, captured in a HIP graph and replayed; successive steps rotate through
+different synthetic routings so the touched experts change.  ``value`` is the
+algorithmic HBM traffic of the step (distinct resident experts x expert bytes
++ shared expert + activations + logits) divided by the measured time.
+
+Also reported in the same line: the roofline of the dominant kernel (the
+gate_up GEMV stage, timed with HIP events on the library's stream), a bounded
+sweep over the other configurations (decode batches 1..64 of the Qwen3-30B
+FP8, GLM MXFP4 and DeepSeek-V3 layers; 8K-token ragged prefill in FP8 and
+MXFP4 against the dense FP8 MFMA peak), and the CPU baseline: the C++
+restatement of the reference's CPU MoE executor on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+from freetoken_amd import _lib, ops  # noqa: E402
+
+METRIC = "MoE layer tok/s + HBM GB/s (decode b=1..64) and MFMA TFLOPS (8K prefill)"
+HBM_PEAK_GBS = 8000.0
+PEAK_TFLOPS = {"fp8": 5000.0, "mxfp4": 10100.0, "bf16": 2500.0}
+
+C2 = dict(name="c2_qwen3_30b_a3b_fp8", H=2048, I=768, E=128, k=8, router="softmax", fmt="fp8_block",
+          shared=None, Is=0, slots=128)
+C3 = dict(name="c3_glm_mxfp4", H=5120, I=1536, E=160, k=8, router="sigmoid", n_group=1, topk_group=1,
+          scale=2.5, fmt="mxfp4", shared="bf16", Is=1536, slots=160)
+C4 = dict(name="c4_deepseek_v3_fp8", H=7168, I=2048, E=256, k=8, router="sigmoid", n_group=8, topk_group=4,
+          scale=2.5, fmt="fp8_block", shared="fp8_block", Is=2048, slots=64)
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ----------------------------------------------------------------------------- synthetic weights
+
+
+def _e2m1_codes(v: torch.Tensor) -> torch.Tensor:
+    """Round |v| <= 6 to e2m1 codes, ties to even (same rule as the oracle)."""
+    m = v.abs()
+    code = torch.full_like(m, 7, dtype=torch.uint8)
+    for thr, c, le in ((5.0, 6, True), (3.5, 5, False), (2.5, 4, True), (1.75, 3, False), (1.25, 2, True),
+                       (0.75, 1, False), (0.25, 0, True)):
+        hit = (m <= thr) if le else (m < thr)
+        code = torch.where(hit, torch.full_like(code, c), code)
+    return code | (torch.signbit(v).to(torch.uint8) << 3)
+
+
+def make_bank(fmt: str, rows: int, H: int, I: int, gen: torch.Generator, dev, std: float = 0.02) -> ops.ExpertBank:
+    """Bank of ``rows`` SwiGLU experts drawn from N(0, std) and quantised on the GPU."""
+
+    def one(n, k):
+        outs = []
+        for e0 in range(0, rows, 4):
+            e1 = min(rows, e0 + 4)
+            w = torch.randn((e1 - e0, n, k), generator=gen, device=dev, dtype=torch.float32) * std
+            if fmt == "bf16":
+                outs.append((w.to(torch.bfloat16), None))
+            elif fmt == "fp8_block":
+                b = w.view(e1 - e0, n // 128, 128, k // 128, 128)
+                s = b.abs().amax(dim=(2, 4)).clamp_min(1e-12) / 448.0
+                q = (b / s[:, :, None, :, None]).clamp(-448, 448).to(torch.float8_e4m3fn).view(e1 - e0, n, k)
+                outs.append((q, s))
+            else:
+                b = w.view(e1 - e0, n, k // 32, 32)
+                amax = b.abs().amax(-1).clamp_min(1e-30)
+                e = torch.ceil(torch.log2(amax / 6.0)).clamp(-127, 127)
+                codes = _e2m1_codes(b / torch.exp2(e)[..., None]).view(e1 - e0, n, k)
+                packed = (codes[..., 0::2] | (codes[..., 1::2] << 4)).contiguous()
+                outs.append((packed, (e + 127).to(torch.uint8)))
+            del w
+        q = torch.cat([o[0] for o in outs])
+        s = torch.cat([o[1] for o in outs]) if outs[0][1] is not None else None
+        return q, s
+
+    gu, gus = one(2 * I, H)
+    dn, dns = one(H, I)
+    return ops.ExpertBank(fmt, gu, dn, gus, dns)
+
+
+def expert_bytes(fmt: str, H: int, I: int) -> int:
+    if fmt == "bf16":
+        return 3 * H * I * 2
+    if fmt == "fp8_block":
+        return 3 * H * I + 4 * ((2 * I // 128) * (H // 128) + (H // 128) * (I // 128))
+    return 3 * H * I // 2 + 3 * H * I // 32
+
+
+def gate_up_bytes(fmt: str, H: int, I: int) -> int:
+    if fmt == "bf16":
+        return 2 * H * I * 2
+    if fmt == "fp8_block":
+        return 2 * H * I + 4 * (2 * I // 128) * (H // 128)
+    return H * I + 2 * H * I // 32
+
+
+# ----------------------------------------------------------------------------- decode layer
+
+
+class DecodeLayer:
+    """One decode configuration on the GPU: router inputs, slot table, banks."""
+
+    def __init__(self, cfg: dict, dev, gen: torch.Generator):
+        self.cfg = cfg
+        self.dev = dev
+        H, I, E = cfg["H"], cfg["I"], cfg["E"]
+        self.bank = make_bank(cfg["fmt"], cfg["slots"], H, I, gen, dev)
+        self.shared = make_bank(cfg["shared"], 1, H, cfg["Is"], gen, dev) if cfg["shared"] else None
+        self.bias = (torch.randn((E,), generator=gen, device=dev) * 0.1) if cfg["router"] == "sigmoid" else None
+        # resident set: the `slots` most popular experts under the seeded router
+        # (popularity estimated on 4096 calibration tokens); all experts when slots == E
+        self.table = torch.full((E,), -1, dtype=torch.int32, device=dev)
+        if cfg["slots"] >= E:
+            self.table = torch.arange(E, dtype=torch.int32, device=dev)
+        else:
+            lg = torch.randn((4096, E), generator=gen, device=dev)
+            _, ids = self.route(lg)
+            freq = torch.bincount(ids.view(-1).long(), minlength=E)
+            top = torch.sort(torch.argsort(freq, descending=True, stable=True)[: cfg["slots"]]).values
+            self.table[top] = torch.arange(cfg["slots"], dtype=torch.int32, device=dev)
+        self.stats = torch.zeros(4, dtype=torch.int64, device=dev)
+
+    def route(self, logits):
+        c = self.cfg
+        if c["router"] == "softmax":
+            return ops.route_softmax_topk(logits, c["k"], True)
+        return ops.route_grouped_sigmoid(logits, self.bias, c["n_group"], c["topk_group"], c["k"], True, c["scale"])
+
+    def step(self, logits, x, out):
+        w, ids = self.route(logits)
+        ops.slot_map(ids, self.table, out=ids, stats=self.stats)
+        ops.experts_decode(x, w, ids, self.bank, shared=self.shared, out=out)
+        return ids
+
+    def step_bytes(self, ids: torch.Tensor, M: int) -> tuple[int, int, int]:
+        """(algorithmic bytes of the step, gate_up-stage bytes, distinct resident experts)."""
+        c = self.cfg
+        valid = ids[ids >= 0]
+        u = int(torch.unique(valid).numel())
+        eb = expert_bytes(c["fmt"], c["H"], c["I"])
+        sh = expert_bytes(c["shared"], c["H"], c["Is"]) if c["shared"] else 0
+        io = M * c["H"] * 2 * 2 + M * c["E"] * 4
+        gu = u * gate_up_bytes(c["fmt"], c["H"], c["I"])
+        gu += gate_up_bytes(c["shared"], c["H"], c["Is"]) if c["shared"] else 0
+        gu += M * c["H"] * 2 + (int(valid.numel()) + (M if c["shared"] else 0)) * max(c["I"], c["Is"]) * 2
+        return u * eb + sh + io, gu, u
+
+
+def run_decode(layer: DecodeLayer, M: int, steps: int, warmup: int, gen, graphs: int = 8, stage_timing=False):
+    """Times `steps` graph replays (rotating over `graphs` routings); returns a dict."""
+    c, dev = layer.cfg, layer.dev
+    G = max(1, min(graphs, steps))
+    logits = [torch.randn((M, c["E"]), generator=gen, device=dev) for _ in range(G)]
+    xs = [torch.randn((M, c["H"]), generator=gen, device=dev).to(torch.bfloat16) for _ in range(G)]
+    outs = [torch.empty((M, c["H"]), dtype=torch.bfloat16, device=dev) for _ in range(G)]
+    ids_eager = [layer.step(logits[g], xs[g], outs[g]) for g in range(G)]  # sizes the workspace
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=dev)
+    graphs_ = []
+    ids_graph = []
+    with torch.cuda.stream(stream):
+        for g in range(G):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=stream):
+                ids_graph.append(layer.step(logits[g], xs[g], outs[g]))
+            graphs_.append(gr)
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        graphs_[i % G].replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        graphs_[i % G].replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1)
+    total_bytes = 0
+    gu_bytes = 0
+    us = []
+    for i in range(steps):
+        b, gb, u = layer.step_bytes(ids_eager[i % G], M)
+        total_bytes += b
+        gu_bytes += gb
+        us.append(u)
+    res = dict(batch=M, steps=steps, ms_per_step=ms / steps, tok_s=M * steps / (ms / 1e3),
+               gbs=total_bytes / (ms / 1e3) / 1e9, bytes_per_step=total_bytes / steps,
+               resident_experts_per_step=statistics.mean(us))
+    res["hbm_frac"] = res["gbs"] / HBM_PEAK_GBS
+    if stage_timing:
+        # instrumented eager pass over the same inputs: per-kernel durations
+        L = _lib.lib()
+        L.ftmoe_stage_timing_begin()
+        for i in range(steps):
+            layer.step(logits[i % G], xs[i % G], outs[i % G])
+        torch.cuda.synchronize()
+        import ctypes
+
+        arr = (ctypes.c_double * 8)()
+        ns, nc = ctypes.c_int(), ctypes.c_int()
+        _lib.check(L.ftmoe_stage_timing_end(arr, 8, ctypes.byref(ns), ctypes.byref(nc)), "stage timing")
+        names = ["align", "gate_up", "down", "combine"]
+        res["stage_us"] = {names[j]: arr[j] / max(1, nc.value) * 1e3 for j in range(min(ns.value, 4))}
+        res["gate_up_bytes_per_launch"] = gu_bytes / steps
+    del graphs_
+    return res
+
+
+# ----------------------------------------------------------------------------- prefill
+
+
+def run_prefill(fmt: str, steps: int, warmup: int, gen, dev, M: int = 8192):
+    c = C4
+    H, I, E, k = c["H"], c["I"], c["E"], c["k"]
+    bank = make_bank(fmt, E, H, I, gen, dev)
+    shared = make_bank(fmt, 1, H, I, gen, dev)
+    # 16 ragged sequences, lengths U[64, 1024] normalised to M (largest remainder);
+    # the MoE layer sees the packed [M, H] rows, so lengths only document the batch
+    g = torch.Generator().manual_seed(5)
+    raw = torch.randint(64, 1025, (16,), generator=g).double()
+    exact = raw / raw.sum() * M
+    lens = exact.floor().long()
+    rem = M - int(lens.sum())
+    lens[torch.argsort(exact - lens, descending=True)[:rem]] += 1
+    ranks = torch.randperm(E, generator=gen, device=dev).double() + 1
+    p = ranks ** -1.1
+    zipf = torch.log(p / p.sum()).float()
+    bias = torch.randn((E,), generator=gen, device=dev) * 0.1
+    logits = torch.randn((M, E), generator=gen, device=dev) + zipf[None, :]
+    x = torch.randn((M, H), generator=gen, device=dev).to(torch.bfloat16)
+    w, ids = ops.route_grouped_sigmoid(logits, bias, 8, 4, k, True, 2.5)
+    out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+    for _ in range(max(1, warmup)):
+        ops.experts_prefill(x, w, ids, bank, shared=shared, out=out)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        ops.experts_prefill(x, w, ids, bank, shared=shared, out=out)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    routes = int((ids >= 0).sum())
+    flops = (routes + M) * 6 * H * I
+    counts = torch.bincount(ids.view(-1).long(), minlength=E)
+    peak = PEAK_TFLOPS["fp8"]
+    res = dict(tokens=M, sequences=lens.tolist(), ms=ms, tflops=flops / (ms / 1e3) / 1e12, flops=flops,
+               max_expert_tokens=int(counts.max()), min_expert_tokens=int(counts.min()))
+    res["frac_of_fp8_peak"] = res["tflops"] / peak
+    if fmt == "mxfp4":
+        res["frac_of_fp4_peak"] = res["tflops"] / PEAK_TFLOPS["mxfp4"]
+    del bank, shared
+    torch.cuda.empty_cache()
+    return res
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+
+
+def cpu_baseline(layer: DecodeLayer, M: int, budget_s: float, gen, dev):
+    """C++ restatement of the reference CPU executor on this host: the same C4
+    routing (resident slots), bf16-dequantised banks (the reference's CPU route
+    for FP8 checkpoints), routed experts only (the reference's CPU executor does
+    not run the shared expert)."""
+    import numpy as np
+
+    from oracle.cpu_moe import CpuMoe, lib as cpulib, physical_cores
+
+    c = layer.cfg
+    H, I, S, k = c["H"], c["I"], c["slots"], c["k"]
+    cores = physical_cores()[:16]
+    gu = np.empty((S, 2 * I, H), dtype=np.uint16)
+    dn = np.empty((S, H, I), dtype=np.uint16)
+    cpulib().cpumoe_fill_bf16(gu.ctypes.data, gu.size, 0.02 * math.sqrt(3), 1, len(cores))
+    cpulib().cpumoe_fill_bf16(dn.ctypes.data, dn.size, 0.02 * math.sqrt(3), 2, len(cores))
+    cpu = CpuMoe(H, I, k, S, "bf16", cpus=cores)
+    cpu.set_bank(gu, dn)
+    steps = []
+    routings = []
+    for _ in range(4):
+        lg = torch.randn((M, c["E"]), generator=gen, device=dev)
+        w, ids = layer.route(lg)
+        ops.slot_map(ids, layer.table, out=ids)
+        routings.append((w.cpu().numpy(), ids.cpu().numpy()))
+    x = (np.random.default_rng(0).standard_normal((M, H)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    cpu.run(x, *routings[0])  # warm-up
+    t_end = time.perf_counter() + budget_s
+    i = 0
+    us = []
+    while time.perf_counter() < t_end and i < 64:
+        w, ids = routings[i % len(routings)]
+        t0 = time.perf_counter()
+        cpu.run(x, w, ids)
+        steps.append(time.perf_counter() - t0)
+        us.append(len(np.unique(ids[ids >= 0])))
+        i += 1
+    isa = cpu.isa
+    cpu.close()
+    t = statistics.median(steps)
+    eb = expert_bytes("bf16", H, I)
+    gbs = statistics.mean(us) * eb / t / 1e9
+    try:
+        model = [ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo") if ln.startswith("model name")][0]
+    except (OSError, IndexError):
+        model = "unknown"
+    return {
+        "value": gbs,
+        "unit": "GB/s",
+        "cores": len(cores),
+        "kind": "port",
+        "sample": (f"C4 decode batch {M}, {len(steps)} timed steps (median {t * 1e3:.1f} ms/step, "
+                   f"{M / t:.1f} tok/s), routed experts only over the {S} resident slots as bf16 banks, "
+                   f"two-pass GEMV restatement, ISA {isa}, {len(cores)} pinned threads on physical cores, "
+                   f"CPU {model}"),
+    }
+
+
+# ----------------------------------------------------------------------------- main
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="run one device copy of this many MiB first (counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (the MoE-layer hot path is measured on one MI355X); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev).manual_seed(1234)
+
+    if args.calib_copy_mib:
+        a = torch.empty((args.calib_copy_mib << 20,), dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+
+    log("[bench] building C4 layer (64 resident FP8 experts + shared)")
+    c4 = DecodeLayer(C4, dev, gen)
+    log(f"[bench] C4 decode batch {args.batch}: {args.steps} steps")
+    head = run_decode(c4, args.batch, args.steps, args.warmup, gen, stage_timing=True)
+    gu_us = head["stage_us"]["gate_up"]
+    gu_gbs = head["gate_up_bytes_per_launch"] / (gu_us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "decode_stage_kernel<FP8,FP8,0> (gate_up + SwiGLU)",
+                "avg_launch_us": round(gu_us, 2),
+                "algorithmic_bytes_per_launch": int(head["gate_up_bytes_per_launch"])}
+
+    sweep = {}
+    if not args.no_sweep:
+        for M in (1, 8, 32):
+            log(f"[bench] sweep C4 decode batch {M}")
+            sweep[f"{C4['name']}_b{M}"] = run_decode(c4, M, 20, 3, gen)
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] CPU baseline")
+        cpu = cpu_baseline(c4, args.batch, args.cpu_seconds, gen, dev)
+    del c4
+    torch.cuda.empty_cache()
+    if not args.no_sweep:
+        for cfg in (C2, C3):
+            log(f"[bench] sweep {cfg['name']}")
+            layer = DecodeLayer(cfg, dev, gen)
+            for M in (1, 8, 32, 64):
+                sweep[f"{cfg['name']}_b{M}"] = run_decode(layer, M, 20, 3, gen)
+            del layer
+            torch.cuda.empty_cache()
+        for fmt in ("fp8_block", "mxfp4"):
+            log(f"[bench] sweep C5 prefill {fmt}")
+            sweep[f"c5_prefill_8192_{fmt}"] = run_prefill(fmt, 5, 1, gen, dev)
+
+    def rnd(d):
+        return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}
+
+    line = {
+        "metric": METRIC,
+        "value": round(head["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8-e4m3 weights x bf16 activations (W8A16, bf16 MFMA, fp32 accumulate)",
+        "data": "synthetic (seeded N(0,0.02) weights quantised to 128x128-block FP8, N(0,1) activations/logits)",
+        "config": {"workload": f"C4 DeepSeek-V3-shaped FP8 MoE layer decode, batch {args.batch}",
+                   "hidden": 7168, "experts": 256, "resident_slots": 64, "top_k": 8,
+                   "router": "grouped sigmoid 8 groups / top-4 groups, bias, scale 2.5",
+                   "intermediate": 2048, "shared_expert": "1 x FP8 (I=2048)",
+                   "tok_s": round(head["tok_s"], 1), "hbm_frac": round(head["hbm_frac"], 4),
+                   "resident_experts_per_step": round(head["resident_experts_per_step"], 2),
+                   "stage_us": {k: round(v, 2) for k, v in head["stage_us"].items()},
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "sweep": {k: rnd(v) for k, v in sweep.items()},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -114,6 +114,7 @@ __global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
     const int e = tid * per + q;
     if (e < eff) {
       cum[e] = pre;
+      if (a.cum_out) a.cum_out[e] = pre;
       const int c = cnt[e];
       if (a.seg_expert && e < a.num_experts && c > 0) {
         a.seg_expert[pre_seg] = e;
@@ -126,6 +127,7 @@ __global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
   }
   if (tid == 0) {
     cum[eff] = total;
+    if (a.cum_out) a.cum_out[eff] = total;
     a.ntpp[0] = total;
     if (a.n_seg) a.n_seg[0] = total_seg;
   }

@@ -5,6 +5,7 @@
 #include <cstdio>
 #include <algorithm>
 #include <string>
+#include <vector>
 
 #include "../../include/ftmoe.h"
 
@@ -94,6 +95,87 @@ DecodeLayout decode_layout(void* ws, int M, int k, const ftmoe_bank* bank, const
   return L;
 }
 
+
+// ---- stage timing (instrumentation) ----------------------------------------
+struct StageTimer {
+  bool on = false;
+  std::vector<std::vector<hipEvent_t>> calls;  // events of each recorded call
+  std::vector<hipEvent_t> cur;
+  hipStream_t stream = nullptr;
+
+  void start_call(hipStream_t s) {
+    if (!on) return;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return;
+    stream = s;
+    cur.clear();
+    mark();
+  }
+  void mark() {
+    if (!on || !stream) return;
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return;
+    if (hipEventRecord(e, stream) != hipSuccess) {
+      (void)hipEventDestroy(e);
+      return;
+    }
+    cur.push_back(e);
+  }
+  void end_call() {
+    if (!on || !stream) return;
+    calls.push_back(cur);
+    cur.clear();
+    stream = nullptr;
+  }
+};
+StageTimer g_timer;
+
+struct PrefillLayout {
+  int32_t* sorted;
+  int32_t* expert_ids;
+  int32_t* ntpp;
+  int32_t* cum;
+  uint8_t* xq;
+  void* xs;
+  uint16_t* act;
+  uint8_t* actq;
+  void* as;
+  uint16_t* ic3;
+  uint16_t* sh_out;
+  int max_padded, max_blocks;
+  size_t bytes;
+};
+
+constexpr int kPrefillBM = 128;
+
+PrefillLayout prefill_layout(void* ws, int M, int k, const ftmoe_bank* bank, const ftmoe_bank* shared) {
+  PrefillLayout L{};
+  Carver c{static_cast<uint8_t*>(ws)};
+  const int numel = M * k;
+  const int H = bank->hidden, I = bank->inter;
+  ftmoe_align_sizes(numel, bank->num_rows, kPrefillBM, &L.max_padded, &L.max_blocks);
+  L.sorted = c.take<int32_t>(L.max_padded);
+  L.expert_ids = c.take<int32_t>(L.max_blocks);
+  L.ntpp = c.take<int32_t>(1);
+  L.cum = c.take<int32_t>(bank->num_rows + 2);
+  const bool quant = bank->format != FTMOE_FMT_BF16;
+  const size_t sc = bank->format == FTMOE_FMT_FP8_B128 ? sizeof(float) : 1;
+  const size_t rows = static_cast<size_t>(numel) + (shared ? M : 0);
+  if (quant) {
+    L.xq = c.take<uint8_t>(static_cast<size_t>(M) * H);
+    L.xs = c.take<uint8_t>(static_cast<size_t>(M) * (H / 128) * sc);
+  }
+  L.act = c.take<uint16_t>(rows * I);
+  if (quant) {
+    L.actq = c.take<uint8_t>(rows * I);
+    L.as = c.take<uint8_t>(rows * (I / 128) * sc);
+  }
+  L.ic3 = c.take<uint16_t>(static_cast<size_t>(numel) * H);
+  L.sh_out = shared ? c.take<uint16_t>(static_cast<size_t>(M) * H) : nullptr;
+  L.bytes = c.off;
+  return L;
+}
+
 }  // namespace
 
 extern "C" {
@@ -169,6 +251,16 @@ int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_i
                    "slot_map launch");
 }
 
+int ftmoe_act_quant_fp8(const void* x, int rows, int K, int mode, void* q, void* scales, ftmoe_stream_t stream) {
+  if ((!x || !q || !scales) && rows) return fail(FTMOE_ERR_INVALID, "act_quant_fp8: NULL pointer");
+  if (rows < 0 || K <= 0 || K % 128 || (mode != 0 && mode != 1))
+    return fail(FTMOE_ERR_UNSUPPORTED, "act_quant_fp8: rows=%d K=%d mode=%d", rows, K, mode);
+  if (rows == 0) return FTMOE_OK;
+  return check_hip(ftmoe::launch_act_quant(mode, static_cast<const uint16_t*>(x), rows, K, static_cast<uint8_t*>(q),
+                                           scales, stream),
+                   "act_quant_fp8 launch");
+}
+
 size_t ftmoe_experts_decode_workspace(int M, int top_k, const ftmoe_bank* bank, const ftmoe_bank* shared) {
   if (!bank || M <= 0 || top_k <= 0) return 0;
   return decode_layout(nullptr, M, top_k, bank, shared).bytes;
@@ -209,8 +301,10 @@ int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, c
   al.seg_start = L.seg_start;
   al.seg_count = L.seg_count;
   al.n_seg = L.n_seg;
+  g_timer.start_call(stream);
   rc = check_hip(ftmoe::launch_align(al, stream), "experts_decode align");
   if (rc) return rc;
+  g_timer.mark();
 
   ftmoe::DecodeArgs d{};
   d.x = static_cast<const uint16_t*>(x);
@@ -238,12 +332,158 @@ int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, c
   d.sh_out = L.sh_out;
   d.act_kind = activation;
   d.weight_on_input = apply_router_weight_on_input;
-  rc = check_hip(ftmoe::launch_decode_stages(bank->format, shared ? shared->format : FTMOE_FMT_NONE, d, stream),
-                 "experts_decode stages");
+  rc = check_hip(ftmoe::launch_decode_stage(0, bank->format, shared ? shared->format : FTMOE_FMT_NONE, d, stream),
+                 "experts_decode gate_up");
   if (rc) return rc;
-  return check_hip(ftmoe::launch_combine(L.ic3, topk_ids, bank->num_rows, L.sh_out, M, top_k, bank->hidden,
-                                         static_cast<uint16_t*>(y), stream),
-                   "experts_decode combine");
+  g_timer.mark();
+  rc = check_hip(ftmoe::launch_decode_stage(1, bank->format, shared ? shared->format : FTMOE_FMT_NONE, d, stream),
+                 "experts_decode down");
+  if (rc) return rc;
+  g_timer.mark();
+  rc = check_hip(ftmoe::launch_combine(L.ic3, topk_ids, bank->num_rows, L.sh_out, M, top_k, bank->hidden,
+                                       static_cast<uint16_t*>(y), stream),
+                 "experts_decode combine");
+  g_timer.mark();
+  g_timer.end_call();
+  return rc;
+}
+
+size_t ftmoe_experts_prefill_workspace(int M, int top_k, const ftmoe_bank* bank, const ftmoe_bank* shared) {
+  if (!bank || M <= 0 || top_k <= 0) return 0;
+  return prefill_layout(nullptr, M, top_k, bank, shared).bytes;
+}
+
+int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
+                          const ftmoe_bank* bank, const ftmoe_bank* shared, int activation, void* y,
+                          void* workspace, size_t workspace_bytes, ftmoe_stream_t stream) {
+  int rc = check_bank(bank, "routed", false);
+  if (rc) return rc;
+  if (shared) {
+    rc = check_bank(shared, "shared", true);
+    if (rc) return rc;
+    if (shared->hidden != bank->hidden || shared->inter != bank->inter || shared->format != bank->format)
+      return fail(FTMOE_ERR_UNSUPPORTED, "experts_prefill: the shared expert must match the routed format and shape");
+  }
+  if (!x || !topk_w || !topk_ids || !y) return fail(FTMOE_ERR_INVALID, "experts_prefill: NULL pointer");
+  if (M <= 0 || top_k <= 0) return fail(FTMOE_ERR_INVALID, "experts_prefill: M=%d top_k=%d", M, top_k);
+  if (bank->num_rows > 1023) return fail(FTMOE_ERR_UNSUPPORTED, "experts_prefill: num_rows %d > 1023", bank->num_rows);
+  if (activation < FTMOE_ACT_SILU || activation > FTMOE_ACT_GELU_TANH)
+    return fail(FTMOE_ERR_UNSUPPORTED, "experts_prefill: activation %d", activation);
+  const PrefillLayout need = prefill_layout(nullptr, M, top_k, bank, shared);
+  if (!workspace || workspace_bytes < need.bytes)
+    return fail(FTMOE_ERR_WORKSPACE, "experts_prefill: workspace %zu < %zu bytes", workspace_bytes, need.bytes);
+  const PrefillLayout L = prefill_layout(workspace, M, top_k, bank, shared);
+  const int numel = M * top_k;
+  const int H = bank->hidden, I = bank->inter;
+  const int fmt = bank->format;
+
+  ftmoe::AlignArgs al{};
+  al.ids = topk_ids;
+  al.numel = numel;
+  al.num_experts = bank->num_rows;
+  al.block_size = kPrefillBM;
+  al.sorted_ids = L.sorted;
+  al.max_padded = L.max_padded;
+  al.expert_ids = L.expert_ids;
+  al.max_blocks = L.max_blocks;
+  al.ntpp = L.ntpp;
+  al.cum_out = L.cum;
+  g_timer.start_call(stream);
+  rc = check_hip(ftmoe::launch_align(al, stream), "experts_prefill align");
+  if (rc) return rc;
+  g_timer.mark();
+
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  const int qmode = fmt == FTMOE_FMT_MXFP4 ? 1 : 0;
+  if (fmt != FTMOE_FMT_BF16) {
+    rc = check_hip(ftmoe::launch_act_quant(qmode, xb, M, H, L.xq, L.xs, stream), "experts_prefill x quant");
+    if (rc) return rc;
+  }
+  g_timer.mark();
+  ftmoe::PrefillGemmArgs g{};
+  g.sorted = L.sorted;
+  g.cum = L.cum;
+  g.ntpp = L.ntpp;
+  g.num_experts = bank->num_rows;
+  g.numel = numel;
+  g.M = M;
+  g.k = top_k;
+  g.max_blocks = L.max_blocks;
+  g.shared_blocks = shared ? (M + kPrefillBM - 1) / kPrefillBM : 0;
+  g.w = {nullptr, nullptr};
+  g.act_kind = activation;
+  g.topk_w = topk_w;
+
+  // gate_up + SwiGLU -> act
+  g.xq = fmt == FTMOE_FMT_BF16 ? reinterpret_cast<const uint8_t*>(xb) : L.xq;
+  g.xs = L.xs;
+  g.x_token_rows = 1;
+  g.ntiles = I / 64;
+  g.K = H;
+  g.N = 2 * I;
+  g.inter = I;
+  g.w = {static_cast<const uint8_t*>(bank->gate_up), bank->gate_up_scale};
+  if (shared) g.ws = {static_cast<const uint8_t*>(shared->gate_up), shared->gate_up_scale};
+  g.out = L.act;
+  rc = check_hip(ftmoe::launch_prefill_gemm(fmt, 1, g, stream), "experts_prefill gate_up");
+  if (rc) return rc;
+  g_timer.mark();
+
+  // down (x router weight) -> ic3 / shared out
+  const size_t rows = static_cast<size_t>(numel) + (shared ? M : 0);
+  if (fmt != FTMOE_FMT_BF16) {
+    rc = check_hip(ftmoe::launch_act_quant(qmode, L.act, static_cast<int>(rows), I, L.actq, L.as, stream),
+                   "experts_prefill act quant");
+    if (rc) return rc;
+  }
+  g_timer.mark();
+  g.xq = fmt == FTMOE_FMT_BF16 ? reinterpret_cast<const uint8_t*>(L.act) : L.actq;
+  g.xs = L.as;
+  g.x_token_rows = 0;
+  g.ntiles = H / 128;
+  g.K = I;
+  g.N = H;
+  g.w = {static_cast<const uint8_t*>(bank->down), bank->down_scale};
+  if (shared) g.ws = {static_cast<const uint8_t*>(shared->down), shared->down_scale};
+  g.out = L.ic3;
+  g.sh_out = L.sh_out;
+  rc = check_hip(ftmoe::launch_prefill_gemm(fmt, 0, g, stream), "experts_prefill down");
+  if (rc) return rc;
+  g_timer.mark();
+  rc = check_hip(ftmoe::launch_combine(L.ic3, topk_ids, bank->num_rows, L.sh_out, M, top_k, H,
+                                       static_cast<uint16_t*>(y), stream),
+                 "experts_prefill combine");
+  g_timer.mark();
+  g_timer.end_call();
+  return rc;
+}
+
+int ftmoe_stage_timing_begin(void) {
+  g_timer.on = true;
+  g_timer.calls.clear();
+  return FTMOE_OK;
+}
+
+int ftmoe_stage_timing_end(double* stage_ms, int max_stages, int* n_stages, int* n_calls) {
+  g_timer.on = false;
+  int ns = 0;
+  for (auto& c : g_timer.calls) ns = std::max(ns, static_cast<int>(c.size()) - 1);
+  for (int i = 0; i < max_stages && stage_ms; ++i) stage_ms[i] = 0.0;
+  int rc = FTMOE_OK;
+  for (auto& c : g_timer.calls) {
+    if (c.empty()) continue;
+    if (hipEventSynchronize(c.back()) != hipSuccess) rc = fail(FTMOE_ERR_HIP, "stage timing: event sync failed");
+    for (size_t i = 1; i < c.size(); ++i) {
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, c[i - 1], c[i]) == hipSuccess && stage_ms && static_cast<int>(i - 1) < max_stages)
+        stage_ms[i - 1] += ms;
+    }
+    for (hipEvent_t e : c) (void)hipEventDestroy(e);
+  }
+  if (n_stages) *n_stages = ns;
+  if (n_calls) *n_calls = static_cast<int>(g_timer.calls.size());
+  g_timer.calls.clear();
+  return rc;
 }
 
 }  // extern "C"

@@ -340,21 +340,21 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
 }
 
 template <int FR, int FS>
-static hipError_t launch_stages(const DecodeArgs& a, bool has_shared, hipStream_t stream) {
+static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared, hipStream_t stream) {
   const int gy = a.max_seg + (has_shared ? 1 : 0);
   const int imax = has_shared ? max(a.I, a.Is) : a.I;
-  hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 0>), dim3(imax / 16, gy), dim3(kDecWaves * kWave), 0, stream, a);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 1>), dim3(a.H / 16, gy), dim3(kDecWaves * kWave), 0, stream, a);
+  if (stage == 0)
+    hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 0>), dim3(imax / 16, gy), dim3(kDecWaves * kWave), 0, stream, a);
+  else
+    hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 1>), dim3(a.H / 16, gy), dim3(kDecWaves * kWave), 0, stream, a);
   return hipGetLastError();
 }
 
-hipError_t launch_decode_stages(int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream) {
+hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream) {
   const bool sh = fmt_s != FMT_NONE;
   const int fs = sh ? fmt_s : fmt_r;  // FMT_S is unused without a shared expert
 #define FTMOE_CASE(R, S) \
-  if (fmt_r == R && fs == S) return launch_stages<R, S>(a, sh, stream);
+  if (fmt_r == R && fs == S) return launch_stage_t<R, S>(stage, a, sh, stream);
   FTMOE_CASE(FMT_BF16, FMT_BF16)
   FTMOE_CASE(FMT_BF16, FMT_FP8)
   FTMOE_CASE(FMT_BF16, FMT_MXFP4)

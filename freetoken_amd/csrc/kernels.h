@@ -26,6 +26,7 @@ struct AlignArgs {
   int32_t* seg_start;
   int32_t* seg_count;
   int32_t* n_seg;              // [1]
+  int32_t* cum_out;            // nullable: [num_experts + 2] padded region starts
 };
 
 struct BankView {
@@ -61,7 +62,37 @@ hipError_t launch_grouped_sigmoid(const float* logits, const float* bias, int M,
 hipError_t launch_align(const AlignArgs& a, hipStream_t stream);
 hipError_t launch_slot_map(const int32_t* ids, int numel, const int32_t* slot_for_id, int table_size,
                            int32_t* slot_ids, uint8_t* miss_mask, long long* stats, hipStream_t stream);
-hipError_t launch_decode_stages(int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream);
+struct PrefillGemmArgs {
+  // rows of the activation operand
+  const uint8_t* xq;        // fp8 [rows, K] (FP8 / MXFP4) or bf16 [rows, K] (BF16)
+  const void* xs;           // float [rows, K/128] (FP8) or uint8 e8m0 [rows, K/128] (MXFP4)
+  int x_token_rows;         // 1: gate_up (row = token = route / k, shared row = token)
+                            // 0: down    (row = route, shared row = M*k + token)
+  const int32_t* sorted;    // [max_padded] route indices per BM block, sentinel numel
+  const int32_t* cum;       // [E + 2] region starts of every expert (incl. the sentinel bucket)
+  const int32_t* ntpp;      // [1]
+  int num_experts;          // bank rows taking part
+  int numel;                // M * k
+  int M, k;
+  int max_blocks;           // routed M blocks of the grid
+  int shared_blocks;        // ceil(M / BM) if a shared expert is present, else 0
+  int ntiles;               // N tiles
+  int K;                    // reduction length
+  int N;                    // weight rows of one expert (2I or H)
+  int inter;                // I (gate/up split) for MODE gate_up
+  BankView w;               // routed weights
+  BankView ws;              // shared weights
+  // outputs
+  uint16_t* out;            // gate_up: act [numel + M, inter]; down: ic3 [numel, N]
+  uint16_t* sh_out;         // down: shared out [M, N]
+  const float* topk_w;      // [numel] (down)
+  int act_kind;
+};
+
+hipError_t launch_act_quant(int mode, const uint16_t* x, int rows, int K, uint8_t* q, void* scales,
+                            hipStream_t stream);
+hipError_t launch_prefill_gemm(int fmt, int gate_up, const PrefillGemmArgs& a, hipStream_t stream);
 hipError_t launch_combine(const uint16_t* ic3, const int32_t* ids, int num_rows, const uint16_t* sh_out, int M,
                           int k, int H, uint16_t* y, hipStream_t stream);
 

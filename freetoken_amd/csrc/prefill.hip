@@ -1,0 +1,442 @@
+// Prefill (grouped GEMM) path: activation quantisation, the two grouped GEMMs
+// with fused epilogues, on CDNA4 matrix cores.
+//
+// Formats
+//   FMT_FP8   W8A8: activations e4m3 with one float32 scale per row per 128 K
+//             (s = amax/448, reference per_token_group_quant_fp8,
+//             kernel/triton/fp8_block_linear.py:38-82), weights e4m3 with float32
+//             128x128 block scales.  One v_mfma_f32_16x16x128_f8f6f4 covers exactly
+//             one 128-deep scale block, so each MFMA result is folded into the
+//             accumulator with the product of both scales (reference
+//             _prefill_fp8_moe_kernel: acc += dot(a, w) * a_s * w_s).
+//   FMT_MXFP4 activations e4m3 with a power-of-two scale per row per 128 K (the
+//             DSV4 act_quant round trip of routed_experts_fp4_prefill), weights e2m1
+//             with e8m0 per 32 K: v_mfma_scale_f32_16x16x128_f8f6f4 applies both
+//             scales in hardware and accumulates directly.
+//   FMT_BF16  bf16 activations and weights, v_mfma_f32_16x16x32_bf16.
+//
+// Tiling: a workgroup computes a 128 (weight rows) x 128 (routes) tile with 4 waves
+// (2 x 2), each 64 x 64 = 4 x 4 MFMA blocks.  Weights are the MFMA A operand, so a
+// lane's four accumulators are four consecutive output features of one route and
+// stores are 8-byte vectors.  K advances 128 per step; global->LDS copies of the
+// next step overlap the MFMAs of the current one (double-buffered LDS).
+//
+// Gate/up: the weight tile holds gate rows [n0, n0+64) and up rows [I+n0, I+n0+64);
+// wave column wn owns gate and up rows n0+32wn..+32, so SwiGLU pairs registers.
+//
+// Schedule: workgroups are ordered expert-major -- for each expert, each N tile,
+// all M blocks of that expert -- so the blocks sharing a weight tile run together
+// and read it from HBM about once; the expert's activation rows stay hot in the
+// memory-side cache across its N tiles.  Shared-expert blocks come last.
+#include "kernels.h"
+
+namespace ftmoe {
+
+constexpr int kPBM = 128;   // routes per tile
+constexpr int kPBN = 128;   // weight rows per tile
+constexpr int kPThreads = 256;
+
+// ----------------------------------------------------------------------------
+// Activation quantisation: one wave per row, 2 values per lane per 128-group.
+//   MODE 0: float scale s = max(amax, 1e-10) / 448, q = e4m3(clamp(x / s))
+//   MODE 1: e8m0 scale 2^ceil(log2(max(amax, 1e-4) * (1/448))), q = e4m3(x / 2^e)
+// ----------------------------------------------------------------------------
+template <int MODE>
+__global__ void __launch_bounds__(256) act_quant_kernel(const uint16_t* __restrict__ x, int rows, int K,
+                                                        uint8_t* __restrict__ q, void* __restrict__ scales) {
+  const int lane = lane_id();
+  const int row = blockIdx.x * 4 + threadIdx.x / kWave;
+  if (row >= rows) return;
+  const uint32_t* xr = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(row) * K);
+  uint16_t* qr = reinterpret_cast<uint16_t*>(q + static_cast<size_t>(row) * K);
+  const int ng = K / 128;
+  for (int gi = 0; gi < ng; ++gi) {
+    const uint32_t pair = xr[gi * 64 + lane];
+    const float a = bf16_to_f32(static_cast<uint16_t>(pair & 0xffffu));
+    const float b = bf16_to_f32(static_cast<uint16_t>(pair >> 16));
+    const float amax = wave_max_f32(fmaxf(fabsf(a), fabsf(b)));
+    float qa, qb;
+    if (MODE == 0) {
+      const float s = fmaxf(amax, 1e-10f) / 448.0f;
+      qa = fminf(fmaxf(__fdiv_rn(a, s), -448.0f), 448.0f);
+      qb = fminf(fmaxf(__fdiv_rn(b, s), -448.0f), 448.0f);
+      if (lane == 0) static_cast<float*>(scales)[static_cast<size_t>(row) * ng + gi] = s;
+    } else {
+      const float t = fmaxf(amax, 1e-4f) * 0x1.24924ap-9f;  // * (1/448) rounded to float
+      const uint32_t bits = __float_as_uint(t);
+      const int e = static_cast<int>((bits >> 23) & 0xff) - 127 + ((bits & 0x7fffff) ? 1 : 0);
+      const float inv = ldexpf(1.0f, -e);
+      qa = fminf(fmaxf(a * inv, -448.0f), 448.0f);
+      qb = fminf(fmaxf(b * inv, -448.0f), 448.0f);
+      if (lane == 0) static_cast<uint8_t*>(scales)[static_cast<size_t>(row) * ng + gi] = static_cast<uint8_t>(e + 127);
+    }
+    const uint32_t pk = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(qa, qb, 0, false));
+    qr[gi * 64 + lane] = static_cast<uint16_t>(pk & 0xffffu);
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Grouped GEMM
+// ----------------------------------------------------------------------------
+
+template <int FMT>
+struct TileCfg;
+template <>
+struct TileCfg<FMT_FP8> {
+  static constexpr int kWRow = 128;  // bytes of a weight row per K step
+  static constexpr int kXRow = 128;
+};
+template <>
+struct TileCfg<FMT_MXFP4> {
+  static constexpr int kWRow = 64;
+  static constexpr int kXRow = 128;
+};
+template <>
+struct TileCfg<FMT_BF16> {
+  static constexpr int kWRow = 256;
+  static constexpr int kXRow = 256;
+};
+
+template <int FMT>
+struct Lds {
+  static constexpr int kWStride = TileCfg<FMT>::kWRow + 16;
+  static constexpr int kXStride = TileCfg<FMT>::kXRow + 16;
+  static constexpr int kW = kPBN * kWStride;
+  static constexpr int kX = kPBM * kXStride;
+  static constexpr int kWS = FMT == FMT_MXFP4 ? kPBN * 4 : 0;  // e8m0 codes, 4 per row per step
+  static constexpr int kXS = kPBM * 4;                          // float or e8m0 (one per row)
+  static constexpr int kBuf = kW + kX + kWS + kXS;
+  static constexpr int kTotal = 2 * kBuf;
+};
+
+// Maps a workgroup to (expert or shared, M block, N tile); returns false when idle.
+__device__ __forceinline__ bool map_tile(const PrefillGemmArgs& a, int wg, bool& shared, int& expert, int& mblock,
+                                         int& ntile) {
+  // blocks of the real experts only; ids == num_experts (the sentinel bucket of
+  // the align contract) take no part in the GEMMs
+  const int routed_wgs = (a.cum[a.num_experts] / kPBM) * a.ntiles;
+  if (wg < routed_wgs) {
+    // expert owning this workgroup: largest e with cum[e]/BM * ntiles <= wg
+    int lo = 0, hi = a.num_experts;  // cum[num_experts] region (sentinel bucket) never has work here
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if ((a.cum[mid] / kPBM) * a.ntiles <= wg) lo = mid; else hi = mid;
+    }
+    const int b0 = a.cum[lo] / kPBM;
+    const int nb = a.cum[lo + 1] / kPBM - b0;
+    const int local = wg - b0 * a.ntiles;
+    shared = false;
+    expert = lo;
+    ntile = local / nb;
+    mblock = b0 + local % nb;
+    return true;
+  }
+  const int sh0 = a.max_blocks * a.ntiles;
+  if (a.shared_blocks > 0 && wg >= sh0 && wg < sh0 + a.shared_blocks * a.ntiles) {
+    const int local = wg - sh0;
+    shared = true;
+    expert = 0;
+    ntile = local / a.shared_blocks;
+    mblock = local % a.shared_blocks;
+    return true;
+  }
+  return false;
+}
+
+template <int FMT, int GATE_UP>
+__global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillGemmArgs a) {
+  using L = Lds<FMT>;
+  using C = TileCfg<FMT>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ int s_row[kPBM];   // activation row of each tile column (-1: padding)
+  __shared__ int s_route[kPBM]; // route (routed) or token (shared) of each column, -1: padding
+
+  bool shared;
+  int expert, mblock, ntile;
+  if (!map_tile(a, blockIdx.x, shared, expert, mblock, ntile)) return;
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  const int wn = wave >> 1, wm = wave & 1;
+  const int r16 = lane & 15, g = lane >> 4;
+
+  if (tid < kPBM) {
+    int row = -1, route = -1;
+    if (shared) {
+      const int t = mblock * kPBM + tid;
+      if (t < a.M) {
+        route = t;
+        row = a.x_token_rows ? t : a.numel + t;
+      }
+    } else {
+      const int rr = a.sorted[mblock * kPBM + tid];
+      if (rr < a.numel) {
+        route = rr;
+        row = a.x_token_rows ? rr / a.k : rr;
+      }
+    }
+    s_row[tid] = row;
+    s_route[tid] = route;
+  }
+  __syncthreads();
+
+  const BankView bank = shared ? a.ws : a.w;
+  const int n0 = GATE_UP ? ntile * (kPBN / 2) : ntile * kPBN;
+  const size_t wrow_bytes = FMT == FMT_BF16 ? static_cast<size_t>(a.K) * 2
+                            : FMT == FMT_FP8 ? static_cast<size_t>(a.K) : static_cast<size_t>(a.K) / 2;
+  const uint8_t* wexp = bank.w + static_cast<size_t>(expert) * a.N * wrow_bytes;
+  const size_t xrow_bytes = FMT == FMT_BF16 ? static_cast<size_t>(a.K) * 2 : static_cast<size_t>(a.K);
+  const int nkb = a.K / 128;
+
+  auto wrow_of = [&](int r) -> int {  // weight row held in tile row r
+    if (GATE_UP) return r < kPBN / 2 ? n0 + r : a.inter + n0 + (r - kPBN / 2);
+    return n0 + r;
+  };
+
+  // ---- global -> register staging of one K step
+  constexpr int kWChunks = kPBN * C::kWRow / 16;
+  constexpr int kXChunks = kPBM * C::kXRow / 16;
+  constexpr int kWPer = kWChunks / kPThreads;
+  constexpr int kXPer = kXChunks / kPThreads;
+  u32x4 wreg[kWPer], xreg[kXPer];
+  uint32_t wsreg = 0;   // MXFP4: 4 e8m0 codes of one weight row (threads < BN)
+  uint32_t xsreg = 0;   // scale of one activation row (threads < BM), float bits or code
+
+  auto load_step = [&](int kb) {
+#pragma unroll
+    for (int q = 0; q < kWPer; ++q) {
+      const int c = tid + q * kPThreads;
+      const int r = c / (C::kWRow / 16), col = c % (C::kWRow / 16);
+      const uint8_t* p = wexp + static_cast<size_t>(wrow_of(r)) * wrow_bytes + static_cast<size_t>(kb) * C::kWRow + col * 16;
+      wreg[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    }
+#pragma unroll
+    for (int q = 0; q < kXPer; ++q) {
+      const int c = tid + q * kPThreads;
+      const int r = c / (C::kXRow / 16), col = c % (C::kXRow / 16);
+      const int row = s_row[r];
+      const int src = row < 0 ? 0 : row;
+      const uint8_t* p = a.xq + static_cast<size_t>(src) * xrow_bytes + static_cast<size_t>(kb) * C::kXRow + col * 16;
+      xreg[q] = *reinterpret_cast<const u32x4*>(p);
+    }
+    if constexpr (FMT == FMT_MXFP4) {
+      if (tid < kPBN) {
+        const uint8_t* sp = static_cast<const uint8_t*>(bank.s) +
+                            (static_cast<size_t>(expert) * a.N + wrow_of(tid)) * (a.K / 32) + kb * 4;
+        wsreg = *reinterpret_cast<const uint32_t*>(sp);
+      }
+    }
+    if constexpr (FMT != FMT_BF16) {
+      if (tid < kPBM) {
+        const int row = s_row[tid];
+        const int src = row < 0 ? 0 : row;
+        if (FMT == FMT_FP8)
+          xsreg = __float_as_uint(static_cast<const float*>(a.xs)[static_cast<size_t>(src) * nkb + kb]);
+        else
+          xsreg = static_cast<const uint8_t*>(a.xs)[static_cast<size_t>(src) * nkb + kb];
+      }
+    }
+  };
+  auto store_step = [&](int buf) {
+    uint8_t* base = lds + buf * L::kBuf;
+#pragma unroll
+    for (int q = 0; q < kWPer; ++q) {
+      const int c = tid + q * kPThreads;
+      const int r = c / (C::kWRow / 16), col = c % (C::kWRow / 16);
+      *reinterpret_cast<u32x4*>(base + r * L::kWStride + col * 16) = wreg[q];
+    }
+#pragma unroll
+    for (int q = 0; q < kXPer; ++q) {
+      const int c = tid + q * kPThreads;
+      const int r = c / (C::kXRow / 16), col = c % (C::kXRow / 16);
+      *reinterpret_cast<u32x4*>(base + L::kW + r * L::kXStride + col * 16) = xreg[q];
+    }
+    if constexpr (FMT == FMT_MXFP4) {
+      if (tid < kPBN) *reinterpret_cast<uint32_t*>(base + L::kW + L::kX + tid * 4) = wsreg;
+    }
+    if constexpr (FMT != FMT_BF16) {
+      if (tid < kPBM) *reinterpret_cast<uint32_t*>(base + L::kW + L::kX + L::kWS + tid * 4) = xsreg;
+    }
+  };
+
+  // wave sub-tiles: weight rows (j) and route columns (i)
+  int wrow_base[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (GATE_UP) wrow_base[j] = (j < 2) ? 32 * wn + 16 * j : kPBN / 2 + 32 * wn + 16 * (j - 2);
+    else wrow_base[j] = 64 * wn + 16 * j;
+  }
+  const int xcol_base = 64 * wm;
+
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[j][i] = zero;
+
+  load_step(0);
+  store_step(0);
+  __syncthreads();
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int cur = kb & 1;
+    if (kb + 1 < nkb) load_step(kb + 1);
+    const uint8_t* base = lds + cur * L::kBuf;
+
+    if constexpr (FMT == FMT_FP8) {
+      float sw[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int wr = wrow_of(wrow_base[j]);
+        sw[j] = static_cast<const float*>(bank.s)[(static_cast<size_t>(expert) * (a.N / 128) + wr / 128) * nkb + kb];
+      }
+      i32x8 xf[4];
+      float sx[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint8_t* p = base + L::kW + (xcol_base + 16 * i + r16) * L::kXStride + g * 32;
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(p);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 16);
+        xf[i] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        sx[i] = *reinterpret_cast<const float*>(base + L::kW + L::kX + L::kWS + (xcol_base + 16 * i + r16) * 4);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint8_t* p = base + (wrow_base[j] + r16) * L::kWStride + g * 32;
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(p);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 16);
+        const i32x8 wf = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf, xf[i], zero, 0, 0, 0, 0, 0, 0);
+          const float f = sx[i] * sw[j];
+          acc[j][i] += t * f;
+        }
+      }
+    } else if constexpr (FMT == FMT_MXFP4) {
+      // The f8f6f4 MFMA reads an fp8 lane-group g as K = 16g+[0,16) (bytes 0-15)
+      // and 64+16g+[0,16) (bytes 16-31), an fp4 lane-group g as the 32-value
+      // block [32g, 32g+32), and scale lane-group q as K block q.  The fp4
+      // weights are stored K-contiguous, so the fp8 activations are fed in that
+      // split order to pair every product with its K.
+      i32x8 xf[4];
+      int sxc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint8_t* p = base + L::kW + (xcol_base + 16 * i + r16) * L::kXStride;
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(p + 16 * g);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 64 + 16 * g);
+        xf[i] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        sxc[i] = static_cast<int>(*reinterpret_cast<const uint32_t*>(base + L::kW + L::kX + L::kWS +
+                                                                     (xcol_base + 16 * i + r16) * 4));
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint8_t* p = base + (wrow_base[j] + r16) * L::kWStride + g * 16;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+        const i32x8 wf = {(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
+        const int swc = base[L::kW + L::kX + (wrow_base[j] + r16) * 4 + g];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf, xf[i], acc[j][i], 4, 0, 0, swc, 0, sxc[i]);
+      }
+    } else {  // FMT_BF16: four K=32 MFMAs per 128 step
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        bf16x8 xf[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint8_t* p = base + L::kW + (xcol_base + 16 * i + r16) * L::kXStride + (g * 32 + s * 8) * 2;
+          xf[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(p));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint8_t* p = base + (wrow_base[j] + r16) * L::kWStride + (g * 32 + s * 8) * 2;
+          const bf16x8 wf = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(p));
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xf[i], acc[j][i], 0, 0, 0);
+        }
+      }
+    }
+
+    if (kb + 1 < nkb) store_step(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds weight rows wrow_base[j] + g*4 + v of route column r16
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int col = xcol_base + 16 * i + r16;
+    const int route = s_route[col];
+    if (route < 0) continue;
+    if (GATE_UP) {
+      const int arow = shared ? a.numel + route : route;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        uint16_t o[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float gg = bf16_round(acc[s][i][v]);
+          const float uu = bf16_round(acc[2 + s][i][v]);
+          o[v] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
+        }
+        const int n = n0 + 32 * wn + 16 * s + g * 4;
+        uint2 pk;
+        pk.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
+        pk.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+        *reinterpret_cast<uint2*>(a.out + static_cast<size_t>(arow) * a.inter + n) = pk;
+      }
+    } else {
+      const float wt = shared ? 1.0f : a.topk_w[route];
+      uint16_t* dst = shared ? a.sh_out + static_cast<size_t>(route) * a.N : a.out + static_cast<size_t>(route) * a.N;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint16_t o[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(acc[j][i][v] * wt);
+        const int n = n0 + wrow_base[j] + g * 4;
+        uint2 pk;
+        pk.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
+        pk.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+        *reinterpret_cast<uint2*>(dst + n) = pk;
+      }
+    }
+  }
+}
+
+hipError_t launch_act_quant(int mode, const uint16_t* x, int rows, int K, uint8_t* q, void* scales,
+                            hipStream_t stream) {
+  const dim3 grid((rows + 3) / 4), block(256);
+  if (mode == 0)
+    hipLaunchKernelGGL(act_quant_kernel<0>, grid, block, 0, stream, x, rows, K, q, scales);
+  else
+    hipLaunchKernelGGL(act_quant_kernel<1>, grid, block, 0, stream, x, rows, K, q, scales);
+  return hipGetLastError();
+}
+
+template <int FMT, int GU>
+static hipError_t launch_gemm_t(const PrefillGemmArgs& a, hipStream_t stream) {
+  static bool attr = false;
+  const void* fn = reinterpret_cast<const void*>(prefill_gemm_kernel<FMT, GU>);
+  if (!attr) {
+    hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, Lds<FMT>::kTotal);
+    if (err != hipSuccess) return err;
+    attr = true;
+  }
+  const int wgs = (a.max_blocks + a.shared_blocks) * a.ntiles;
+  hipLaunchKernelGGL((prefill_gemm_kernel<FMT, GU>), dim3(wgs), dim3(kPThreads), Lds<FMT>::kTotal, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_gemm(int fmt, int gate_up, const PrefillGemmArgs& a, hipStream_t stream) {
+  if (fmt == FMT_FP8) return gate_up ? launch_gemm_t<FMT_FP8, 1>(a, stream) : launch_gemm_t<FMT_FP8, 0>(a, stream);
+  if (fmt == FMT_MXFP4)
+    return gate_up ? launch_gemm_t<FMT_MXFP4, 1>(a, stream) : launch_gemm_t<FMT_MXFP4, 0>(a, stream);
+  if (fmt == FMT_BF16) return gate_up ? launch_gemm_t<FMT_BF16, 1>(a, stream) : launch_gemm_t<FMT_BF16, 0>(a, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ftmoe

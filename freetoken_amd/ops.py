@@ -121,6 +121,20 @@ def slot_map(topk_ids: torch.Tensor, slot_for_id: torch.Tensor, out: torch.Tenso
     return out
 
 
+def act_quant_fp8(x: torch.Tensor, mode: int = 0):
+    """Per-token per-128 FP8 quantisation of bf16 rows: mode 0 -> float32 scales
+    (amax/448), mode 1 -> uint8 e8m0 power-of-two scale codes."""
+    if x.dtype != torch.bfloat16:
+        raise ValueError("x must be bfloat16")
+    _require_gpu(x)
+    rows, k = x.shape
+    q = torch.empty((rows, k), dtype=torch.uint8, device=x.device)
+    sdt = torch.float32 if mode == 0 else torch.uint8
+    s = torch.empty((rows, k // 128), dtype=sdt, device=x.device)
+    check(lib().ftmoe_act_quant_fp8(_ptr(x), rows, k, mode, _ptr(q), _ptr(s), _stream(x.device)), "act_quant_fp8")
+    return q, s
+
+
 # --------------------------------------------------------------------------- expert banks
 
 _FORMATS = {"bf16": _lib.FMT_BF16, "fp8_block": _lib.FMT_FP8_B128, "mxfp4": _lib.FMT_MXFP4}
@@ -225,5 +239,36 @@ def experts_decode(x: torch.Tensor, topk_w: torch.Tensor, topk_ids: torch.Tensor
                                    int(apply_router_weight_on_input), _ptr(y), _ptr(ws), ws.numel(),
                                    _stream(x.device)),
         "experts_decode",
+    )
+    return y
+
+
+def experts_prefill(x: torch.Tensor, topk_w: torch.Tensor, topk_ids: torch.Tensor, bank: ExpertBank,
+                    shared: ExpertBank | None = None, activation: str = "silu",
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Prefill-regime experts (grouped GEMMs on MFMA) for a precomputed routing."""
+    if x.dtype != torch.bfloat16:
+        raise ValueError("hidden_states must be bfloat16")
+    if topk_w.dtype != torch.float32 or topk_ids.dtype != torch.int32:
+        raise ValueError("topk_weights must be float32 and topk_ids int32")
+    if topk_w.shape != topk_ids.shape:
+        raise ValueError("topk shape mismatch")
+    if activation not in _lib.ACT:
+        raise ValueError(f"Unsupported activation: {activation}")
+    _require_gpu(x, topk_w, topk_ids)
+    m, k = topk_ids.shape
+    if x.shape[0] != m:
+        raise ValueError("Number of tokens mismatch")
+    b = bank.cstruct()
+    sb = shared.cstruct() if shared is not None else None
+    bp = ctypes.byref(b)
+    sp = ctypes.byref(sb) if sb is not None else None
+    nbytes = lib().ftmoe_experts_prefill_workspace(m, k, bp, sp)
+    ws = _WS.get(x.device, nbytes)
+    y = out if out is not None else torch.empty_like(x)
+    check(
+        lib().ftmoe_experts_prefill(_ptr(x), m, k, _ptr(topk_w), _ptr(topk_ids), bp, sp, _lib.ACT[activation],
+                                    _ptr(y), _ptr(ws), ws.numel(), _stream(x.device)),
+        "experts_prefill",
     )
     return y

@@ -113,6 +113,13 @@ int ftmoe_align(const int32_t* topk_ids, int numel, int num_experts, int block_s
 int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_id, int num_experts,
                    int32_t* slot_ids, uint8_t* miss_mask, int64_t* stats, ftmoe_stream_t stream);
 
+/* Per-token per-128-group FP8 activation quantisation; replaces
+ * per_token_group_quant_fp8 (kernel/triton/fp8_block_linear.py:38-82, mode 0:
+ * float32 scale amax/448) and the DSV4 act_quant with power-of-two scales
+ * (kernel/triton/dsv4/fp8_linear.py:54-80, mode 1: uint8 e8m0 codes).
+ * x bf16 [rows, K]; q e4m3 [rows, K]; scales [rows, K/128]; K % 128 == 0. */
+int ftmoe_act_quant_fp8(const void* x, int rows, int K, int mode, void* q, void* scales, ftmoe_stream_t stream);
+
 /* Decode (W8A16 / W4A16 / bf16) expert computation for a precomputed routing;
  * replaces fused_experts_decode_impl (moe/fused.py:340-423),
  * fused_experts_decode_fp8_block (moe/fused_fp8_block.py:32-44) and
@@ -129,6 +136,29 @@ int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, c
                          const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
                          int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
                          ftmoe_stream_t stream);
+
+/* Prefill (grouped GEMM) expert computation for a precomputed routing;
+ * replaces fused_experts_fp8_block (moe/fused_fp8_block.py:16-29 ->
+ * kernel/triton/fp8_blockscale_moe.py:218-256, W8A8 with per-token per-128
+ * activation scales), routed_experts_fp4_prefill (moe/fused_ds_fp4.py:181-235,
+ * FP8-round-tripped activations with power-of-two scales) and the bf16
+ * fused_experts_impl (moe/fused.py:233-337), plus the shared-expert add.
+ * Same tensor conventions as ftmoe_experts_decode; the shared expert (nullable)
+ * must have the routed format and intermediate size.  Router weights always
+ * scale the down outputs. */
+size_t ftmoe_experts_prefill_workspace(int M, int top_k, const ftmoe_bank* bank, const ftmoe_bank* shared);
+int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
+                          const ftmoe_bank* bank, const ftmoe_bank* shared, int activation, void* y,
+                          void* workspace, size_t workspace_bytes, ftmoe_stream_t stream);
+
+/* Instrumentation (no counterpart in the reference, whose NVTX ranges play this
+ * role): between begin and end, every ftmoe_experts_* call made outside graph
+ * capture records a HIP event on its stream before its first kernel and after
+ * each kernel.  end synchronises on those events, writes the summed
+ * milliseconds of each stage (decode: align, gate_up, down, combine; prefill:
+ * align, x quant, gate_up, act quant, down, combine) and releases them. */
+int ftmoe_stage_timing_begin(void);
+int ftmoe_stage_timing_end(double* stage_ms, int max_stages, int* n_stages, int* n_calls);
 
 #ifdef __cplusplus
 }

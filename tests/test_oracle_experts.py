@@ -136,3 +136,27 @@ def test_slot_map_closed_form():
     ids2 = np.array([[0, 7, 3]], dtype=np.int32)
     s2, m2, st2 = S.slot_map(ids2, ident)
     assert s2.tolist() == ids2.tolist() and m2.sum() == 0 and st2[1] == 0
+
+
+def test_cpu_executor_restatement_matches_oracle():
+    """Two independent CPU implementations of the decode math agree: the numpy
+    oracle and the C++ restatement of the reference's CPU executor
+    (tolerance of the reference's CPU-vs-GPU check, tests/moe/test_cpu_moe.py:40-75)."""
+    from oracle.cpu_moe import CpuMoe
+    from oracle.numerics import bf16_bits
+
+    rng = np.random.default_rng(9)
+    for fmt, (E, H, I, k, M) in (("bf16", (16, 1024, 512, 4, 5)), ("mxfp4", (8, 512, 256, 2, 4))):
+        bank = synth.make_bank(fmt, E, H, I, rng, std=0.1)
+        x = synth.activations(rng, M, H)
+        ids = np.stack([rng.choice(E, k, replace=False) for _ in range(M)]).astype(np.int32)
+        w = rng.random((M, k)).astype(np.float32)
+        y_ref = X.moe_layer("decode", x, w, ids, bank)
+        cpu = CpuMoe(H, I, k, E, fmt, cpus=[0, 1])
+        if fmt == "bf16":
+            cpu.set_bank(bf16_bits(bank.gate_up), bf16_bits(bank.down))
+        else:
+            cpu.set_bank(bank.gate_up, bank.down, bank.gate_up_scale, bank.down_scale)
+        y = (cpu.run(bf16_bits(x), w, ids).astype(np.uint32) << 16).view(np.float32)
+        cpu.close()
+        assert max_rel(y, y_ref) < 2e-2 and cosine(y, y_ref) > 0.9995, fmt
