@@ -220,6 +220,8 @@ def run_decode(layer: DecodeLayer, M: int, steps: int, warmup: int, gen, graphs:
         arr = (ctypes.c_double * 8)()
         ns, nc = ctypes.c_int(), ctypes.c_int()
         _lib.check(L.ftmoe_stage_timing_end(arr, 8, ctypes.byref(ns), ctypes.byref(nc)), "stage timing")
+        if nc.value == 0 or ns.value < 4:
+            raise RuntimeError(f"stage timing recorded {nc.value} calls / {ns.value} stages")
         names = ["align", "gate_up", "down", "combine"]
         res["stage_us"] = {names[j]: arr[j] / max(1, nc.value) * 1e3 for j in range(min(ns.value, 4))}
         res["gate_up_bytes_per_launch"] = gu_bytes / steps

@@ -99,20 +99,26 @@ DecodeLayout decode_layout(void* ws, int M, int k, const ftmoe_bank* bank, const
 // ---- stage timing (instrumentation) ----------------------------------------
 struct StageTimer {
   bool on = false;
+  bool active = false;  // a call is being recorded
   std::vector<std::vector<hipEvent_t>> calls;  // events of each recorded call
   std::vector<hipEvent_t> cur;
   hipStream_t stream = nullptr;
 
   void start_call(hipStream_t s) {
+    active = false;
     if (!on) return;
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return;
+    // the legacy null stream cannot be captured; other streams are asked
+    if (s != nullptr) {
+      hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return;
+    }
     stream = s;
+    active = true;
     cur.clear();
     mark();
   }
   void mark() {
-    if (!on || !stream) return;
+    if (!active) return;
     hipEvent_t e;
     if (hipEventCreate(&e) != hipSuccess) return;
     if (hipEventRecord(e, stream) != hipSuccess) {
@@ -122,10 +128,10 @@ struct StageTimer {
     cur.push_back(e);
   }
   void end_call() {
-    if (!on || !stream) return;
+    if (!active) return;
     calls.push_back(cur);
     cur.clear();
-    stream = nullptr;
+    active = false;
   }
 };
 StageTimer g_timer;
