@@ -147,16 +147,28 @@ __global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
     }
     a.expert_ids[b] = e;
   }
-  if (a.stats && tid == 0) {
-    long long act = 0, miss = 0;
-    for (int e = 0; e < a.table_size; ++e)
+  if (a.stats) {
+    // distinct active / missing experts, counted in parallel
+    __shared__ unsigned long long s_act, s_miss;
+    if (tid == 0) {
+      s_act = 0;
+      s_miss = 0;
+    }
+    __syncthreads();
+    unsigned long long act = 0, miss = 0;
+    for (int e = tid; e < a.table_size; e += kAlignThreads)
       if (seen[e]) {
         ++act;
         miss += (a.slot_for_id[e] < 0) ? 1 : 0;
       }
-    a.stats[0] += act;
-    a.stats[1] += miss;
-    a.stats[2] += 1;
+    if (act) atomicAdd(&s_act, act);
+    if (miss) atomicAdd(&s_miss, miss);
+    __syncthreads();
+    if (tid == 0) {
+      a.stats[0] += static_cast<long long>(s_act);
+      a.stats[1] += static_cast<long long>(s_miss);
+      a.stats[2] += 1;
+    }
   }
 
   // ---- pass 2: stable scatter, 64 routes at a time per wave
@@ -260,17 +272,25 @@ __global__ void __launch_bounds__(1024) slot_map_kernel(const int32_t* ids, int 
     missed += (valid && s < 0) ? 1 : 0;
   }
   if (!stats) return;
+  __shared__ unsigned long long s_act, s_miss;
+  if (tid == 0) {
+    s_act = 0;
+    s_miss = 0;
+  }
   if (missed) atomicAdd(&s_missed, missed);
   __syncthreads();
+  unsigned long long act = 0, miss = 0;
+  for (int e = tid; e < table_size; e += blockDim.x)
+    if (seen[e]) {
+      ++act;
+      miss += slot_for_id[e] < 0 ? 1 : 0;
+    }
+  if (act) atomicAdd(&s_act, act);
+  if (miss) atomicAdd(&s_miss, miss);
+  __syncthreads();
   if (tid == 0) {
-    long long act = 0, miss = 0;
-    for (int e = 0; e < table_size; ++e)
-      if (seen[e]) {
-        ++act;
-        miss += slot_for_id[e] < 0 ? 1 : 0;
-      }
-    stats[0] += act;
-    stats[1] += miss;
+    stats[0] += static_cast<long long>(s_act);
+    stats[1] += static_cast<long long>(s_miss);
     stats[2] += 1;
     stats[3] += static_cast<long long>(s_missed);
   }

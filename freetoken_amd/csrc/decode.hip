@@ -34,7 +34,6 @@
 
 namespace ftmoe {
 
-constexpr int kTch = 4;       // route chunks (of 16) held in registers per pass
 constexpr int kDecWaves = 4;  // waves per workgroup (K split)
 
 template <int FMT>
@@ -42,20 +41,47 @@ __device__ __forceinline__ size_t row_bytes(int K) {
   return FMT == FMT_BF16 ? static_cast<size_t>(K) * 2 : FMT == FMT_FP8 ? static_cast<size_t>(K) : static_cast<size_t>(K) / 2;
 }
 
-// Loads and dequantises the lane's 32 K values of one weight row for K block kb
-// into four bf16x8 MFMA operands.  Returns the block scale for FMT_FP8 (else 1).
+// Raw (still quantised) A-operand bytes of one lane for one 128-wide K block.
 template <int FMT>
-__device__ __forceinline__ void load_a(const uint8_t* row, const void* sbase, int row_idx, int K, int kb,
-                                       int g, bf16x8 (&a)[4]) {
+struct RawA;
+template <>
+struct RawA<FMT_BF16> {
+  bf16x8 v[4];
+};
+template <>
+struct RawA<FMT_FP8> {
+  u32x4 v[2];
+};
+template <>
+struct RawA<FMT_MXFP4> {
+  u32x4 v[1];
+  uint32_t code;
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_raw(const uint8_t* row, const uint8_t* srow, int kb, int g, RawA<FMT>& r) {
   if constexpr (FMT == FMT_BF16) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(row + (static_cast<size_t>(kb) * 128 + g * 32) * 2);
+    const bf16x8* p = reinterpret_cast<const bf16x8*>(row + (static_cast<size_t>(kb) * 128 + g * 32) * 2);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) a[j] = __builtin_bit_cast(bf16x8, __builtin_nontemporal_load(p + j));
+    for (int j = 0; j < 4; ++j) r.v[j] = p[j];
   } else if constexpr (FMT == FMT_FP8) {
     const u32x4* p = reinterpret_cast<const u32x4*>(row + static_cast<size_t>(kb) * 128 + g * 32);
-    const u32x4 v0 = __builtin_nontemporal_load(p);
-    const u32x4 v1 = __builtin_nontemporal_load(p + 1);
-    const uint32_t wds[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+    r.v[0] = p[0];
+    r.v[1] = p[1];
+  } else {
+    r.v[0] = *reinterpret_cast<const u32x4*>(row + (static_cast<size_t>(kb) * 128 + g * 32) / 2);
+    r.code = srow[kb * 4 + g];
+  }
+}
+
+// Dequantises raw bytes into four bf16x8 MFMA operands (exact conversions).
+template <int FMT>
+__device__ __forceinline__ void dequant(const RawA<FMT>& r, bf16x8 (&a)[4]) {
+  if constexpr (FMT == FMT_BF16) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = r.v[j];
+  } else if constexpr (FMT == FMT_FP8) {
+    const uint32_t wds[8] = {r.v[0][0], r.v[0][1], r.v[0][2], r.v[0][3], r.v[1][0], r.v[1][1], r.v[1][2], r.v[1][3]};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wds[2 * j], 1.0f, false);
@@ -64,233 +90,276 @@ __device__ __forceinline__ void load_a(const uint8_t* row, const void* sbase, in
       const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wds[2 * j + 1], 1.0f, true);
       a[j] = bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
     }
-  } else {  // FMT_MXFP4
-    const u32x4 v = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x4*>(row + (static_cast<size_t>(kb) * 128 + g * 32) / 2));
-    const uint8_t code = static_cast<const uint8_t*>(sbase)[static_cast<size_t>(row_idx) * (K / 32) + kb * 4 + g];
-    const float sc = __uint_as_float(static_cast<uint32_t>(code) << 23);
-    const uint32_t wds[4] = {v[0], v[1], v[2], v[3]};
+  } else {
+    const float sc = __uint_as_float(r.code << 23);  // 2^(code-127), exact for codes >= 1
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wds[j], sc, 0);
-      const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wds[j], sc, 1);
-      const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wds[j], sc, 2);
-      const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wds[j], sc, 3);
+      const uint32_t w = r.v[0][j];
+      const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0);
+      const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1);
+      const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2);
+      const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3);
       a[j] = bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
     }
   }
 }
 
-__device__ __forceinline__ void load_b(const uint16_t* row, int kb, int g, bf16x8 (&b)[4]) {
-  const u32x4* p = reinterpret_cast<const u32x4*>(row + static_cast<size_t>(kb) * 128 + g * 32);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) b[j] = __builtin_bit_cast(bf16x8, p[j]);
-}
+// Registers of one K block in flight: NMAT weight tiles and NCH activation chunks.
+template <int FMT, int NMAT, int NCH>
+struct KStage {
+  RawA<FMT> w[NMAT];
+  u32x4 b[NCH][4];
+};
 
-template <int FMT>
-__device__ __forceinline__ float fp8_block_scale(const void* sbase, int row0, int N, int K, int kb) {
-  if constexpr (FMT == FMT_FP8) {
-    return static_cast<const float*>(sbase)[static_cast<size_t>(row0 / 128) * (K / 128) + kb];
-  } else {
-    return 1.0f;
+// Lanes whose route column lies past the segment's end skip their activation
+// loads and supply zeros (MFMA output column c depends on B column c only, and
+// those columns are never stored).
+template <int FMT, int NMAT, int NCH>
+__device__ __forceinline__ void load_stage(KStage<FMT, NMAT, NCH>& st, const uint8_t* const (&rows)[NMAT],
+                                           const uint8_t* const (&srows)[NMAT], const uint16_t* const* brow,
+                                           const bool (&bvalid)[NCH], int kb, int g) {
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m) load_raw<FMT>(rows[m], srows[m], kb, g, st.w[m]);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(brow[c] + static_cast<size_t>(kb) * 128 + g * 32);
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) st.b[c][j] = bvalid[c] ? p[j] : zero;
   }
 }
 
-// Accumulates rows [row0, row0+16) of one matrix against up to kTch route chunks.
-// NMAT = 2 processes a second matrix (up rows, offset by row_off) in the same pass.
-template <int FMT, int NMAT>
-__device__ __forceinline__ void gemv_tile(const uint8_t* wbase, const void* sbase, int N, int K, int row0,
-                                          int row_off, const uint16_t* const* brow, int nch,
-                                          f32x4 (&acc)[NMAT][kTch]) {
-  const int lane = lane_id();
-  const int r = lane & 15, g = lane >> 4;
-  const int wave = threadIdx.x / kWave;
-  const int nkb = K / 128;
-  const size_t rb = row_bytes<FMT>(K);
-  const uint8_t* rows[NMAT];
-  int ridx[NMAT];
+template <int FMT, int NMAT, int NCH>
+__device__ __forceinline__ void compute_stage(const KStage<FMT, NMAT, NCH>& st, const float* const (&fscale)[NMAT],
+                                              int kb, f32x4 (&acc)[NMAT][NCH]) {
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) {
-    ridx[m] = row0 + r + m * row_off;
-    rows[m] = wbase + static_cast<size_t>(ridx[m]) * rb;
+    bf16x8 a[4];
+    if constexpr (FMT == FMT_BF16) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[j] = st.w[m].v[j];  // element-wise: no aggregate copy
+    } else {
+      dequant<FMT>(st.w[m], a);
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if constexpr (FMT == FMT_FP8) {
+        f32x4 t = zero;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j], __builtin_bit_cast(bf16x8, st.b[c][j]), t, 0, 0, 0);
+        acc[m][c] += t * fscale[m][kb];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[m][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j], __builtin_bit_cast(bf16x8, st.b[c][j]), acc[m][c],
+                                                              0, 0, 0);
+      }
+    }
   }
+}
+
+// Accumulates NMAT 16-row weight tiles against NCH route chunks of 16.  Wave w
+// owns the contiguous K blocks [w*nkb/4, (w+1)*nkb/4) and keeps the loads of
+// the next K block in flight while it computes the current one.
+template <int FMT, int NMAT, int NCH>
+__device__ __forceinline__ void gemv_tile(const uint8_t* const (&rows)[NMAT], const uint8_t* const (&srows)[NMAT],
+                                          const float* const (&fscale)[NMAT], int K, const uint16_t* const* brow,
+                                          const bool (&bvalid)[NCH], f32x4 (&acc)[NMAT][NCH]) {
+  const int g = lane_id() >> 4;
+  const int wave = threadIdx.x / kWave;
+  const int nkb = K / 128;
+  const int kb_lo = wave * nkb / kDecWaves, kb_hi = (wave + 1) * nkb / kDecWaves;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-    for (int c = 0; c < kTch; ++c) acc[m][c] = zero;
-
-  for (int kb = wave; kb < nkb; kb += kDecWaves) {
-    bf16x8 a[NMAT][4];
-#pragma unroll
-    for (int m = 0; m < NMAT; ++m) load_a<FMT>(rows[m], sbase, ridx[m], K, kb, g, a[m]);
-    bf16x8 b[kTch][4];
-#pragma unroll
-    for (int c = 0; c < kTch; ++c)
-      if (c < nch) load_b(brow[c], kb, g, b[c]);
-#pragma unroll
-    for (int m = 0; m < NMAT; ++m) {
-      const float sc = fp8_block_scale<FMT>(sbase, row0 + m * row_off, N, K, kb);
-#pragma unroll
-      for (int c = 0; c < kTch; ++c) {
-        if (c < nch) {
-          if constexpr (FMT == FMT_FP8) {
-            f32x4 t = zero;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[m][j], b[c][j], t, 0, 0, 0);
-            acc[m][c] += t * sc;
-          } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[m][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[m][j], b[c][j], acc[m][c], 0, 0, 0);
-          }
-        }
-      }
+    for (int c = 0; c < NCH; ++c) acc[m][c] = zero;
+  KStage<FMT, NMAT, NCH> s0, s1;
+  if (kb_lo < kb_hi) load_stage(s0, rows, srows, brow, bvalid, kb_lo, g);
+  for (int kb = kb_lo; kb < kb_hi; kb += 2) {
+    if (kb + 1 < kb_hi) load_stage(s1, rows, srows, brow, bvalid, kb + 1, g);
+    compute_stage(s0, fscale, kb, acc);
+    if (kb + 1 < kb_hi) {
+      if (kb + 2 < kb_hi) load_stage(s0, rows, srows, brow, bvalid, kb + 2, g);
+      compute_stage(s1, fscale, kb + 1, acc);
     }
   }
 }
 
-template <int FMT_R, int FMT_S, int STAGE>
-__global__ void __launch_bounds__(kDecWaves * kWave) decode_stage_kernel(DecodeArgs a) {
-  __shared__ f32x4 red[kDecWaves][2][kTch][kWave];
-  const int seg = blockIdx.y;
-  const bool shared = seg == a.max_seg;
-  if (!shared && seg >= a.n_seg[0]) return;
+// One pass over up to NCH chunks (16 routes each) of a segment for a workgroup
+// tile of RT 16-row tiles per matrix, including the split-K reduction and the
+// epilogue.  LDS: red[waves][NMAT][NCH][64] float4.
+template <int FMT, int STAGE, int RT, int NCH>
+__device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView& bank, bool shared, int expert,
+                                            int start, int count, int base, int row0, int inter, f32x4* red) {
+  constexpr int NMAT = STAGE == 0 ? 2 * RT : RT;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int r16 = lane & 15, g = lane >> 4;
+  const int N = STAGE == 0 ? 2 * inter : a.H;
+  const int K = STAGE == 0 ? a.H : inter;
+  const int nch = min(NCH, (count - base + 15) / 16);
 
+  const uint16_t* brow[NCH];
+  bool bvalid[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    bvalid[c] = base + c * 16 + r16 < count;
+    const int col = min(base + c * 16 + r16, count - 1);
+    if (STAGE == 0) {
+      const int tok = shared ? col : a.sorted[start + col] / a.k;
+      brow[c] = a.x + static_cast<size_t>(tok) * a.H;
+    } else {
+      const int arow = shared ? a.M * a.k + col : a.sorted[start + col];
+      brow[c] = a.act + static_cast<size_t>(arow) * a.act_stride;
+    }
+  }
+  const size_t rb = row_bytes<FMT>(K);
+  const uint8_t* wexp = bank.w + static_cast<size_t>(expert) * N * rb;
+  const uint8_t* rows[NMAT];
+  const uint8_t* srows[NMAT];
+  const float* fscale[NMAT];
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m) {
+    // matrix m: gate tiles first, then up tiles (stage 0); down tiles (stage 1)
+    const int tile_row = (STAGE == 0 && m >= RT) ? inter + row0 + 16 * (m - RT) : row0 + 16 * m;
+    const int ridx = tile_row + r16;
+    rows[m] = wexp + static_cast<size_t>(ridx) * rb;
+    if constexpr (FMT == FMT_MXFP4) {
+      srows[m] = static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(expert) * N + ridx) * (K / 32);
+    } else {
+      srows[m] = nullptr;
+    }
+    if constexpr (FMT == FMT_FP8) {
+      // the 16-row tile sits inside one 128-row scale block
+      fscale[m] = static_cast<const float*>(bank.s) +
+                  (static_cast<size_t>(expert) * (N / 128) + tile_row / 128) * (K / 128);
+    } else {
+      fscale[m] = nullptr;
+    }
+  }
+  f32x4 acc[NMAT][NCH];
+  gemv_tile<FMT, NMAT, NCH>(rows, srows, fscale, K, brow, bvalid, acc);
+
+  // split-K reduction in fixed wave order
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      if (c < nch) red[((wave * NMAT + m) * NCH + c) * kWave + lane] = acc[m][c];
+  __syncthreads();
+  // wave w finishes (output tile, chunk) items w, w+4, ...
+  for (int item = wave; item < RT * nch; item += kDecWaves) {
+    const int t = item / nch, c = item % nch;
+    const int col = base + c * 16 + r16;
+    const int mg = t, mu = STAGE == 0 ? RT + t : t;  // gate / up matrices (down: mg == mu)
+    f32x4 sg = red[((0 * NMAT + mg) * NCH + c) * kWave + lane];
+    f32x4 su = red[((0 * NMAT + mu) * NCH + c) * kWave + lane];
+#pragma unroll
+    for (int v = 1; v < kDecWaves; ++v) {
+      sg += red[((v * NMAT + mg) * NCH + c) * kWave + lane];
+      if (STAGE == 0) su += red[((v * NMAT + mu) * NCH + c) * kWave + lane];
+    }
+    if (col >= count) continue;
+    const int rows_at = row0 + 16 * t + g * 4;  // this lane's 4 consecutive output rows
+    uint16_t o[4];
+    if (STAGE == 0) {
+      const int route = shared ? -1 : a.sorted[start + col];
+      const float win = (!shared && a.weight_on_input) ? a.topk_w[route] : 1.0f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float gg = bf16_round(sg[v] * win);
+        const float uu = bf16_round(su[v] * win);
+        o[v] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
+      }
+      const int arow = shared ? a.M * a.k + col : route;
+      uint2 pk;
+      pk.x = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
+      pk.y = static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16);
+      *reinterpret_cast<uint2*>(a.act + static_cast<size_t>(arow) * a.act_stride + rows_at) = pk;
+    } else {
+      uint16_t* dst;
+      float wt = 1.0f;
+      if (shared) {
+        dst = a.sh_out + static_cast<size_t>(col) * a.H + rows_at;
+      } else {
+        const int route = a.sorted[start + col];
+        if (!a.weight_on_input) wt = a.topk_w[route];
+        dst = a.ic3 + static_cast<size_t>(route) * a.H + rows_at;
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(sg[v] * wt);
+      uint2 pk;
+      pk.x = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
+      pk.y = static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16);
+      *reinterpret_cast<uint2*>(dst) = pk;
+    }
+  }
+  __syncthreads();
+}
+
+constexpr int kRedFloats4 = kDecWaves * 4 * kWave;  // NMAT * chunks_per_pass <= 4
+
+// Route chunks (of 16) per pass, sized so that two K stages of weights and
+// activations plus the accumulators fit the 256 registers of a wave at
+// occupancy 2: stage 0 holds gate and up tiles, stage 1 only down tiles.
+template <int STAGE, int RT>
+constexpr int chunks_per_pass() {
+  return STAGE == 0 ? (RT == 1 ? 2 : 1) : (RT == 1 ? 4 : 2);
+}
+
+template <int FMT, int STAGE, int RT>
+__device__ __forceinline__ void decode_segment(const DecodeArgs& a, const BankView& bank, bool shared, int expert,
+                                               int start, int count, int row0, int inter, f32x4* red) {
+  constexpr int CMAX = chunks_per_pass<STAGE, RT>();
+  for (int base = 0; base < count; base += 16 * CMAX) {
+    const int nch = min(CMAX, (count - base + 15) / 16);
+    if constexpr (CMAX == 1) {
+      decode_pass<FMT, STAGE, RT, 1>(a, bank, shared, expert, start, count, base, row0, inter, red);
+    } else if constexpr (CMAX == 2) {
+      if (nch == 1) decode_pass<FMT, STAGE, RT, 1>(a, bank, shared, expert, start, count, base, row0, inter, red);
+      else decode_pass<FMT, STAGE, RT, 2>(a, bank, shared, expert, start, count, base, row0, inter, red);
+    } else {
+      if (nch == 1) decode_pass<FMT, STAGE, RT, 1>(a, bank, shared, expert, start, count, base, row0, inter, red);
+      else if (nch == 2) decode_pass<FMT, STAGE, RT, 2>(a, bank, shared, expert, start, count, base, row0, inter, red);
+      else decode_pass<FMT, STAGE, RT, 4>(a, bank, shared, expert, start, count, base, row0, inter, red);
+    }
+  }
+}
+
+template <int FMT_R, int FMT_S, int STAGE, int RT>
+__global__ void __launch_bounds__(kDecWaves * kWave) decode_stage_kernel(DecodeArgs a) {
+  __shared__ f32x4 red[kRedFloats4];
+  const int seg = blockIdx.y;
+  const bool shared = seg == a.max_seg;
+  if (!shared && seg >= a.n_seg[0]) return;
   const int inter = shared ? a.Is : a.I;
-  const int row0 = blockIdx.x * 16;
+  const int row0 = blockIdx.x * 16 * RT;
   if (STAGE == 0 && row0 >= inter) return;
   const int count = shared ? a.M : a.seg_count[seg];
   const int start = shared ? 0 : a.seg_start[seg];
   const int expert = shared ? 0 : a.seg_expert[seg];
-  const BankView bank = STAGE == 0 ? (shared ? a.sh_gate_up : a.gate_up) : (shared ? a.sh_down : a.down);
-  const int N = STAGE == 0 ? 2 * inter : a.H;
-  const int K = STAGE == 0 ? a.H : inter;
+  // field-wise selects keep the kernel argument block out of private memory
+  BankView bank;
+  if constexpr (STAGE == 0) {
+    bank.w = shared ? a.sh_gate_up.w : a.gate_up.w;
+    bank.s = shared ? a.sh_gate_up.s : a.gate_up.s;
+  } else {
+    bank.w = shared ? a.sh_down.w : a.down.w;
+    bank.s = shared ? a.sh_down.s : a.down.s;
+  }
   const int fmt = shared ? FMT_S : FMT_R;
-
-  for (int pass = 0; pass * 16 * kTch < count; ++pass) {
-    const int base = pass * 16 * kTch;
-    const int nch = min(kTch, (count - base + 15) / 16);
-    // B operand rows of this lane's route column in each chunk (clamped, masked later)
-    const uint16_t* brow[kTch];
-#pragma unroll
-    for (int c = 0; c < kTch; ++c) {
-      const int col = min(base + c * 16 + r16, count - 1);
-      if (STAGE == 0) {
-        const int tok = shared ? col : a.sorted[start + col] / a.k;
-        brow[c] = a.x + static_cast<size_t>(tok) * a.H;
-      } else {
-        const int arow = shared ? a.M * a.k + col : a.sorted[start + col];
-        brow[c] = a.act + static_cast<size_t>(arow) * a.act_stride;
-      }
-    }
-    f32x4 acc[2][kTch];
-    if (fmt == FMT_BF16) {
-      if constexpr (FMT_R == FMT_BF16 || FMT_S == FMT_BF16) {
-        const size_t eb = static_cast<size_t>(N) * row_bytes<FMT_BF16>(K);
-        if (STAGE == 0) {
-          f32x4 t[2][kTch];
-          gemv_tile<FMT_BF16, 2>(bank.w + expert * eb, nullptr, N, K, row0, inter, brow, nch, t);
-#pragma unroll
-          for (int c = 0; c < kTch; ++c) { acc[0][c] = t[0][c]; acc[1][c] = t[1][c]; }
-        } else {
-          f32x4 t[1][kTch];
-          gemv_tile<FMT_BF16, 1>(bank.w + expert * eb, nullptr, N, K, row0, 0, brow, nch, t);
-#pragma unroll
-          for (int c = 0; c < kTch; ++c) acc[0][c] = t[0][c];
-        }
-      }
-    } else if (fmt == FMT_FP8) {
-      if constexpr (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) {
-        const size_t eb = static_cast<size_t>(N) * K;
-        const float* sb = static_cast<const float*>(bank.s) + static_cast<size_t>(expert) * (N / 128) * (K / 128);
-        if (STAGE == 0) {
-          f32x4 t[2][kTch];
-          gemv_tile<FMT_FP8, 2>(bank.w + expert * eb, sb, N, K, row0, inter, brow, nch, t);
-#pragma unroll
-          for (int c = 0; c < kTch; ++c) { acc[0][c] = t[0][c]; acc[1][c] = t[1][c]; }
-        } else {
-          f32x4 t[1][kTch];
-          gemv_tile<FMT_FP8, 1>(bank.w + expert * eb, sb, N, K, row0, 0, brow, nch, t);
-#pragma unroll
-          for (int c = 0; c < kTch; ++c) acc[0][c] = t[0][c];
-        }
-      }
-    } else {
-      if constexpr (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4) {
-        const size_t eb = static_cast<size_t>(N) * (K / 2);
-        const uint8_t* sb = static_cast<const uint8_t*>(bank.s) + static_cast<size_t>(expert) * N * (K / 32);
-        if (STAGE == 0) {
-          f32x4 t[2][kTch];
-          gemv_tile<FMT_MXFP4, 2>(bank.w + expert * eb, sb, N, K, row0, inter, brow, nch, t);
-#pragma unroll
-          for (int c = 0; c < kTch; ++c) { acc[0][c] = t[0][c]; acc[1][c] = t[1][c]; }
-        } else {
-          f32x4 t[1][kTch];
-          gemv_tile<FMT_MXFP4, 1>(bank.w + expert * eb, sb, N, K, row0, 0, brow, nch, t);
-#pragma unroll
-          for (int c = 0; c < kTch; ++c) acc[0][c] = t[0][c];
-        }
-      }
-    }
-    // ---- split-K reduction in fixed wave order
-    constexpr int NM = STAGE == 0 ? 2 : 1;
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int c = 0; c < kTch; ++c)
-        if (c < nch) red[wave][m][c][lane] = acc[m][c];
-    __syncthreads();
-    if (wave < nch) {
-      const int c = wave;
-      f32x4 s[NM];
-#pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        s[m] = red[0][m][c][lane];
-#pragma unroll
-        for (int v = 1; v < kDecWaves; ++v) s[m] += red[v][m][c][lane];
-      }
-      const int col = base + c * 16 + r16;
-      if (col < count) {
-        const int rows_at = row0 + g * 4;  // this lane's 4 consecutive output rows
-        uint16_t o[4];
-        if (STAGE == 0) {
-          const int route = shared ? -1 : a.sorted[start + col];
-          const float win = (!shared && a.weight_on_input) ? a.topk_w[route] : 1.0f;
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const float gg = bf16_round(s[0][v] * win);
-            const float uu = bf16_round(s[1][v] * win);
-            o[v] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
-          }
-          const int arow = shared ? a.M * a.k + col : route;
-          uint2 pk;
-          pk.x = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
-          pk.y = static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16);
-          *reinterpret_cast<uint2*>(a.act + static_cast<size_t>(arow) * a.act_stride + rows_at) = pk;
-        } else {
-          uint16_t* dst;
-          float wt = 1.0f;
-          if (shared) {
-            dst = a.sh_out + static_cast<size_t>(col) * a.H + rows_at;
-          } else {
-            const int route = a.sorted[start + col];
-            if (!a.weight_on_input) wt = a.topk_w[route];
-            dst = a.ic3 + static_cast<size_t>(route) * a.H + rows_at;
-          }
-#pragma unroll
-          for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(s[0][v] * wt);
-          uint2 pk;
-          pk.x = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
-          pk.y = static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16);
-          *reinterpret_cast<uint2*>(dst) = pk;
-        }
-      }
-    }
-    __syncthreads();
+  if (fmt == FMT_BF16) {
+    if constexpr (FMT_R == FMT_BF16 || FMT_S == FMT_BF16)
+      decode_segment<FMT_BF16, STAGE, RT>(a, bank, shared, expert, start, count, row0, inter, red);
+  } else if (fmt == FMT_FP8) {
+    if constexpr (FMT_R == FMT_FP8 || FMT_S == FMT_FP8)
+      decode_segment<FMT_FP8, STAGE, RT>(a, bank, shared, expert, start, count, row0, inter, red);
+  } else {
+    if constexpr (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4)
+      decode_segment<FMT_MXFP4, STAGE, RT>(a, bank, shared, expert, start, count, row0, inter, red);
   }
 }
 
@@ -307,15 +376,25 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
   const int t = idx / per_tok;
   const int h = (idx - t * per_tok) * 8;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int r = 0; r < k; ++r) {
-    const int e = ids[t * k + r];
-    if (e < 0 || e >= num_rows) continue;
-    const uint4 v = *reinterpret_cast<const uint4*>(ic3 + static_cast<size_t>(t * k + r) * H + h);
-    const uint32_t wds[4] = {v.x, v.y, v.z, v.w};
+  // routes in groups of 8: all loads of a group are issued before the adds
+  for (int r0 = 0; r0 < k; r0 += 8) {
+    u32x4 v[8];
+    bool ok[8];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      acc[2 * q] += bf16_to_f32(static_cast<uint16_t>(wds[q] & 0xffffu));
-      acc[2 * q + 1] += bf16_to_f32(static_cast<uint16_t>(wds[q] >> 16));
+    for (int q = 0; q < 8; ++q) {
+      const int r = r0 + q;
+      const int e = r < k ? ids[t * k + r] : -1;
+      ok[q] = e >= 0 && e < num_rows;
+      if (ok[q]) v[q] = *reinterpret_cast<const u32x4*>(ic3 + static_cast<size_t>(t * k + r) * H + h);
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      if (!ok[q]) continue;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        acc[2 * w] += bf16_to_f32(static_cast<uint16_t>(v[q][w] & 0xffffu));
+        acc[2 * w + 1] += bf16_to_f32(static_cast<uint16_t>(v[q][w] >> 16));
+      }
     }
   }
   uint16_t o[8];
@@ -343,10 +422,23 @@ template <int FR, int FS>
 static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared, hipStream_t stream) {
   const int gy = a.max_seg + (has_shared ? 1 : 0);
   const int imax = has_shared ? max(a.I, a.Is) : a.I;
-  if (stage == 0)
-    hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 0>), dim3(imax / 16, gy), dim3(kDecWaves * kWave), 0, stream, a);
-  else
-    hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 1>), dim3(a.H / 16, gy), dim3(kDecWaves * kWave), 0, stream, a);
+  const dim3 block(kDecWaves * kWave);
+  // two 16-row tiles per workgroup once the grid has enough workgroups to fill
+  // the chip twice over; they halve the activation loads per weight byte
+  constexpr int kMinWgs = 2048;
+  if (stage == 0) {
+    const bool rt2 = (imax % 32 == 0) && a.I % 32 == 0 && (a.Is % 32 == 0) && (imax / 32) * gy >= kMinWgs;
+    if (rt2)
+      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 0, 2>), dim3(imax / 32, gy), block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 0, 1>), dim3(imax / 16, gy), block, 0, stream, a);
+  } else {
+    const bool rt2 = (a.H % 32 == 0) && (a.H / 32) * gy >= kMinWgs;
+    if (rt2)
+      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 1, 2>), dim3(a.H / 32, gy), block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 1, 1>), dim3(a.H / 16, gy), block, 0, stream, a);
+  }
   return hipGetLastError();
 }
 

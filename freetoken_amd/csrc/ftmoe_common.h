@@ -79,28 +79,69 @@ __device__ __forceinline__ float act_apply(int act, float g) {
   return 0.5f * g * (1.0f + tanhf(inner));
 }
 
-// 64-bit wave max via xor shuffles (all lanes end with the maximum).
+// Cross-lane reductions: DPP butterflies inside each 16-lane row (quad_perm
+// xor1 / xor2, row_half_mirror, row_mirror leave every lane of a row with the
+// row's result), then the four row results are combined from readlanes.  This
+// keeps the dependent chain at a few VALU latencies instead of the LDS-latency
+// permutes of generic shuffles.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL, 0xF, 0xF,
+                                                           false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = dpp_u32<CTRL>(static_cast<uint32_t>(v));
+  const uint32_t hi = dpp_u32<CTRL>(static_cast<uint32_t>(v >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(v), lane);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), lane);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// Wave-wide maximum of a 64-bit key; the result is uniform across the wave.
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), off, kWave);
-    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), off, kWave);
-    const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
-    v = o > v ? o : v;
-  }
-  return v;
+  v = max_u64(v, dpp_u64<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = max_u64(v, dpp_u64<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = max_u64(v, dpp_u64<0x141>(v));  // row_half_mirror
+  v = max_u64(v, dpp_u64<0x140>(v));  // row_mirror
+  return max_u64(max_u64(readlane_u64(v, 0), readlane_u64(v, 16)),
+                 max_u64(readlane_u64(v, 32), readlane_u64(v, 48)));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(v)));
 }
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x141>(v);
+  v += dpp_f32<0x140>(v);
+  const float a = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+  const float b = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16));
+  const float c = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32));
+  const float d = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 48));
+  return (a + b) + (c + d);
 }
 
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  const float a = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+  const float b = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16));
+  const float c = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32));
+  const float d = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }

@@ -1,15 +1,17 @@
 // Router top-k kernels: softmax top-k and DeepSeek-V3 grouped sigmoid top-k.
 //
-// One wave per token.  Expert e lives in lane (e % 64), register slot e / 64,
-// so E <= 64 * kMaxPerLane.  Selection is k rounds of a wave-wide maximum over
-// 64-bit keys (order_key(value) << 32 | ~index): the larger value wins and on
-// equal values the lower expert index wins -- the lowest-index tie rule of the
-// reference's gpt-oss router (kernel/triton/mxfp4_moe.py:288-331).
+// One wave per token.  Expert e lives in lane (e % 64), register slot e / 64;
+// PER = ceil(E / 64) slots per lane is a template parameter.  Selection is k
+// rounds of a wave-wide maximum over 64-bit keys (order_key(value) << 32 | ~index):
+// the larger value wins and on equal values the lower expert index wins -- the
+// lowest-index tie rule of the reference's gpt-oss router
+// (kernel/triton/mxfp4_moe.py:288-331).  Each lane keeps the best not-yet-taken
+// key of its own slots, so a round costs one wave reduction plus a local update.
 #include "kernels.h"
 
 namespace ftmoe {
 
-constexpr int kMaxPerLane = 16;  // E <= 1024
+constexpr int kRouteWaves = 4;
 
 __device__ __forceinline__ uint64_t pack_key(float v, int e) {
   return (static_cast<uint64_t>(order_key(v)) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(e));
@@ -22,62 +24,59 @@ __device__ __forceinline__ float load_logit<float>(const float* p) { return *p; 
 template <>
 __device__ __forceinline__ float load_logit<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
 
-// fused_topk (reference moe/fused.py:38-85): selection on fp32 logits; with
-// renormalize the weights are the softmax over the k selected logits, else the
-// softmax over all experts evaluated at the selected ones.
-template <typename T>
-__global__ void __launch_bounds__(256) softmax_topk_kernel(const T* __restrict__ logits, int M, int E,
-                                                           int k, int renorm, float* __restrict__ out_w,
-                                                           int32_t* __restrict__ out_ids) {
+// k rounds of selection over keys[PER] (0 = empty); returns the winner index of
+// round r in lane r (lanes >= k: -1).
+template <int PER>
+__device__ __forceinline__ int select_topk(uint64_t (&keys)[PER], int k) {
   const int lane = lane_id();
-  const int tok = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-  if (tok >= M) return;
-  const T* row = logits + static_cast<size_t>(tok) * E;
-  float v[kMaxPerLane];
-  uint32_t taken = 0;
-#pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
-    const int e = lane + j * kWave;
-    v[j] = (e < E) ? load_logit<T>(row + e) : -INFINITY;
-  }
-  float my_val = 0.0f;
-  int my_idx = -1;
+  int mine = -1;
   for (int r = 0; r < k; ++r) {
     uint64_t best = 0;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
-      const int e = lane + j * kWave;
-      if (e < E && !((taken >> j) & 1u)) {
-        const uint64_t key = pack_key(v[j], e);
-        best = key > best ? key : best;
-      }
-    }
+    for (int j = 0; j < PER; ++j) best = max_u64(best, keys[j]);
     best = wave_max_u64(best);
     const int win = static_cast<int>(~static_cast<uint32_t>(best));
-    if ((win & (kWave - 1)) == lane) taken |= 1u << (win / kWave);
-    // value of the winner, broadcast from its owner lane
-    float wv = 0.0f;
+    if ((win & (kWave - 1)) == lane) {
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j)
-      if (j == win / kWave) wv = v[j];
-    wv = __shfl(wv, win & (kWave - 1), kWave);
-    if (lane == r) {
-      my_val = wv;
-      my_idx = win;
+      for (int j = 0; j < PER; ++j)
+        if (j == win / kWave) keys[j] = 0;
     }
+    if (lane == r) mine = win;
   }
-  const float vmax = __shfl(my_val, 0, kWave);  // rank 0 holds the maximum
+  return mine;
+}
+
+// fused_topk (reference moe/fused.py:38-85): selection on fp32 logits; with
+// renormalize the weights are the softmax over the k selected logits, else the
+// softmax over all experts evaluated at the selected ones.
+template <typename T, int PER>
+__global__ void __launch_bounds__(kRouteWaves * kWave) softmax_topk_kernel(const T* __restrict__ logits, int M,
+                                                                            int E, int k, int renorm,
+                                                                            float* __restrict__ out_w,
+                                                                            int32_t* __restrict__ out_ids) {
+  const int lane = lane_id();
+  const int tok = blockIdx.x * kRouteWaves + threadIdx.x / kWave;
+  if (tok >= M) return;
+  const T* row = logits + static_cast<size_t>(tok) * E;
+  float v[PER];
+  uint64_t keys[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int e = lane + j * kWave;
+    v[j] = (e < E) ? load_logit<T>(row + e) : -INFINITY;
+    keys[j] = (e < E) ? pack_key(v[j], e) : 0;
+  }
+  const int my_idx = select_topk<PER>(keys, k);
+  const float my_val = (lane < k) ? load_logit<T>(row + my_idx) : -INFINITY;
+  const float vmax = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_val), 0));  // rank 0
   float denom;
   if (renorm) {
-    const float ex = (lane < k) ? expf(my_val - vmax) : 0.0f;
-    denom = wave_sum_f32(ex);
+    denom = wave_sum_f32((lane < k) ? expf(my_val - vmax) : 0.0f);
   } else {
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
-      const int e = lane + j * kWave;
-      if (e < E) s += expf(v[j] - vmax);
-    }
+    for (int j = 0; j < PER; ++j)
+      if (lane + j * kWave < E) s += expf(v[j] - vmax);
     denom = wave_sum_f32(s);
   }
   if (lane < k) {
@@ -90,19 +89,22 @@ __global__ void __launch_bounds__(256) softmax_topk_kernel(const T* __restrict__
 //   s = sigmoid(l); c = s + bias; group score = top1(c) + top2(c) in the group;
 //   keep topk_group groups; top-k of c over kept groups; w = s[id];
 //   renorm w / (sum + 1e-20); times scale.  Uses det_sigmoid so the selection
-//   is bit-identical to the CPU oracle.
-__global__ void __launch_bounds__(256) grouped_sigmoid_kernel(
-    const float* __restrict__ logits, const float* __restrict__ bias, int M, int E, int n_group,
-    int topk_group, int k, int renorm, float scale, float* __restrict__ out_w,
-    int32_t* __restrict__ out_ids) {
+//   is bit-identical to the CPU oracle.  Group scores: the wave stages c in LDS
+//   and lane g scans group g.
+template <int PER>
+__global__ void __launch_bounds__(kRouteWaves * kWave) grouped_sigmoid_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int M, int E, int n_group, int topk_group,
+    int k, int renorm, float scale, float* __restrict__ out_w, int32_t* __restrict__ out_ids) {
+  __shared__ float s_c[kRouteWaves][PER * kWave];
   const int lane = lane_id();
-  const int tok = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const int wave = threadIdx.x / kWave;
+  const int tok = blockIdx.x * kRouteWaves + wave;
   if (tok >= M) return;
   const float* row = logits + static_cast<size_t>(tok) * E;
   const int per = E / n_group;
-  float c[kMaxPerLane];
+  float c[PER];
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int e = lane + j * kWave;
     if (e < E) {
       const float s = det_sigmoid(row[e]);
@@ -111,71 +113,47 @@ __global__ void __launch_bounds__(256) grouped_sigmoid_kernel(
       c[j] = -INFINITY;
     }
   }
+  uint64_t gmask = ~0ull;
   if (n_group > 1) {
-    // group g's score lands in lane g (n_group <= 64)
-    float gscore = -INFINITY;
-    for (int g = 0; g < n_group; ++g) {
-      float a1 = -INFINITY, a2 = -INFINITY;  // local top-2 of c in group g
 #pragma unroll
-      for (int j = 0; j < kMaxPerLane; ++j) {
-        const int e = lane + j * kWave;
-        if (e < E && e / per == g) {
-          const float x = c[j];
-          if (x > a1) {
-            a2 = a1;
-            a1 = x;
-          } else if (x > a2) {
-            a2 = x;
-          }
+    for (int j = 0; j < PER; ++j) s_c[wave][lane + j * kWave] = c[j];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float gscore = -INFINITY;
+    if (lane < n_group) {
+      float a1 = -INFINITY, a2 = -INFINITY;  // top-2 with duplicates kept
+      for (int i = 0; i < per; ++i) {
+        const float x = s_c[wave][lane * per + i];
+        if (x > a1) {
+          a2 = a1;
+          a1 = x;
+        } else if (x > a2) {
+          a2 = x;
         }
       }
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        const float b1 = __shfl_xor(a1, off, kWave);
-        const float b2 = __shfl_xor(a2, off, kWave);
-        const float n1 = fmaxf(a1, b1);
-        const float n2 = fmaxf(fminf(a1, b1), fmaxf(a2, b2));
-        a1 = n1;
-        a2 = n2;
-      }
-      if (lane == g) gscore = a1 + a2;
+      gscore = a1 + a2;
     }
-    uint64_t gmask = 0;
-    bool kept = false;
+    uint64_t gkey = (lane < n_group) ? pack_key(gscore, lane) : 0;
+    gmask = 0;
     for (int r = 0; r < topk_group; ++r) {
-      const uint64_t key = (lane < n_group && !kept) ? pack_key(gscore, lane) : 0;
-      const uint64_t best = wave_max_u64(key);
+      const uint64_t best = wave_max_u64(gkey);
       const int win = static_cast<int>(~static_cast<uint32_t>(best));
-      if (lane == win) kept = true;
+      if (lane == win) gkey = 0;
       gmask |= 1ull << win;
     }
-#pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
-      const int e = lane + j * kWave;
-      if (e < E && !((gmask >> (e / per)) & 1ull)) c[j] = -INFINITY;
-    }
   }
-  uint32_t taken = 0;
-  int my_idx = -1;
-  for (int r = 0; r < k; ++r) {
-    uint64_t best = 0;
+  uint64_t keys[PER];
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
-      const int e = lane + j * kWave;
-      if (e < E && !((taken >> j) & 1u)) {
-        const uint64_t key = pack_key(c[j], e);
-        best = key > best ? key : best;
-      }
-    }
-    best = wave_max_u64(best);
-    const int win = static_cast<int>(~static_cast<uint32_t>(best));
-    if ((win & (kWave - 1)) == lane) taken |= 1u << (win / kWave);
-    if (lane == r) my_idx = win;
+  for (int j = 0; j < PER; ++j) {
+    const int e = lane + j * kWave;
+    const bool kept = (gmask >> ((e < E ? e : 0) / per)) & 1ull;
+    keys[j] = (e < E) ? pack_key(kept ? c[j] : -INFINITY, e) : 0;
   }
+  const int my_idx = select_topk<PER>(keys, k);
   float w = (lane < k) ? det_sigmoid(row[my_idx]) : 0.0f;
   if (renorm) {
     float tot = 0.0f;  // sequential sum in rank order, as the oracle does
-    for (int r = 0; r < k; ++r) tot += __shfl(w, r, kWave);
+    for (int r = 0; r < k; ++r) tot += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(w), r));
     w = w / (tot + 1e-20f);
   }
   w = w * scale;
@@ -185,26 +163,45 @@ __global__ void __launch_bounds__(256) grouped_sigmoid_kernel(
   }
 }
 
-hipError_t launch_softmax_topk(const void* logits, int logits_bf16, int M, int E, int k, int renorm,
-                               float* w, int32_t* ids, hipStream_t stream) {
-  const int waves = 4;
-  dim3 grid((M + waves - 1) / waves), block(waves * kWave);
-  if (logits_bf16)
-    hipLaunchKernelGGL(softmax_topk_kernel<uint16_t>, grid, block, 0, stream,
+template <int PER>
+static void launch_softmax_per(const void* logits, int bf16, int M, int E, int k, int renorm, float* w, int32_t* ids,
+                               hipStream_t stream) {
+  dim3 grid((M + kRouteWaves - 1) / kRouteWaves), block(kRouteWaves * kWave);
+  if (bf16)
+    hipLaunchKernelGGL((softmax_topk_kernel<uint16_t, PER>), grid, block, 0, stream,
                        static_cast<const uint16_t*>(logits), M, E, k, renorm, w, ids);
   else
-    hipLaunchKernelGGL(softmax_topk_kernel<float>, grid, block, 0, stream,
-                       static_cast<const float*>(logits), M, E, k, renorm, w, ids);
+    hipLaunchKernelGGL((softmax_topk_kernel<float, PER>), grid, block, 0, stream, static_cast<const float*>(logits),
+                       M, E, k, renorm, w, ids);
+}
+
+hipError_t launch_softmax_topk(const void* logits, int logits_bf16, int M, int E, int k, int renorm, float* w,
+                               int32_t* ids, hipStream_t stream) {
+  const int per = (E + kWave - 1) / kWave;
+  if (per <= 1) launch_softmax_per<1>(logits, logits_bf16, M, E, k, renorm, w, ids, stream);
+  else if (per <= 2) launch_softmax_per<2>(logits, logits_bf16, M, E, k, renorm, w, ids, stream);
+  else if (per <= 4) launch_softmax_per<4>(logits, logits_bf16, M, E, k, renorm, w, ids, stream);
+  else if (per <= 8) launch_softmax_per<8>(logits, logits_bf16, M, E, k, renorm, w, ids, stream);
+  else launch_softmax_per<16>(logits, logits_bf16, M, E, k, renorm, w, ids, stream);
   return hipGetLastError();
 }
 
-hipError_t launch_grouped_sigmoid(const float* logits, const float* bias, int M, int E, int n_group,
-                                  int topk_group, int k, int renorm, float scale, float* w, int32_t* ids,
-                                  hipStream_t stream) {
-  const int waves = 4;
-  dim3 grid((M + waves - 1) / waves), block(waves * kWave);
-  hipLaunchKernelGGL(grouped_sigmoid_kernel, grid, block, 0, stream, logits, bias, M, E, n_group,
-                     topk_group, k, renorm, scale, w, ids);
+template <int PER>
+static void launch_grouped_per(const float* logits, const float* bias, int M, int E, int n_group, int topk_group,
+                               int k, int renorm, float scale, float* w, int32_t* ids, hipStream_t stream) {
+  dim3 grid((M + kRouteWaves - 1) / kRouteWaves), block(kRouteWaves * kWave);
+  hipLaunchKernelGGL((grouped_sigmoid_kernel<PER>), grid, block, 0, stream, logits, bias, M, E, n_group, topk_group,
+                     k, renorm, scale, w, ids);
+}
+
+hipError_t launch_grouped_sigmoid(const float* logits, const float* bias, int M, int E, int n_group, int topk_group,
+                                  int k, int renorm, float scale, float* w, int32_t* ids, hipStream_t stream) {
+  const int per = (E + kWave - 1) / kWave;
+  if (per <= 1) launch_grouped_per<1>(logits, bias, M, E, n_group, topk_group, k, renorm, scale, w, ids, stream);
+  else if (per <= 2) launch_grouped_per<2>(logits, bias, M, E, n_group, topk_group, k, renorm, scale, w, ids, stream);
+  else if (per <= 4) launch_grouped_per<4>(logits, bias, M, E, n_group, topk_group, k, renorm, scale, w, ids, stream);
+  else if (per <= 8) launch_grouped_per<8>(logits, bias, M, E, n_group, topk_group, k, renorm, scale, w, ids, stream);
+  else launch_grouped_per<16>(logits, bias, M, E, n_group, topk_group, k, renorm, scale, w, ids, stream);
   return hipGetLastError();
 }
 
