@@ -104,7 +104,7 @@ __global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
       }
       cnt[e] = acc;
       local += (acc + a.block_size - 1) / a.block_size * a.block_size;
-      local_seg += (e < a.num_experts && acc > 0) ? 1 : 0;
+      if (a.seg_expert && e < a.num_experts) local_seg += (acc + a.seg_cap - 1) / a.seg_cap;
     }
   }
   int total = 0, total_seg = 0;
@@ -116,11 +116,13 @@ __global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
       cum[e] = pre;
       if (a.cum_out) a.cum_out[e] = pre;
       const int c = cnt[e];
-      if (a.seg_expert && e < a.num_experts && c > 0) {
-        a.seg_expert[pre_seg] = e;
-        a.seg_start[pre_seg] = pre;
-        a.seg_count[pre_seg] = c;
-        ++pre_seg;
+      if (a.seg_expert && e < a.num_experts) {
+        for (int s0 = 0; s0 < c; s0 += a.seg_cap) {
+          a.seg_expert[pre_seg] = e;
+          a.seg_start[pre_seg] = pre + s0;
+          a.seg_count[pre_seg] = min(a.seg_cap, c - s0);
+          ++pre_seg;
+        }
       }
       pre += (c + a.block_size - 1) / a.block_size * a.block_size;
     }

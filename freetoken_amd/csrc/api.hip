@@ -83,9 +83,10 @@ DecodeLayout decode_layout(void* ws, int M, int k, const ftmoe_bank* bank, const
   L.sorted = c.take<int32_t>(numel);
   L.expert_ids = c.take<int32_t>(numel);
   L.ntpp = c.take<int32_t>(1);
-  L.seg_expert = c.take<int32_t>(bank->num_rows);
-  L.seg_start = c.take<int32_t>(bank->num_rows);
-  L.seg_count = c.take<int32_t>(bank->num_rows);
+  const int max_seg = ftmoe::decode_max_segments(numel, bank->num_rows);
+  L.seg_expert = c.take<int32_t>(max_seg);
+  L.seg_start = c.take<int32_t>(max_seg);
+  L.seg_count = c.take<int32_t>(max_seg);
   L.n_seg = c.take<int32_t>(1);
   L.act_stride = shared ? std::max(bank->inter, shared->inter) : bank->inter;
   L.act = c.take<uint16_t>(static_cast<size_t>(numel + M) * L.act_stride);
@@ -289,6 +290,20 @@ int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, c
   if (activation < FTMOE_ACT_SILU || activation > FTMOE_ACT_GELU_TANH)
     return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode: activation %d", activation);
   const DecodeLayout need = decode_layout(nullptr, M, top_k, bank, shared);
+  {
+    // the decode kernels address activations and one expert's matrices with
+    // 32-bit buffer offsets
+    const size_t lim = size_t{1} << 31;
+    const size_t act_bytes = static_cast<size_t>(M) * (top_k + 1) * need.act_stride * 2;
+    const size_t x_bytes = static_cast<size_t>(M) * bank->hidden * 2;
+    const auto mat_bytes = [](const ftmoe_bank* b) {
+      const size_t n = static_cast<size_t>(2) * b->inter * b->hidden;  // gate_up elements
+      return b->format == FTMOE_FMT_BF16 ? 2 * n : b->format == FTMOE_FMT_FP8_B128 ? n : n / 2;
+    };
+    if (act_bytes >= lim || x_bytes >= lim || mat_bytes(bank) >= lim || (shared && mat_bytes(shared) >= lim))
+      return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode: batch %d or expert size beyond the decode path's 2 GiB "
+                  "buffer ranges (use experts_prefill)", M);
+  }
   if (!workspace || workspace_bytes < need.bytes)
     return fail(FTMOE_ERR_WORKSPACE, "experts_decode: workspace %zu < %zu bytes", workspace_bytes, need.bytes);
   const DecodeLayout L = decode_layout(workspace, M, top_k, bank, shared);
@@ -307,6 +322,7 @@ int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, c
   al.seg_start = L.seg_start;
   al.seg_count = L.seg_count;
   al.n_seg = L.n_seg;
+  al.seg_cap = ftmoe::kDecodeSegCap;
   g_timer.start_call(stream);
   rc = check_hip(ftmoe::launch_align(al, stream), "experts_decode align");
   if (rc) return rc;
@@ -325,7 +341,8 @@ int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, c
   d.H = bank->hidden;
   d.I = bank->inter;
   d.Is = shared ? shared->inter : 0;
-  d.max_seg = std::min(numel, bank->num_rows);
+  d.max_seg = ftmoe::decode_max_segments(numel, bank->num_rows);
+  d.seg_cap = ftmoe::kDecodeSegCap;
   d.gate_up = {static_cast<const uint8_t*>(bank->gate_up), bank->gate_up_scale};
   d.down = {static_cast<const uint8_t*>(bank->down), bank->down_scale};
   if (shared) {

@@ -58,18 +58,36 @@ struct RawA<FMT_MXFP4> {
   uint32_t code;
 };
 
+// Buffer loads: weights and activations are read through buffer descriptors
+// (base in SGPRs, 32-bit lane offsets, the K-block offset in soffset).  A lane
+// whose offset is kOutOfRange reads zeros without touching memory.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+constexpr int kBufDword3 = 0x00020000;  // gfx9 raw-buffer descriptor word 3
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufDword3);
+}
+
+__device__ __forceinline__ u32x4 buf_x4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// Weight bytes of one lane for K block kb: the lane's row starts at voff
+// (row * row_bytes + the lane group's 32-value slice); the K block adds
+// kb * 128 values.
 template <int FMT>
-__device__ __forceinline__ void load_raw(const uint8_t* row, const uint8_t* srow, int kb, int g, RawA<FMT>& r) {
+__device__ __forceinline__ void load_raw(__amdgpu_buffer_rsrc_t wr, uint32_t voff, const uint8_t* srow, int kb, int g,
+                                         RawA<FMT>& r) {
   if constexpr (FMT == FMT_BF16) {
-    const bf16x8* p = reinterpret_cast<const bf16x8*>(row + (static_cast<size_t>(kb) * 128 + g * 32) * 2);
+    const uint32_t so = static_cast<uint32_t>(kb) * 256;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r.v[j] = p[j];
+    for (int j = 0; j < 4; ++j) r.v[j] = __builtin_bit_cast(bf16x8, buf_x4(wr, voff + 16 * j, so));
   } else if constexpr (FMT == FMT_FP8) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(row + static_cast<size_t>(kb) * 128 + g * 32);
-    r.v[0] = p[0];
-    r.v[1] = p[1];
+    const uint32_t so = static_cast<uint32_t>(kb) * 128;
+    r.v[0] = buf_x4(wr, voff, so);
+    r.v[1] = buf_x4(wr, voff + 16, so);
   } else {
-    r.v[0] = *reinterpret_cast<const u32x4*>(row + (static_cast<size_t>(kb) * 128 + g * 32) / 2);
+    r.v[0] = buf_x4(wr, voff, static_cast<uint32_t>(kb) * 64);
     r.code = srow[kb * 4 + g];
   }
 }
@@ -111,22 +129,20 @@ struct KStage {
   u32x4 b[NCH][4];
 };
 
-// Lanes whose route column lies past the segment's end skip their activation
-// loads and supply zeros (MFMA output column c depends on B column c only, and
-// those columns are never stored).
+// Lanes whose route column lies past the segment's end carry kOutOfRange and
+// read zeros (MFMA output column c depends on B column c only, and those
+// columns are never stored).
 template <int FMT, int NMAT, int NCH>
-__device__ __forceinline__ void load_stage(KStage<FMT, NMAT, NCH>& st, const uint8_t* const (&rows)[NMAT],
-                                           const uint8_t* const (&srows)[NMAT], const uint16_t* const* brow,
-                                           const bool (&bvalid)[NCH], int kb, int g) {
+__device__ __forceinline__ void load_stage(KStage<FMT, NMAT, NCH>& st, __amdgpu_buffer_rsrc_t wr,
+                                           const uint32_t (&wvoff)[NMAT], const uint8_t* const (&srows)[NMAT],
+                                           __amdgpu_buffer_rsrc_t br, const uint32_t (&bvoff)[NCH], int kb, int g) {
 #pragma unroll
-  for (int m = 0; m < NMAT; ++m) load_raw<FMT>(rows[m], srows[m], kb, g, st.w[m]);
+  for (int m = 0; m < NMAT; ++m) load_raw<FMT>(wr, wvoff[m], srows[m], kb, g, st.w[m]);
+  const uint32_t so = static_cast<uint32_t>(kb) * 256;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(brow[c] + static_cast<size_t>(kb) * 128 + g * 32);
-    const u32x4 zero = {0u, 0u, 0u, 0u};
+  for (int c = 0; c < NCH; ++c)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) st.b[c][j] = bvalid[c] ? p[j] : zero;
-  }
+    for (int j = 0; j < 4; ++j) st.b[c][j] = buf_x4(br, bvoff[c] + 16 * j, so);
 }
 
 template <int FMT, int NMAT, int NCH>
@@ -160,206 +176,244 @@ __device__ __forceinline__ void compute_stage(const KStage<FMT, NMAT, NCH>& st, 
   }
 }
 
-// Accumulates NMAT 16-row weight tiles against NCH route chunks of 16.  Wave w
-// owns the contiguous K blocks [w*nkb/4, (w+1)*nkb/4) and keeps the loads of
-// the next K block in flight while it computes the current one.
-template <int FMT, int NMAT, int NCH>
-__device__ __forceinline__ void gemv_tile(const uint8_t* const (&rows)[NMAT], const uint8_t* const (&srows)[NMAT],
-                                          const float* const (&fscale)[NMAT], int K, const uint16_t* const* brow,
-                                          const bool (&bvalid)[NCH], f32x4 (&acc)[NMAT][NCH]) {
+// Accumulates NMAT 16-row weight tiles against NCH route chunks of 16 over the
+// K blocks [kw*nkb/KS, (kw+1)*nkb/KS) (contiguous per wave), keeping the loads
+// of the next K block in flight while the current one is computed.
+template <int FMT, int NMAT, int NCH, int KS>
+__device__ __forceinline__ void gemv_tile(__amdgpu_buffer_rsrc_t wr, const uint32_t (&wvoff)[NMAT],
+                                          const uint8_t* const (&srows)[NMAT], const float* const (&fscale)[NMAT],
+                                          int K, int kw, __amdgpu_buffer_rsrc_t br, const uint32_t (&bvoff)[NCH],
+                                          f32x4 (&acc)[NMAT][NCH]) {
   const int g = lane_id() >> 4;
-  const int wave = threadIdx.x / kWave;
   const int nkb = K / 128;
-  const int kb_lo = wave * nkb / kDecWaves, kb_hi = (wave + 1) * nkb / kDecWaves;
+  const int kb_lo = kw * nkb / KS, kb_hi = (kw + 1) * nkb / KS;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int m = 0; m < NMAT; ++m)
 #pragma unroll
     for (int c = 0; c < NCH; ++c) acc[m][c] = zero;
   KStage<FMT, NMAT, NCH> s0, s1;
-  if (kb_lo < kb_hi) load_stage(s0, rows, srows, brow, bvalid, kb_lo, g);
+  if (kb_lo < kb_hi) load_stage(s0, wr, wvoff, srows, br, bvoff, kb_lo, g);
   for (int kb = kb_lo; kb < kb_hi; kb += 2) {
-    if (kb + 1 < kb_hi) load_stage(s1, rows, srows, brow, bvalid, kb + 1, g);
+    if (kb + 1 < kb_hi) load_stage(s1, wr, wvoff, srows, br, bvoff, kb + 1, g);
     compute_stage(s0, fscale, kb, acc);
     if (kb + 1 < kb_hi) {
-      if (kb + 2 < kb_hi) load_stage(s0, rows, srows, brow, bvalid, kb + 2, g);
+      if (kb + 2 < kb_hi) load_stage(s0, wr, wvoff, srows, br, bvoff, kb + 2, g);
       compute_stage(s1, fscale, kb + 1, acc);
     }
   }
 }
 
-// One pass over up to NCH chunks (16 routes each) of a segment for a workgroup
-// tile of RT 16-row tiles per matrix, including the split-K reduction and the
-// epilogue.  LDS: red[waves][NMAT][NCH][64] float4.
-template <int FMT, int STAGE, int RT, int NCH>
-__device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView& bank, bool shared, int expert,
-                                            int start, int count, int base, int row0, int inter, f32x4* red) {
+// Where a segment's column lives.  Routed segments: column col is route
+// sorted[start + col]; shared pieces: column col is token start + col.
+struct SegView {
+  bool shared;
+  int expert, start, count;
+};
+
+// Epilogue of one 16-row output tile for one lane (4 consecutive rows
+// rows_at..rows_at+3, column col < count).  Stage 0: g, u are the gate and up
+// sums; stage 1: g is the down sum (u unused).
+template <int STAGE>
+__device__ __forceinline__ void tile_epilogue(const DecodeArgs& a, const SegView& sv, int col, int rows_at, f32x4 g,
+                                              f32x4 u) {
+  uint16_t o[4];
+  uint16_t* dst;
+  if constexpr (STAGE == 0) {
+    const int route = sv.shared ? -1 : a.sorted[sv.start + col];
+    const float win = (!sv.shared && a.weight_on_input) ? a.topk_w[route] : 1.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float gg = bf16_round(g[v] * win);
+      const float uu = bf16_round(u[v] * win);
+      o[v] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
+    }
+    const int arow = sv.shared ? a.M * a.k + sv.start + col : route;
+    dst = a.act + static_cast<size_t>(arow) * a.act_stride + rows_at;
+  } else {
+    float wt = 1.0f;
+    if (sv.shared) {
+      dst = a.sh_out + static_cast<size_t>(sv.start + col) * a.H + rows_at;
+    } else {
+      const int route = a.sorted[sv.start + col];
+      if (!a.weight_on_input) wt = a.topk_w[route];
+      dst = a.ic3 + static_cast<size_t>(route) * a.H + rows_at;
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(g[v] * wt);
+  }
+  uint2 pk;
+  pk.x = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
+  pk.y = static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16);
+  *reinterpret_cast<uint2*>(dst) = pk;
+}
+
+// One pass over up to NCH chunks (16 columns each) of a segment.  The 4 waves
+// of the workgroup form 4/KS row groups of KS waves; a row group covers RT
+// 16-row tiles per matrix (gate and up tiles in stage 0) and its KS waves split
+// K.  With KS > 1 the partial sums meet in LDS (red[4][NMAT][NCH][64] float4)
+// and are added in fixed wave order, so results do not depend on timing.
+template <int FMT, int STAGE, int RT, int KS, int NCH>
+__device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView& bank, const SegView& sv, int base,
+                                            int row0, int inter, f32x4* red) {
   constexpr int NMAT = STAGE == 0 ? 2 * RT : RT;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
+  const int kw = wave % KS, rg = wave / KS;
   const int r16 = lane & 15, g = lane >> 4;
   const int N = STAGE == 0 ? 2 * inter : a.H;
   const int K = STAGE == 0 ? a.H : inter;
-  const int nch = min(NCH, (count - base + 15) / 16);
+  const int nch = min(NCH, (sv.count - base + 15) / 16);
+  const int wrow0 = row0 + rg * 16 * RT;
 
-  const uint16_t* brow[NCH];
-  bool bvalid[NCH];
+  // activation rows: x (stage 0) or the act buffer (stage 1)
+  const uint16_t* bbase = STAGE == 0 ? a.x : a.act;
+  const uint32_t brows = STAGE == 0 ? static_cast<uint32_t>(a.M)
+                                    : static_cast<uint32_t>(a.M * a.k + (a.sh_out ? a.M : 0));
+  const uint32_t bstride = STAGE == 0 ? static_cast<uint32_t>(a.H) : static_cast<uint32_t>(a.act_stride);
+  const __amdgpu_buffer_rsrc_t br = make_rsrc(bbase, brows * bstride * 2);
+  uint32_t bvoff[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    bvalid[c] = base + c * 16 + r16 < count;
-    const int col = min(base + c * 16 + r16, count - 1);
-    if (STAGE == 0) {
-      const int tok = shared ? col : a.sorted[start + col] / a.k;
-      brow[c] = a.x + static_cast<size_t>(tok) * a.H;
+    const int col = base + c * 16 + r16;
+    if (col < sv.count) {
+      int row;
+      if (STAGE == 0) row = sv.shared ? sv.start + col : a.sorted[sv.start + col] / a.k;
+      else row = sv.shared ? a.M * a.k + sv.start + col : a.sorted[sv.start + col];
+      bvoff[c] = static_cast<uint32_t>(row) * bstride * 2 + g * 64;
     } else {
-      const int arow = shared ? a.M * a.k + col : a.sorted[start + col];
-      brow[c] = a.act + static_cast<size_t>(arow) * a.act_stride;
+      bvoff[c] = kOutOfRange;
     }
   }
-  const size_t rb = row_bytes<FMT>(K);
-  const uint8_t* wexp = bank.w + static_cast<size_t>(expert) * N * rb;
-  const uint8_t* rows[NMAT];
+  const uint32_t rb = static_cast<uint32_t>(row_bytes<FMT>(K));
+  const __amdgpu_buffer_rsrc_t wr =
+      make_rsrc(bank.w + static_cast<size_t>(sv.expert) * N * rb, static_cast<uint32_t>(N) * rb);
+  const uint32_t gbytes = FMT == FMT_BF16 ? 64 : FMT == FMT_FP8 ? 32 : 16;  // a lane group's 32 values
+  uint32_t wvoff[NMAT];
   const uint8_t* srows[NMAT];
   const float* fscale[NMAT];
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) {
-    // matrix m: gate tiles first, then up tiles (stage 0); down tiles (stage 1)
-    const int tile_row = (STAGE == 0 && m >= RT) ? inter + row0 + 16 * (m - RT) : row0 + 16 * m;
+    // matrix m: gate tiles then up tiles (stage 0); down tiles (stage 1)
+    const int tile_row = (STAGE == 0 && m >= RT) ? inter + wrow0 + 16 * (m - RT) : wrow0 + 16 * m;
     const int ridx = tile_row + r16;
-    rows[m] = wexp + static_cast<size_t>(ridx) * rb;
+    wvoff[m] = static_cast<uint32_t>(ridx) * rb + g * gbytes;
     if constexpr (FMT == FMT_MXFP4) {
-      srows[m] = static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(expert) * N + ridx) * (K / 32);
+      srows[m] = static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(sv.expert) * N + ridx) * (K / 32);
     } else {
       srows[m] = nullptr;
     }
     if constexpr (FMT == FMT_FP8) {
-      // the 16-row tile sits inside one 128-row scale block
+      // a 16-row tile lies inside one 128-row scale block
       fscale[m] = static_cast<const float*>(bank.s) +
-                  (static_cast<size_t>(expert) * (N / 128) + tile_row / 128) * (K / 128);
+                  (static_cast<size_t>(sv.expert) * (N / 128) + tile_row / 128) * (K / 128);
     } else {
       fscale[m] = nullptr;
     }
   }
   f32x4 acc[NMAT][NCH];
-  gemv_tile<FMT, NMAT, NCH>(rows, srows, fscale, K, brow, bvalid, acc);
+  gemv_tile<FMT, NMAT, NCH, KS>(wr, wvoff, srows, fscale, K, kw, br, bvoff, acc);
 
-  // split-K reduction in fixed wave order
+  if constexpr (KS == 1) {
 #pragma unroll
-  for (int m = 0; m < NMAT; ++m)
+    for (int t = 0; t < RT; ++t)
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
-      if (c < nch) red[((wave * NMAT + m) * NCH + c) * kWave + lane] = acc[m][c];
-  __syncthreads();
-  // wave w finishes (output tile, chunk) items w, w+4, ...
-  for (int item = wave; item < RT * nch; item += kDecWaves) {
-    const int t = item / nch, c = item % nch;
-    const int col = base + c * 16 + r16;
-    const int mg = t, mu = STAGE == 0 ? RT + t : t;  // gate / up matrices (down: mg == mu)
-    f32x4 sg = red[((0 * NMAT + mg) * NCH + c) * kWave + lane];
-    f32x4 su = red[((0 * NMAT + mu) * NCH + c) * kWave + lane];
-#pragma unroll
-    for (int v = 1; v < kDecWaves; ++v) {
-      sg += red[((v * NMAT + mg) * NCH + c) * kWave + lane];
-      if (STAGE == 0) su += red[((v * NMAT + mu) * NCH + c) * kWave + lane];
-    }
-    if (col >= count) continue;
-    const int rows_at = row0 + 16 * t + g * 4;  // this lane's 4 consecutive output rows
-    uint16_t o[4];
-    if (STAGE == 0) {
-      const int route = shared ? -1 : a.sorted[start + col];
-      const float win = (!shared && a.weight_on_input) ? a.topk_w[route] : 1.0f;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float gg = bf16_round(sg[v] * win);
-        const float uu = bf16_round(su[v] * win);
-        o[v] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
+      for (int c = 0; c < NCH; ++c) {
+        const int col = base + c * 16 + r16;
+        if (c < nch && col < sv.count)
+          tile_epilogue<STAGE>(a, sv, col, wrow0 + 16 * t + g * 4, acc[t][c], acc[STAGE == 0 ? RT + t : t][c]);
       }
-      const int arow = shared ? a.M * a.k + col : route;
-      uint2 pk;
-      pk.x = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
-      pk.y = static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16);
-      *reinterpret_cast<uint2*>(a.act + static_cast<size_t>(arow) * a.act_stride + rows_at) = pk;
-    } else {
-      uint16_t* dst;
-      float wt = 1.0f;
-      if (shared) {
-        dst = a.sh_out + static_cast<size_t>(col) * a.H + rows_at;
-      } else {
-        const int route = a.sorted[start + col];
-        if (!a.weight_on_input) wt = a.topk_w[route];
-        dst = a.ic3 + static_cast<size_t>(route) * a.H + rows_at;
-      }
+  } else {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(sg[v] * wt);
-      uint2 pk;
-      pk.x = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
-      pk.y = static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16);
-      *reinterpret_cast<uint2*>(dst) = pk;
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        if (c < nch) red[((wave * NMAT + m) * NCH + c) * kWave + lane] = acc[m][c];
+    __syncthreads();
+    // the KS waves of a row group finish its (tile, chunk) items round robin
+    for (int item = kw; item < RT * nch; item += KS) {
+      const int t = item / nch, c = item % nch;
+      const int col = base + c * 16 + r16;
+      const int mg = t, mu = STAGE == 0 ? RT + t : t;
+      const int w0 = rg * KS;
+      f32x4 sg = red[((w0 * NMAT + mg) * NCH + c) * kWave + lane];
+      f32x4 su = red[((w0 * NMAT + mu) * NCH + c) * kWave + lane];
+#pragma unroll
+      for (int v = 1; v < KS; ++v) {
+        sg += red[(((w0 + v) * NMAT + mg) * NCH + c) * kWave + lane];
+        if (STAGE == 0) su += red[(((w0 + v) * NMAT + mu) * NCH + c) * kWave + lane];
+      }
+      if (col < sv.count) tile_epilogue<STAGE>(a, sv, col, wrow0 + 16 * t + g * 4, sg, su);
     }
+    __syncthreads();
   }
-  __syncthreads();
 }
-
-constexpr int kRedFloats4 = kDecWaves * 4 * kWave;  // NMAT * chunks_per_pass <= 4
 
 // Route chunks (of 16) per pass, sized so that two K stages of weights and
-// activations plus the accumulators fit the 256 registers of a wave at
-// occupancy 2: stage 0 holds gate and up tiles, stage 1 only down tiles.
-template <int STAGE, int RT>
+// activations plus the accumulators fit 256 registers per lane (occupancy 2).
+template <int FMT, int STAGE, int RT>
 constexpr int chunks_per_pass() {
-  return STAGE == 0 ? (RT == 1 ? 2 : 1) : (RT == 1 ? 4 : 2);
+  if constexpr (STAGE == 0) return RT == 1 ? 2 : (FMT == FMT_BF16 ? 1 : 2);
+  return RT == 1 ? 2 : 2;
 }
 
-template <int FMT, int STAGE, int RT>
-__device__ __forceinline__ void decode_segment(const DecodeArgs& a, const BankView& bank, bool shared, int expert,
-                                               int start, int count, int row0, int inter, f32x4* red) {
-  constexpr int CMAX = chunks_per_pass<STAGE, RT>();
-  for (int base = 0; base < count; base += 16 * CMAX) {
-    const int nch = min(CMAX, (count - base + 15) / 16);
+template <int FMT, int STAGE, int RT, int KS>
+__device__ __forceinline__ void decode_segment(const DecodeArgs& a, const BankView& bank, const SegView& sv, int row0,
+                                               int inter, f32x4* red) {
+  constexpr int CMAX = chunks_per_pass<FMT, STAGE, RT>();
+  for (int base = 0; base < sv.count; base += 16 * CMAX) {
     if constexpr (CMAX == 1) {
-      decode_pass<FMT, STAGE, RT, 1>(a, bank, shared, expert, start, count, base, row0, inter, red);
-    } else if constexpr (CMAX == 2) {
-      if (nch == 1) decode_pass<FMT, STAGE, RT, 1>(a, bank, shared, expert, start, count, base, row0, inter, red);
-      else decode_pass<FMT, STAGE, RT, 2>(a, bank, shared, expert, start, count, base, row0, inter, red);
+      decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, red);
     } else {
-      if (nch == 1) decode_pass<FMT, STAGE, RT, 1>(a, bank, shared, expert, start, count, base, row0, inter, red);
-      else if (nch == 2) decode_pass<FMT, STAGE, RT, 2>(a, bank, shared, expert, start, count, base, row0, inter, red);
-      else decode_pass<FMT, STAGE, RT, 4>(a, bank, shared, expert, start, count, base, row0, inter, red);
+      if (sv.count - base <= 16) decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, red);
+      else decode_pass<FMT, STAGE, RT, KS, 2>(a, bank, sv, base, row0, inter, red);
     }
   }
 }
 
-template <int FMT_R, int FMT_S, int STAGE, int RT>
-__global__ void __launch_bounds__(kDecWaves * kWave) decode_stage_kernel(DecodeArgs a) {
-  __shared__ f32x4 red[kRedFloats4];
+constexpr int kRedFloats4 = kDecWaves * 8 * kWave;  // NMAT * chunks_per_pass <= 8
+
+// Grid: x = row blocks of (4/KS) * RT * 16 rows, y = routed segments
+// (max_seg, the tail beyond n_seg exits) followed by the shared expert's token
+// pieces of seg_cap tokens.
+template <int FMT_R, int FMT_S, int STAGE, int RT, int KS>
+__global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) decode_stage_kernel(DecodeArgs a) {
+  __shared__ f32x4 red[KS > 1 ? kRedFloats4 : 1];
   const int seg = blockIdx.y;
-  const bool shared = seg == a.max_seg;
-  if (!shared && seg >= a.n_seg[0]) return;
-  const int inter = shared ? a.Is : a.I;
-  const int row0 = blockIdx.x * 16 * RT;
+  SegView sv;
+  sv.shared = seg >= a.max_seg;
+  if (sv.shared) {
+    sv.expert = 0;
+    sv.start = (seg - a.max_seg) * a.seg_cap;
+    sv.count = min(a.seg_cap, a.M - sv.start);
+  } else {
+    if (seg >= a.n_seg[0]) return;
+    sv.expert = a.seg_expert[seg];
+    sv.start = a.seg_start[seg];
+    sv.count = a.seg_count[seg];
+  }
+  const int inter = sv.shared ? a.Is : a.I;
+  const int row0 = blockIdx.x * (kDecWaves / KS) * RT * 16;
   if (STAGE == 0 && row0 >= inter) return;
-  const int count = shared ? a.M : a.seg_count[seg];
-  const int start = shared ? 0 : a.seg_start[seg];
-  const int expert = shared ? 0 : a.seg_expert[seg];
   // field-wise selects keep the kernel argument block out of private memory
   BankView bank;
   if constexpr (STAGE == 0) {
-    bank.w = shared ? a.sh_gate_up.w : a.gate_up.w;
-    bank.s = shared ? a.sh_gate_up.s : a.gate_up.s;
+    bank.w = sv.shared ? a.sh_gate_up.w : a.gate_up.w;
+    bank.s = sv.shared ? a.sh_gate_up.s : a.gate_up.s;
   } else {
-    bank.w = shared ? a.sh_down.w : a.down.w;
-    bank.s = shared ? a.sh_down.s : a.down.s;
+    bank.w = sv.shared ? a.sh_down.w : a.down.w;
+    bank.s = sv.shared ? a.sh_down.s : a.down.s;
   }
-  const int fmt = shared ? FMT_S : FMT_R;
+  const int fmt = sv.shared ? FMT_S : FMT_R;
   if (fmt == FMT_BF16) {
     if constexpr (FMT_R == FMT_BF16 || FMT_S == FMT_BF16)
-      decode_segment<FMT_BF16, STAGE, RT>(a, bank, shared, expert, start, count, row0, inter, red);
+      decode_segment<FMT_BF16, STAGE, RT, KS>(a, bank, sv, row0, inter, red);
   } else if (fmt == FMT_FP8) {
     if constexpr (FMT_R == FMT_FP8 || FMT_S == FMT_FP8)
-      decode_segment<FMT_FP8, STAGE, RT>(a, bank, shared, expert, start, count, row0, inter, red);
+      decode_segment<FMT_FP8, STAGE, RT, KS>(a, bank, sv, row0, inter, red);
   } else {
     if constexpr (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4)
-      decode_segment<FMT_MXFP4, STAGE, RT>(a, bank, shared, expert, start, count, row0, inter, red);
+      decode_segment<FMT_MXFP4, STAGE, RT, KS>(a, bank, sv, row0, inter, red);
   }
 }
 
@@ -418,26 +472,28 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
   *reinterpret_cast<uint4*>(y + static_cast<size_t>(t) * H + h) = out;
 }
 
+// Launch shapes.  Stage 0 (K = hidden, long rows): the 4 waves split K and a
+// workgroup covers RT tiles of gate and of up.  Stage 1 (K = intermediate,
+// short rows): each wave owns RT whole tiles.  Two tiles per wave are used when
+// the grid still has at least kMinWgs workgroups; they halve the activation
+// loads per weight byte.
+constexpr int kMinWgs = 1024;
+
 template <int FR, int FS>
 static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared, hipStream_t stream) {
-  const int gy = a.max_seg + (has_shared ? 1 : 0);
+  const int gy = a.max_seg + (has_shared ? (a.M + a.seg_cap - 1) / a.seg_cap : 0);
   const int imax = has_shared ? max(a.I, a.Is) : a.I;
   const dim3 block(kDecWaves * kWave);
-  // two 16-row tiles per workgroup once the grid has enough workgroups to fill
-  // the chip twice over; they halve the activation loads per weight byte
-  constexpr int kMinWgs = 2048;
   if (stage == 0) {
-    const bool rt2 = (imax % 32 == 0) && a.I % 32 == 0 && (a.Is % 32 == 0) && (imax / 32) * gy >= kMinWgs;
-    if (rt2)
-      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 0, 2>), dim3(imax / 32, gy), block, 0, stream, a);
+    if ((imax / 32) * gy >= kMinWgs)
+      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 0, 2, 4>), dim3((imax + 31) / 32, gy), block, 0, stream, a);
     else
-      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 0, 1>), dim3(imax / 16, gy), block, 0, stream, a);
+      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 0, 1, 4>), dim3((imax + 15) / 16, gy), block, 0, stream, a);
   } else {
-    const bool rt2 = (a.H % 32 == 0) && (a.H / 32) * gy >= kMinWgs;
-    if (rt2)
-      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 1, 2>), dim3(a.H / 32, gy), block, 0, stream, a);
+    if ((a.H / 128) * gy >= kMinWgs)
+      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 1, 2, 1>), dim3(a.H / 128, gy), block, 0, stream, a);
     else
-      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 1, 1>), dim3(a.H / 16, gy), block, 0, stream, a);
+      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 1, 1, 1>), dim3(a.H / 64, gy), block, 0, stream, a);
   }
   return hipGetLastError();
 }

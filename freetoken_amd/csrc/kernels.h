@@ -22,10 +22,11 @@ struct AlignArgs {
   int32_t* expert_ids;         // [max_blocks]
   int max_blocks;
   int32_t* ntpp;               // [1]
-  int32_t* seg_expert;         // nullable: [num_experts] compact segments
-  int32_t* seg_start;
-  int32_t* seg_count;
+  int32_t* seg_expert;         // nullable: compact segments (an expert's routes in
+  int32_t* seg_start;          //   pieces of at most seg_cap; at most
+  int32_t* seg_count;          //   min(numel, num_experts + numel / seg_cap) of them)
   int32_t* n_seg;              // [1]
+  int seg_cap;                 // > 0 when segments are requested
   int32_t* cum_out;            // nullable: [num_experts + 2] padded region starts
 };
 
@@ -33,6 +34,15 @@ struct BankView {
   const uint8_t* w;  // weights, [S, N, K] elements of the format
   const void* s;     // fp8: float [S, N/128, K/128]; mxfp4: uint8 [S, N, K/32]; bf16: null
 };
+
+// Decode segments hold at most this many routes: one workgroup covers a whole
+// segment in one pass over its weight rows.
+constexpr int kDecodeSegCap = 32;
+
+inline int decode_max_segments(int numel, int num_experts) {
+  const int bound = num_experts + numel / kDecodeSegCap;
+  return numel < bound ? numel : bound;
+}
 
 struct DecodeArgs {
   const uint16_t* x;        // [M, H] bf16
@@ -43,7 +53,8 @@ struct DecodeArgs {
   const int32_t* seg_count;
   const int32_t* n_seg;
   int M, k, H, I, Is;       // Is: shared expert intermediate size (0: none)
-  int max_seg;              // routed segments of the grid (the shared one follows)
+  int max_seg;              // routed segments of the grid (the shared expert's pieces follow)
+  int seg_cap;              // routes per segment at most (also the shared expert's token pieces)
   BankView gate_up, down;   // routed bank
   BankView sh_gate_up, sh_down;
   uint16_t* act;            // [M*k + M, act_stride] bf16

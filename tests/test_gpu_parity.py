@@ -143,8 +143,10 @@ def _decode_case(name, fmt, rows, H, I, k, sfmt, sI, M, seed=0):
 
 
 @pytest.mark.parametrize("case", DECODE_CASES, ids=[c[0] for c in DECODE_CASES])
-@pytest.mark.parametrize("M", [1, 4, 33, 64])
+@pytest.mark.parametrize("M", [1, 4, 33, 64, 160])
 def test_decode_parity(dev, case, M):
+    """M = 64 and 160 put 25-80 routes on every expert: segments are cut into
+    pieces of at most 32 routes and the shared expert into pieces of 32 tokens."""
     name, fmt, rows, H, I, k, sfmt, sI = case
     bank, shared, x, w, ids = _decode_case(*case, M)
     y_ref = oracle.experts.moe_layer("decode", x, w, ids, bank, shared)
