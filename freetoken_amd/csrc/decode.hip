@@ -127,17 +127,35 @@ template <int FMT, int NMAT, int NCH>
 struct KStage {
   RawA<FMT> w[NMAT];
   u32x4 b[NCH][4];
+  float sc[NMAT];  // FP8: the 128x128 block scale of each tile for this K block
 };
 
 // Lanes whose route column lies past the segment's end carry kOutOfRange and
 // read zeros (MFMA output column c depends on B column c only, and those
 // columns are never stored).
+// Weight-side addressing of one wave: the expert's matrix (wr), each tile's
+// lane offset (wvoff), and the scales (FP8: scale array sr with each tile's
+// scale row at soff; MXFP4: the lane's row of e8m0 codes).
+template <int NMAT>
+struct WTiles {
+  __amdgpu_buffer_rsrc_t wr, sr;
+  uint32_t wvoff[NMAT];
+  uint32_t soff[NMAT];
+  const uint8_t* srows[NMAT];
+};
+
 template <int FMT, int NMAT, int NCH>
-__device__ __forceinline__ void load_stage(KStage<FMT, NMAT, NCH>& st, __amdgpu_buffer_rsrc_t wr,
-                                           const uint32_t (&wvoff)[NMAT], const uint8_t* const (&srows)[NMAT],
+__device__ __forceinline__ void load_stage(KStage<FMT, NMAT, NCH>& st, const WTiles<NMAT>& wt,
                                            __amdgpu_buffer_rsrc_t br, const uint32_t (&bvoff)[NCH], int kb, int g) {
 #pragma unroll
-  for (int m = 0; m < NMAT; ++m) load_raw<FMT>(wr, wvoff[m], srows[m], kb, g, st.w[m]);
+  for (int m = 0; m < NMAT; ++m) load_raw<FMT>(wt.wr, wt.wvoff[m], wt.srows[m], kb, g, st.w[m]);
+  if constexpr (FMT == FMT_FP8) {
+    // wave-uniform address: one request per tile, in flight with the weights
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+      st.sc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wt.sr, wt.soff[m],
+                                                                                static_cast<uint32_t>(kb) * 4, 0));
+  }
   const uint32_t so = static_cast<uint32_t>(kb) * 256;
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
@@ -146,8 +164,7 @@ __device__ __forceinline__ void load_stage(KStage<FMT, NMAT, NCH>& st, __amdgpu_
 }
 
 template <int FMT, int NMAT, int NCH>
-__device__ __forceinline__ void compute_stage(const KStage<FMT, NMAT, NCH>& st, const float* const (&fscale)[NMAT],
-                                              int kb, f32x4 (&acc)[NMAT][NCH]) {
+__device__ __forceinline__ void compute_stage(const KStage<FMT, NMAT, NCH>& st, f32x4 (&acc)[NMAT][NCH]) {
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) {
@@ -165,7 +182,7 @@ __device__ __forceinline__ void compute_stage(const KStage<FMT, NMAT, NCH>& st, 
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j], __builtin_bit_cast(bf16x8, st.b[c][j]), t, 0, 0, 0);
-        acc[m][c] += t * fscale[m][kb];
+        acc[m][c] += t * st.sc[m];
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -180,10 +197,8 @@ __device__ __forceinline__ void compute_stage(const KStage<FMT, NMAT, NCH>& st, 
 // K blocks [kw*nkb/KS, (kw+1)*nkb/KS) (contiguous per wave), keeping the loads
 // of the next K block in flight while the current one is computed.
 template <int FMT, int NMAT, int NCH, int KS>
-__device__ __forceinline__ void gemv_tile(__amdgpu_buffer_rsrc_t wr, const uint32_t (&wvoff)[NMAT],
-                                          const uint8_t* const (&srows)[NMAT], const float* const (&fscale)[NMAT],
-                                          int K, int kw, __amdgpu_buffer_rsrc_t br, const uint32_t (&bvoff)[NCH],
-                                          f32x4 (&acc)[NMAT][NCH]) {
+__device__ __forceinline__ void gemv_tile(const WTiles<NMAT>& wt, int K, int kw, __amdgpu_buffer_rsrc_t br,
+                                          const uint32_t (&bvoff)[NCH], f32x4 (&acc)[NMAT][NCH]) {
   const int g = lane_id() >> 4;
   const int nkb = K / 128;
   const int kb_lo = kw * nkb / KS, kb_hi = (kw + 1) * nkb / KS;
@@ -193,13 +208,13 @@ __device__ __forceinline__ void gemv_tile(__amdgpu_buffer_rsrc_t wr, const uint3
 #pragma unroll
     for (int c = 0; c < NCH; ++c) acc[m][c] = zero;
   KStage<FMT, NMAT, NCH> s0, s1;
-  if (kb_lo < kb_hi) load_stage(s0, wr, wvoff, srows, br, bvoff, kb_lo, g);
+  if (kb_lo < kb_hi) load_stage(s0, wt, br, bvoff, kb_lo, g);
   for (int kb = kb_lo; kb < kb_hi; kb += 2) {
-    if (kb + 1 < kb_hi) load_stage(s1, wr, wvoff, srows, br, bvoff, kb + 1, g);
-    compute_stage(s0, fscale, kb, acc);
+    if (kb + 1 < kb_hi) load_stage(s1, wt, br, bvoff, kb + 1, g);
+    compute_stage(s0, acc);
     if (kb + 1 < kb_hi) {
-      if (kb + 2 < kb_hi) load_stage(s0, wr, wvoff, srows, br, bvoff, kb + 2, g);
-      compute_stage(s1, fscale, kb + 1, acc);
+      if (kb + 2 < kb_hi) load_stage(s0, wt, br, bvoff, kb + 2, g);
+      compute_stage(s1, acc);
     }
   }
 }
@@ -286,33 +301,31 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
     }
   }
   const uint32_t rb = static_cast<uint32_t>(row_bytes<FMT>(K));
-  const __amdgpu_buffer_rsrc_t wr =
-      make_rsrc(bank.w + static_cast<size_t>(sv.expert) * N * rb, static_cast<uint32_t>(N) * rb);
+  WTiles<NMAT> wt;
+  wt.wr = make_rsrc(bank.w + static_cast<size_t>(sv.expert) * N * rb, static_cast<uint32_t>(N) * rb);
+  if constexpr (FMT == FMT_FP8) {
+    const uint32_t sbytes = static_cast<uint32_t>(N / 128) * (K / 128) * 4;
+    wt.sr = make_rsrc(static_cast<const uint8_t*>(bank.s) + static_cast<size_t>(sv.expert) * sbytes, sbytes);
+  } else {
+    wt.sr = wt.wr;
+  }
   const uint32_t gbytes = FMT == FMT_BF16 ? 64 : FMT == FMT_FP8 ? 32 : 16;  // a lane group's 32 values
-  uint32_t wvoff[NMAT];
-  const uint8_t* srows[NMAT];
-  const float* fscale[NMAT];
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) {
     // matrix m: gate tiles then up tiles (stage 0); down tiles (stage 1)
     const int tile_row = (STAGE == 0 && m >= RT) ? inter + wrow0 + 16 * (m - RT) : wrow0 + 16 * m;
     const int ridx = tile_row + r16;
-    wvoff[m] = static_cast<uint32_t>(ridx) * rb + g * gbytes;
+    wt.wvoff[m] = static_cast<uint32_t>(ridx) * rb + g * gbytes;
+    // a 16-row tile lies inside one 128-row scale block
+    wt.soff[m] = static_cast<uint32_t>(tile_row / 128) * (K / 128) * 4;
     if constexpr (FMT == FMT_MXFP4) {
-      srows[m] = static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(sv.expert) * N + ridx) * (K / 32);
+      wt.srows[m] = static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(sv.expert) * N + ridx) * (K / 32);
     } else {
-      srows[m] = nullptr;
-    }
-    if constexpr (FMT == FMT_FP8) {
-      // a 16-row tile lies inside one 128-row scale block
-      fscale[m] = static_cast<const float*>(bank.s) +
-                  (static_cast<size_t>(sv.expert) * (N / 128) + tile_row / 128) * (K / 128);
-    } else {
-      fscale[m] = nullptr;
+      wt.srows[m] = nullptr;
     }
   }
   f32x4 acc[NMAT][NCH];
-  gemv_tile<FMT, NMAT, NCH, KS>(wr, wvoff, srows, fscale, K, kw, br, bvoff, acc);
+  gemv_tile<FMT, NMAT, NCH, KS>(wt, K, kw, br, bvoff, acc);
 
   if constexpr (KS == 1) {
 #pragma unroll
@@ -474,28 +487,70 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
 
 // Launch shapes.  Stage 0 (K = hidden, long rows): the 4 waves split K and a
 // workgroup covers RT tiles of gate and of up.  Stage 1 (K = intermediate,
-// short rows): each wave owns RT whole tiles.  Two tiles per wave are used when
-// the grid still has at least kMinWgs workgroups; they halve the activation
-// loads per weight byte.
-constexpr int kMinWgs = 1024;
+// short rows): each wave owns RT whole tiles.  RT = 2 halves the activation
+// loads per weight byte and is faster at every measured batch except when its
+// grid leaves the resident slots much emptier than RT = 1's (b = 1 gate_up:
+// 1.1 rounds against 2.25), so RT = 1 is used only when it fills the slots at
+// least 15 points better.
+
+// Resident workgroups per CU of a kernel (runtime occupancy query, cached).
+template <auto KERNEL>
+static int resident_per_cu() {
+  static int cached = 0;
+  if (cached == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(KERNEL), kDecWaves * kWave, 0) !=
+            hipSuccess ||
+        n < 1)
+      n = 1;
+    cached = n;
+  }
+  return cached;
+}
+
+static int cu_count() {
+  static int cached = 0;
+  if (cached == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                  hipSuccess || n < 1)
+      n = 256;
+    cached = n;
+  }
+  return cached;
+}
+
+// Fraction of the resident slots kept busy over the rounds of a grid.
+static double fill(long long wgs, long long slots) {
+  const long long rounds = (wgs + slots - 1) / slots;
+  return static_cast<double>(wgs) / static_cast<double>(rounds * slots);
+}
+
+template <auto K1, auto K2>
+static hipError_t launch_pick(long long n1, long long n2, dim3 g1, dim3 g2, const DecodeArgs& a, hipStream_t stream) {
+  const int cus = cu_count();
+  const double f1 = fill(n1, static_cast<long long>(cus) * resident_per_cu<K1>());
+  const double f2 = fill(n2, static_cast<long long>(cus) * resident_per_cu<K2>());
+  const dim3 block(kDecWaves * kWave);
+  if (f2 >= f1 - 0.15)
+    hipLaunchKernelGGL(K2, g2, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL(K1, g1, block, 0, stream, a);
+  return hipGetLastError();
+}
 
 template <int FR, int FS>
 static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared, hipStream_t stream) {
   const int gy = a.max_seg + (has_shared ? (a.M + a.seg_cap - 1) / a.seg_cap : 0);
   const int imax = has_shared ? max(a.I, a.Is) : a.I;
-  const dim3 block(kDecWaves * kWave);
   if (stage == 0) {
-    if ((imax / 32) * gy >= kMinWgs)
-      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 0, 2, 4>), dim3((imax + 31) / 32, gy), block, 0, stream, a);
-    else
-      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 0, 1, 4>), dim3((imax + 15) / 16, gy), block, 0, stream, a);
-  } else {
-    if ((a.H / 128) * gy >= kMinWgs)
-      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 1, 2, 1>), dim3(a.H / 128, gy), block, 0, stream, a);
-    else
-      hipLaunchKernelGGL((decode_stage_kernel<FR, FS, 1, 1, 1>), dim3(a.H / 64, gy), block, 0, stream, a);
+    const dim3 g1((imax + 15) / 16, gy), g2((imax + 31) / 32, gy);
+    return launch_pick<decode_stage_kernel<FR, FS, 0, 1, 4>, decode_stage_kernel<FR, FS, 0, 2, 4>>(
+        static_cast<long long>(g1.x) * gy, static_cast<long long>(g2.x) * gy, g1, g2, a, stream);
   }
-  return hipGetLastError();
+  const dim3 g1(a.H / 64, gy), g2(a.H / 128, gy);
+  return launch_pick<decode_stage_kernel<FR, FS, 1, 1, 1>, decode_stage_kernel<FR, FS, 1, 2, 1>>(
+      static_cast<long long>(g1.x) * gy, static_cast<long long>(g2.x) * gy, g1, g2, a, stream);
 }
 
 hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream) {
