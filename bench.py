@@ -263,12 +263,27 @@ def run_prefill(fmt: str, steps: int, warmup: int, gen, dev, M: int = 8192):
     t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
+    # instrumented eager pass: per-kernel durations of one call
+    import ctypes
+
+    L = _lib.lib()
+    L.ftmoe_stage_timing_begin()
+    for _ in range(steps):
+        ops.experts_prefill(x, w, ids, bank, shared=shared, out=out)
+    torch.cuda.synchronize()
+    arr = (ctypes.c_double * 8)()
+    ns, nc = ctypes.c_int(), ctypes.c_int()
+    _lib.check(L.ftmoe_stage_timing_end(arr, 8, ctypes.byref(ns), ctypes.byref(nc)), "stage timing")
+    names = ["align", "x_quant", "gate_up", "act_quant", "down", "combine"]
+    stage_us = {names[j]: arr[j] / max(1, nc.value) * 1e3 for j in range(min(ns.value, len(names)))}
     routes = int((ids >= 0).sum())
     flops = (routes + M) * 6 * H * I
     counts = torch.bincount(ids.view(-1).long(), minlength=E)
     peak = PEAK_TFLOPS["fp8"]
+    padded = int(((counts + 127) // 128 * 128).sum()) + (M + 127) // 128 * 128
     res = dict(tokens=M, sequences=lens.tolist(), ms=ms, tflops=flops / (ms / 1e3) / 1e12, flops=flops,
-               max_expert_tokens=int(counts.max()), min_expert_tokens=int(counts.min()))
+               max_expert_tokens=int(counts.max()), min_expert_tokens=int(counts.min()),
+               padded_rows_per_real_row=round(padded / (routes + M), 4), stage_us=stage_us)
     res["frac_of_fp8_peak"] = res["tflops"] / peak
     if fmt == "mxfp4":
         res["frac_of_fp4_peak"] = res["tflops"] / PEAK_TFLOPS["mxfp4"]
@@ -387,7 +402,7 @@ def main() -> int:
     if not args.no_sweep:
         for M in (1, 8, 32):
             log(f"[bench] sweep C4 decode batch {M}")
-            sweep[f"{C4['name']}_b{M}"] = run_decode(c4, M, 20, 3, gen)
+            sweep[f"{C4['name']}_b{M}"] = run_decode(c4, M, 20, 3, gen, stage_timing=True)
     cpu = None
     if not args.no_cpu:
         log("[bench] CPU baseline")
@@ -399,7 +414,7 @@ def main() -> int:
             log(f"[bench] sweep {cfg['name']}")
             layer = DecodeLayer(cfg, dev, gen)
             for M in (1, 8, 32, 64):
-                sweep[f"{cfg['name']}_b{M}"] = run_decode(layer, M, 20, 3, gen)
+                sweep[f"{cfg['name']}_b{M}"] = run_decode(layer, M, 20, 3, gen, stage_timing=True)
             del layer
             torch.cuda.empty_cache()
         for fmt in ("fp8_block", "mxfp4"):

@@ -72,6 +72,16 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout.decode(errors="replace"))
+    # a kernel whose host-side instantiation the compiler dropped shows up as an
+    # undefined symbol of the library's own namespace: fail the build on it
+    nm = shutil.which("nm")
+    if nm:
+        und = subprocess.run([nm, "-D", "--undefined-only", "-C", str(tmp)], stdout=subprocess.PIPE,
+                             stderr=subprocess.STDOUT).stdout.decode(errors="replace")
+        missing = [ln.strip() for ln in und.splitlines() if "ftmoe::" in ln]
+        if missing:
+            os.unlink(tmp)
+            raise RuntimeError("libftmoe.so has undefined library symbols:\n" + "\n".join(missing))
     os.replace(tmp, LIB)
     return LIB
 

@@ -7,7 +7,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/ftmoe.h"
+#include "ftmoe.h"
 
 #include "kernels.h"
 
@@ -166,7 +166,7 @@ PrefillLayout prefill_layout(void* ws, int M, int k, const ftmoe_bank* bank, con
   L.ntpp = c.take<int32_t>(1);
   L.cum = c.take<int32_t>(bank->num_rows + 2);
   const bool quant = bank->format != FTMOE_FMT_BF16;
-  const size_t sc = bank->format == FTMOE_FMT_FP8_B128 ? sizeof(float) : 1;
+  const size_t sc = 4;  // float scale (FP8) or e8m0 code in 32 bits (MXFP4)
   const size_t rows = static_cast<size_t>(numel) + (shared ? M : 0);
   if (quant) {
     L.xq = c.take<uint8_t>(static_cast<size_t>(M) * H);
@@ -417,7 +417,7 @@ int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, 
   g_timer.mark();
 
   const uint16_t* xb = static_cast<const uint16_t*>(x);
-  const int qmode = fmt == FTMOE_FMT_MXFP4 ? 1 : 0;
+  const int qmode = fmt == FTMOE_FMT_MXFP4 ? 2 : 0;
   if (fmt != FTMOE_FMT_BF16) {
     rc = check_hip(ftmoe::launch_act_quant(qmode, xb, M, H, L.xq, L.xs, stream), "experts_prefill x quant");
     if (rc) return rc;

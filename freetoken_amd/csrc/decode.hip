@@ -58,19 +58,8 @@ struct RawA<FMT_MXFP4> {
   uint32_t code;
 };
 
-// Buffer loads: weights and activations are read through buffer descriptors
-// (base in SGPRs, 32-bit lane offsets, the K-block offset in soffset).  A lane
-// whose offset is kOutOfRange reads zeros without touching memory.
-constexpr uint32_t kOutOfRange = 0x80000000u;
-constexpr int kBufDword3 = 0x00020000;  // gfx9 raw-buffer descriptor word 3
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufDword3);
-}
-
-__device__ __forceinline__ u32x4 buf_x4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
+// Weights and activations are read through buffer descriptors (make_rsrc,
+// buf_x4): base in SGPRs, 32-bit lane offsets, the K-block offset in soffset.
 
 // Weight bytes of one lane for K block kb: the lane's row starts at voff
 // (row * row_bytes + the lane group's 32-value slice); the K block adds
@@ -153,8 +142,7 @@ __device__ __forceinline__ void load_stage(KStage<FMT, NMAT, NCH>& st, const WTi
     // wave-uniform address: one request per tile, in flight with the weights
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
-      st.sc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wt.sr, wt.soff[m],
-                                                                                static_cast<uint32_t>(kb) * 4, 0));
+      st.sc[m] = buf_f32(wt.sr, wt.soff[m], static_cast<uint32_t>(kb) * 4);
   }
   const uint32_t so = static_cast<uint32_t>(kb) * 256;
 #pragma unroll

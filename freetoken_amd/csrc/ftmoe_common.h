@@ -146,4 +146,27 @@ __device__ __forceinline__ float wave_max_f32(float v) {
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 
+// ---- raw buffer loads ---------------------------------------------------------
+// A descriptor covers [base, base + bytes); a lane offset at or beyond `bytes`
+// reads zeros without touching memory (kOutOfRange is beyond every range the
+// library builds: callers keep ranges below 2 GiB).
+constexpr uint32_t kOutOfRange = 0x80000000u;
+constexpr int kBufDword3 = 0x00020000;  // gfx9 raw-buffer descriptor word 3
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufDword3);
+}
+
+__device__ __forceinline__ u32x4 buf_x4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+__device__ __forceinline__ float buf_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+
+__device__ __forceinline__ uint32_t buf_u8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, 0));
+}
+
 }  // namespace ftmoe

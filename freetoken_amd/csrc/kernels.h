@@ -77,7 +77,7 @@ hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs
 struct PrefillGemmArgs {
   // rows of the activation operand
   const uint8_t* xq;        // fp8 [rows, K] (FP8 / MXFP4) or bf16 [rows, K] (BF16)
-  const void* xs;           // float [rows, K/128] (FP8) or uint8 e8m0 [rows, K/128] (MXFP4)
+  const void* xs;           // float [rows, K/128] (FP8) or uint32 e8m0 codes [rows, K/128] (MXFP4)
   int x_token_rows;         // 1: gate_up (row = token = route / k, shared row = token)
                             // 0: down    (row = route, shared row = M*k + token)
   const int32_t* sorted;    // [max_padded] route indices per BM block, sentinel numel

@@ -39,7 +39,9 @@ constexpr int kPThreads = 256;
 // ----------------------------------------------------------------------------
 // Activation quantisation: one wave per row, 2 values per lane per 128-group.
 //   MODE 0: float scale s = max(amax, 1e-10) / 448, q = e4m3(clamp(x / s))
-//   MODE 1: e8m0 scale 2^ceil(log2(max(amax, 1e-4) * (1/448))), q = e4m3(x / 2^e)
+//   MODE 1: e8m0 scale 2^ceil(log2(max(amax, 1e-4) * (1/448))), q = e4m3(x / 2^e),
+//           codes stored as uint8; MODE 2: the same with codes stored as uint32
+//           (the grouped GEMM copies them to LDS in 4-byte units)
 // ----------------------------------------------------------------------------
 template <int MODE>
 __global__ void __launch_bounds__(256) act_quant_kernel(const uint16_t* __restrict__ x, int rows, int K,
@@ -68,7 +70,10 @@ __global__ void __launch_bounds__(256) act_quant_kernel(const uint16_t* __restri
       const float inv = ldexpf(1.0f, -e);
       qa = fminf(fmaxf(a * inv, -448.0f), 448.0f);
       qb = fminf(fmaxf(b * inv, -448.0f), 448.0f);
-      if (lane == 0) static_cast<uint8_t*>(scales)[static_cast<size_t>(row) * ng + gi] = static_cast<uint8_t>(e + 127);
+      if (lane == 0) {
+        if (MODE == 1) static_cast<uint8_t*>(scales)[static_cast<size_t>(row) * ng + gi] = static_cast<uint8_t>(e + 127);
+        else static_cast<uint32_t*>(scales)[static_cast<size_t>(row) * ng + gi] = static_cast<uint32_t>(e + 127);
+      }
     }
     const uint32_t pk = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(qa, qb, 0, false));
     qr[gi * 64 + lane] = static_cast<uint16_t>(pk & 0xffffu);
@@ -407,13 +412,393 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillGemmArgs
   }
 }
 
+// ----------------------------------------------------------------------------
+// Quantised grouped GEMM (FP8, MXFP4) on direct-to-LDS loads
+//
+// A workgroup computes 256 weight rows x 128 routes; wave w owns weight rows
+// 64w..64w+63 of the tile (four 16-row MFMA tiles) against all 128 routes
+// (eight 16-column tiles).  Every operand of a 128-deep K step -- the wave's
+// weight rows, the activation tile, the weight scales and the activation
+// scales -- is copied global -> LDS by the LDS-DMA form of the global loads
+// (no register staging), into a ring of three stages: the copies of step kb+2
+// are in flight while step kb computes.  The waits are explicit (vmcnt of the
+// copies of one step) and the barrier is a bare s_barrier, so a barrier never
+// drains the copies still in flight.
+//
+// LDS rows are 128-byte (FP8; 64-byte MXFP4 weights) lines of 16-byte chunks
+// stored XOR-swizzled by the line index, so the MFMA operand reads of eight
+// lanes hit eight different bank groups.
+//
+// Gate/up: wave w owns gate rows n0+32w+[0,32) and up rows I+n0+32w+[0,32), so
+// SwiGLU pairs registers; a workgroup covers 128 intermediate features.
+// Down: rows at or past N (the last tile when N % 256 != 0) are read clamped
+// to row N-1 and never stored.
+//
+// Schedule (map_tile_q): the active workgroups are laid out XCD-major
+// (workgroup b runs on XCD b % 8), so each XCD works through a contiguous range
+// of the logical order, in which chunks of 4 M blocks of one expert sweep its N
+// tiles: the 32 workgroups an XCD runs at once read 8 weight tiles (many
+// distinct weight bytes in flight, each fetched into the XCD's L2 once per
+// chunk) and share 4 M blocks of activations.
+// ----------------------------------------------------------------------------
+constexpr int kQRows = 256;   // weight rows per workgroup
+constexpr int kQStages = 3;
+constexpr int kXcds = 8;
+
+template <int FMT>
+struct QLds {
+  static constexpr int kALine = FMT == FMT_FP8 ? 128 : 64;   // weight bytes per row per K step
+  static constexpr int kA = 16 * 16 * kALine;                 // 4 waves x 4 tiles x 16 rows
+  static constexpr int kAS = FMT == FMT_FP8 ? 16 * 16 : 256 * 4;  // fp8: float per tile (16 B per wave); mxfp4: 4 codes per row
+  static constexpr int kB = kPBM * 128;
+  static constexpr int kBS = kPBM * 4;
+  static constexpr int kOffAS = kA, kOffB = kA + kAS, kOffBS = kA + kAS + kB;
+  static constexpr int kStage = kA + kAS + kB + kBS;
+  static constexpr int kTotal = kQStages * kStage;
+  // LDS-DMA instructions each wave issues per K step (uniform over waves)
+  static constexpr int kDmaPerStep = FMT == FMT_FP8 ? 8 + 1 + 4 + 1 : 4 + 1 + 4 + 1;
+};
+
+__device__ __forceinline__ int xcd_major(int b, int n) {
+  const int per = n / kXcds, rem = n % kXcds;
+  const int x = b % kXcds, i = b / kXcds;
+  return x * per + min(x, rem) + i;
+}
+
+// M blocks that run next to each other on one weight tile
+constexpr int kQChunk = 4;
+
+// (M block, N tile) of position `local` in a group of nb M blocks x ntiles:
+// chunks of kQChunk M blocks, each chunk sweeping all N tiles, so a window of
+// 32 consecutive workgroups reads 8 different weight tiles (weights in flight
+// from 8 places) while sharing the activations of 4 M blocks.
+__device__ __forceinline__ void chunked(int local, int nb, int ntiles, int& m, int& ntile) {
+  const int full = nb / kQChunk, rem = nb - full * kQChunk;
+  const int span = kQChunk * ntiles;
+  if (local < full * span) {
+    const int c = local / span, w = local - c * span;
+    ntile = w / kQChunk;
+    m = c * kQChunk + (w - ntile * kQChunk);
+  } else {
+    const int w = local - full * span;
+    ntile = w / rem;
+    m = full * kQChunk + (w - ntile * rem);
+  }
+}
+
+// Workgroup b of the grid -> (expert or shared, M block, N tile).  Only the
+// active workgroups -- routed blocks of the real experts, then the shared
+// expert's blocks -- take part; they are laid out XCD-major over their own
+// count, so every XCD gets the same share.  Returns false for idle ones.
+__device__ __forceinline__ bool map_tile_q(const PrefillGemmArgs& a, int b, bool& shared, int& expert, int& mblock,
+                                           int& ntile) {
+  const int routed = (a.cum[a.num_experts] / kPBM) * a.ntiles;
+  const int total = routed + a.shared_blocks * a.ntiles;
+  if (b >= total) return false;
+  const int wg = xcd_major(b, total);
+  if (wg < routed) {
+    int lo = 0, hi = a.num_experts;  // largest e with cum[e]/BM * ntiles <= wg
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if ((a.cum[mid] / kPBM) * a.ntiles <= wg) lo = mid; else hi = mid;
+    }
+    const int b0 = a.cum[lo] / kPBM;
+    const int nb = a.cum[lo + 1] / kPBM - b0;
+    int m;
+    chunked(wg - b0 * a.ntiles, nb, a.ntiles, m, ntile);
+    shared = false;
+    expert = lo;
+    mblock = b0 + m;
+    return true;
+  }
+  chunked(wg - routed, a.shared_blocks, a.ntiles, mblock, ntile);
+  shared = true;
+  expert = 0;
+  return true;
+}
+
+// s_barrier without the memory fence of __syncthreads (which would wait for
+// every copy in flight); the clobber keeps the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// LDS-DMA copies: each lane's `bytes` from src land at dst + lane * bytes
+// (dst is wave-uniform).
+__device__ __forceinline__ void lds_copy16(const uint8_t* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_copy4(const uint8_t* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
+}
+
+// Empty asm that keeps the value's update at this point of the instruction
+// stream (no code is emitted).
+__device__ __forceinline__ void pin(f32x4& v) { asm volatile("" : "+v"(v)); }
+
+template <int FMT, int GATE_UP>
+__global__ void __launch_bounds__(kPThreads) prefill_qgemm_kernel(PrefillGemmArgs a) {
+  using L = QLds<FMT>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t q_lds[];
+  __shared__ int s_row[kPBM];
+  __shared__ int s_route[kPBM];
+
+  bool shared;
+  int expert, mblock, ntile;
+  if (!map_tile_q(a, blockIdx.x, shared, expert, mblock, ntile)) return;
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  const int r16 = lane & 15, g = lane >> 4;
+
+  if (tid < kPBM) {
+    int row = -1, route = -1;
+    if (shared) {
+      const int t = mblock * kPBM + tid;
+      if (t < a.M) {
+        route = t;
+        row = a.x_token_rows ? t : a.numel + t;
+      }
+    } else {
+      const int rr = a.sorted[mblock * kPBM + tid];
+      if (rr < a.numel) {
+        route = rr;
+        row = a.x_token_rows ? rr / a.k : rr;
+      }
+    }
+    s_row[tid] = row;
+    s_route[tid] = route;
+  }
+  __syncthreads();
+
+  const BankView bank = shared ? a.ws : a.w;
+  const int K = a.K, nkb = K / 128;
+  const size_t rb = FMT == FMT_FP8 ? static_cast<size_t>(K) : static_cast<size_t>(K) / 2;
+  const uint8_t* wexp = bank.w + static_cast<size_t>(expert) * a.N * rb;
+
+  // the wave's four weight tiles
+  const int n0 = GATE_UP ? ntile * (kQRows / 2) : ntile * kQRows;
+  int trow[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (GATE_UP) trow[j] = (j < 2 ? 0 : a.inter) + n0 + 32 * wave + 16 * (j & 1);
+    else trow[j] = n0 + 64 * wave + 16 * j;
+  }
+
+  // ---- per-lane sources of the copies (K step 0; step kb adds kb * step bytes)
+  // weights: FP8 tile j is 2 copies of 8 rows x 8 chunks, MXFP4 one copy of 16 rows x 4 chunks
+  constexpr int kACopies = FMT == FMT_FP8 ? 8 : 4;
+  const uint8_t* asrc[kACopies];
+#pragma unroll
+  for (int c = 0; c < kACopies; ++c) {
+    int r, q;
+    if constexpr (FMT == FMT_FP8) {
+      const int j = c >> 1, h = c & 1;
+      r = 8 * h + (lane >> 3);
+      q = (lane & 7) ^ (r & 7);
+      asrc[c] = wexp + static_cast<size_t>(min(trow[j] + r, a.N - 1)) * rb + q * 16;
+    } else {
+      const int j = c;
+      r = lane >> 2;
+      q = (lane & 3) ^ ((r >> 1) & 3);
+      asrc[c] = wexp + static_cast<size_t>(min(trow[j] + r, a.N - 1)) * rb + q * 16;
+    }
+  }
+  // weight scales: FP8 lanes 0..3 -> the float of tile `lane`; MXFP4 lane -> the 4 codes of row 16(lane/16)+lane%16
+  const uint8_t* wssrc;
+  if constexpr (FMT == FMT_FP8) {
+    const int j = lane & 3;
+    wssrc = static_cast<const uint8_t*>(bank.s) +
+            ((static_cast<size_t>(expert) * (a.N / 128) + min(trow[j], a.N - 1) / 128) * nkb) * 4;
+  } else {
+    const int row = min(trow[lane >> 4] + (lane & 15), a.N - 1);
+    wssrc = static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(expert) * a.N + row) * (K / 32);
+  }
+  // activations: copy c (0..3) of wave w moves 8 columns x 8 chunks
+  const uint8_t* bsrc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int col = 8 * (4 * wave + c) + (lane >> 3);
+    const int q = (lane & 7) ^ (col & 7);
+    const int row = s_row[col] < 0 ? 0 : s_row[col];  // padding columns compute on row 0, never stored
+    bsrc[c] = a.xq + static_cast<size_t>(row) * K + q * 16;
+  }
+  // activation scales: lanes 0..31 of wave w -> column 32w + lane
+  const int scol = 32 * wave + (lane & 31);
+  const uint8_t* xssrc =
+      static_cast<const uint8_t*>(a.xs) + static_cast<size_t>(s_row[scol] < 0 ? 0 : s_row[scol]) * nkb * 4;
+
+  auto issue = [&](int kb) {
+    uint8_t* st = q_lds + (kb % kQStages) * L::kStage;
+    const size_t ka = static_cast<size_t>(kb) * L::kALine;
+#pragma unroll
+    for (int c = 0; c < kACopies; ++c) {
+      uint8_t* dst = st + (FMT == FMT_FP8 ? (wave * 4 + (c >> 1)) * 2048 + (c & 1) * 1024 : (wave * 4 + c) * 1024);
+      lds_copy16(asrc[c] + ka, dst);
+    }
+    if constexpr (FMT == FMT_FP8) {
+      if (lane < 4) lds_copy4(wssrc + kb * 4, st + L::kOffAS + wave * 16);
+    } else {
+      lds_copy4(wssrc + kb * 4, st + L::kOffAS + wave * 256);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      lds_copy16(bsrc[c] + static_cast<size_t>(kb) * 128, st + L::kOffB + (4 * wave + c) * 1024);
+    if (lane < 32) lds_copy4(xssrc + kb * 4, st + L::kOffBS + wave * 128);
+  };
+
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[j][i] = zero;
+
+  auto compute = [&](int kb) {
+    const uint8_t* st = q_lds + (kb % kQStages) * L::kStage;
+    // weight operands of the four tiles
+    i32x8 wf[4];
+    int wcode[4];
+    float sw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (FMT == FMT_FP8) {
+        const uint8_t* p = st + (wave * 4 + j) * 2048 + r16 * 128;
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(p + (((2 * g) ^ (r16 & 7)) * 16));
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + (((2 * g + 1) ^ (r16 & 7)) * 16));
+        wf[j] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        sw[j] = *reinterpret_cast<const float*>(st + L::kOffAS + wave * 16 + j * 4);
+      } else {
+        const uint8_t* p = st + (wave * 4 + j) * 1024 + r16 * 64;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(p + ((g ^ ((r16 >> 1) & 3)) * 16));
+        wf[j] = i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
+        wcode[j] = st[L::kOffAS + (wave * 64 + 16 * j + r16) * 4 + g];
+      }
+    }
+    auto read_x = [&](int i, i32x8& xf, uint32_t& xs) {
+      const int col = 16 * i + r16;
+      const uint8_t* p = st + L::kOffB + col * 128;
+      u32x4 lo, hi;
+      if constexpr (FMT == FMT_FP8) {
+        lo = *reinterpret_cast<const u32x4*>(p + (((2 * g) ^ (col & 7)) * 16));
+        hi = *reinterpret_cast<const u32x4*>(p + (((2 * g + 1) ^ (col & 7)) * 16));
+      } else {
+        // the f8f6f4 MFMA reads an fp8 lane group g as K = 16g+[0,16) and
+        // 64+16g+[0,16), an fp4 lane group as the block [32g, 32g+32)
+        lo = *reinterpret_cast<const u32x4*>(p + ((g ^ (col & 7)) * 16));
+        hi = *reinterpret_cast<const u32x4*>(p + (((4 + g) ^ (col & 7)) * 16));
+      }
+      xf = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      xs = *reinterpret_cast<const uint32_t*>(st + L::kOffBS + col * 4);
+    };
+    // The next column tile's LDS reads are issued before this tile's MFMAs.
+    // FP8: every MFMA is followed by the scale fold of the previous one; the
+    // empty asm pins each fold there, so the VALU work runs while the matrix
+    // core is busy instead of piling up after the last MFMA.
+    i32x8 xf[2];
+    uint32_t xs[2];
+    read_x(0, xf[0], xs[0]);
+    f32x4 tp = zero;
+    float fp = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i + 1 < 8) read_x(i + 1, xf[(i + 1) & 1], xs[(i + 1) & 1]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (FMT == FMT_FP8) {
+          const f32x4 t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[j], xf[i & 1], zero, 0, 0, 0, 0, 0, 0);
+          const int k = 4 * i + j;
+          if (k > 0) {
+            const int pi = (k - 1) >> 2, pj = (k - 1) & 3;
+            acc[pj][pi] += tp * fp;
+            pin(acc[pj][pi]);
+          }
+          tp = t;
+          fp = __uint_as_float(xs[i & 1]) * sw[j];
+        } else {
+          acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[j], xf[i & 1], acc[j][i], 4, 0, 0, wcode[j], 0,
+                                                                       static_cast<int>(xs[i & 1]));
+        }
+      }
+    }
+    if constexpr (FMT == FMT_FP8) acc[3][7] += tp * fp;
+  };
+
+  // K pipeline over a ring of three LDS stages
+  issue(0);
+  if (nkb > 1) issue(1);
+  if (nkb > 1) wait_vm<L::kDmaPerStep>();
+  else wait_vm<0>();
+  bare_barrier();
+  for (int kb = 0; kb < nkb; ++kb) {
+    if (kb + 2 < nkb) issue(kb + 2);
+    compute(kb);
+    // step kb+1's copies must have landed (step kb+2's may still fly); every
+    // LDS read of this step has returned before its MFMA used it
+    if (kb + 2 < nkb) wait_vm<L::kDmaPerStep>();
+    else wait_vm<0>();
+    wait_lgkm0();
+    bare_barrier();
+  }
+
+  // ---- epilogue: lane holds rows trow[j] + g*4 + v of route column 16i + r16
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int col = 16 * i + r16;
+    const int route = s_route[col];
+    if (route < 0) continue;
+    if (GATE_UP) {
+      const int arow = shared ? a.numel + route : route;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        uint16_t o[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float gg = bf16_round(acc[s2][i][v]);
+          const float uu = bf16_round(acc[2 + s2][i][v]);
+          o[v] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
+        }
+        const int n = n0 + 32 * wave + 16 * s2 + g * 4;
+        uint2 pk;
+        pk.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
+        pk.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+        *reinterpret_cast<uint2*>(a.out + static_cast<size_t>(arow) * a.inter + n) = pk;
+      }
+    } else {
+      const float wt = shared ? 1.0f : a.topk_w[route];
+      uint16_t* dst = shared ? a.sh_out + static_cast<size_t>(route) * a.N : a.out + static_cast<size_t>(route) * a.N;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = trow[j] + g * 4;
+        if (n >= a.N) continue;
+        uint16_t o[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(acc[j][i][v] * wt);
+        uint2 pk;
+        pk.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
+        pk.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+        *reinterpret_cast<uint2*>(dst + n) = pk;
+      }
+    }
+  }
+}
+
 hipError_t launch_act_quant(int mode, const uint16_t* x, int rows, int K, uint8_t* q, void* scales,
                             hipStream_t stream) {
   const dim3 grid((rows + 3) / 4), block(256);
   if (mode == 0)
     hipLaunchKernelGGL(act_quant_kernel<0>, grid, block, 0, stream, x, rows, K, q, scales);
-  else
+  else if (mode == 1)
     hipLaunchKernelGGL(act_quant_kernel<1>, grid, block, 0, stream, x, rows, K, q, scales);
+  else
+    hipLaunchKernelGGL(act_quant_kernel<2>, grid, block, 0, stream, x, rows, K, q, scales);
   return hipGetLastError();
 }
 
@@ -431,10 +816,25 @@ static hipError_t launch_gemm_t(const PrefillGemmArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <int FMT, int GU>
+static hipError_t launch_qgemm_t(PrefillGemmArgs a, hipStream_t stream) {
+  static bool attr = false;
+  if (!attr) {
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_qgemm_kernel<FMT, GU>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, QLds<FMT>::kTotal);
+    if (err != hipSuccess) return err;
+    attr = true;
+  }
+  a.ntiles = GU ? a.inter / (kQRows / 2) : (a.N + kQRows - 1) / kQRows;
+  const int wgs = (a.max_blocks + a.shared_blocks) * a.ntiles;
+  hipLaunchKernelGGL((prefill_qgemm_kernel<FMT, GU>), dim3(wgs), dim3(kPThreads), QLds<FMT>::kTotal, stream, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_prefill_gemm(int fmt, int gate_up, const PrefillGemmArgs& a, hipStream_t stream) {
-  if (fmt == FMT_FP8) return gate_up ? launch_gemm_t<FMT_FP8, 1>(a, stream) : launch_gemm_t<FMT_FP8, 0>(a, stream);
+  if (fmt == FMT_FP8) return gate_up ? launch_qgemm_t<FMT_FP8, 1>(a, stream) : launch_qgemm_t<FMT_FP8, 0>(a, stream);
   if (fmt == FMT_MXFP4)
-    return gate_up ? launch_gemm_t<FMT_MXFP4, 1>(a, stream) : launch_gemm_t<FMT_MXFP4, 0>(a, stream);
+    return gate_up ? launch_qgemm_t<FMT_MXFP4, 1>(a, stream) : launch_qgemm_t<FMT_MXFP4, 0>(a, stream);
   if (fmt == FMT_BF16) return gate_up ? launch_gemm_t<FMT_BF16, 1>(a, stream) : launch_gemm_t<FMT_BF16, 0>(a, stream);
   return hipErrorInvalidValue;
 }
