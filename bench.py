@@ -280,7 +280,8 @@ def run_prefill(fmt: str, steps: int, warmup: int, gen, dev, M: int = 8192):
     flops = (routes + M) * 6 * H * I
     counts = torch.bincount(ids.view(-1).long(), minlength=E)
     peak = PEAK_TFLOPS["fp8"]
-    padded = int(((counts + 127) // 128 * 128).sum()) + (M + 127) // 128 * 128
+    bm = 128 if fmt == "bf16" else 256  # routes per M block of the prefill GEMMs
+    padded = int(((counts + bm - 1) // bm * bm).sum()) + (M + bm - 1) // bm * bm
     res = dict(tokens=M, sequences=lens.tolist(), ms=ms, tflops=flops / (ms / 1e3) / 1e12, flops=flops,
                max_expert_tokens=int(counts.max()), min_expert_tokens=int(counts.min()),
                padded_rows_per_real_row=round(padded / (routes + M), 4), stage_us=stage_us)

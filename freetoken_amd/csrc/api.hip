@@ -153,14 +153,12 @@ struct PrefillLayout {
   size_t bytes;
 };
 
-constexpr int kPrefillBM = 128;
-
 PrefillLayout prefill_layout(void* ws, int M, int k, const ftmoe_bank* bank, const ftmoe_bank* shared) {
   PrefillLayout L{};
   Carver c{static_cast<uint8_t*>(ws)};
   const int numel = M * k;
   const int H = bank->hidden, I = bank->inter;
-  ftmoe_align_sizes(numel, bank->num_rows, kPrefillBM, &L.max_padded, &L.max_blocks);
+  ftmoe_align_sizes(numel, bank->num_rows, ftmoe::prefill_block_size(bank->format), &L.max_padded, &L.max_blocks);
   L.sorted = c.take<int32_t>(L.max_padded);
   L.expert_ids = c.take<int32_t>(L.max_blocks);
   L.ntpp = c.take<int32_t>(1);
@@ -404,7 +402,8 @@ int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, 
   al.ids = topk_ids;
   al.numel = numel;
   al.num_experts = bank->num_rows;
-  al.block_size = kPrefillBM;
+  const int bm = ftmoe::prefill_block_size(bank->format);
+  al.block_size = bm;
   al.sorted_ids = L.sorted;
   al.max_padded = L.max_padded;
   al.expert_ids = L.expert_ids;
@@ -432,7 +431,7 @@ int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, 
   g.M = M;
   g.k = top_k;
   g.max_blocks = L.max_blocks;
-  g.shared_blocks = shared ? (M + kPrefillBM - 1) / kPrefillBM : 0;
+  g.shared_blocks = shared ? (M + bm - 1) / bm : 0;
   g.w = {nullptr, nullptr};
   g.act_kind = activation;
   g.topk_w = topk_w;

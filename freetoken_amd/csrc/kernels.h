@@ -101,6 +101,10 @@ struct PrefillGemmArgs {
   int act_kind;
 };
 
+// Routes per M block of the prefill GEMMs (the align block size): the
+// quantised kernels tile 256 routes, the bf16 kernel 128.
+inline int prefill_block_size(int fmt) { return fmt == FMT_BF16 ? 128 : 256; }
+
 hipError_t launch_act_quant(int mode, const uint16_t* x, int rows, int K, uint8_t* q, void* scales,
                             hipStream_t stream);
 hipError_t launch_prefill_gemm(int fmt, int gate_up, const PrefillGemmArgs& a, hipStream_t stream);

@@ -413,50 +413,55 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillGemmArgs
 }
 
 // ----------------------------------------------------------------------------
-// Quantised grouped GEMM (FP8, MXFP4) on direct-to-LDS loads
+// Quantised grouped GEMM (FP8, MXFP4) on direct-to-LDS copies
 //
-// A workgroup computes 256 weight rows x 128 routes; wave w owns weight rows
-// 64w..64w+63 of the tile (four 16-row MFMA tiles) against all 128 routes
-// (eight 16-column tiles).  Every operand of a 128-deep K step -- the wave's
-// weight rows, the activation tile, the weight scales and the activation
-// scales -- is copied global -> LDS by the LDS-DMA form of the global loads
-// (no register staging), into a ring of three stages: the copies of step kb+2
-// are in flight while step kb computes.  The waits are explicit (vmcnt of the
-// copies of one step) and the barrier is a bare s_barrier, so a barrier never
-// drains the copies still in flight.
+// A workgroup of 8 waves computes 256 weight rows x 256 routes (kQBM).  Wave w
+// is row group rg = w/2 (64 weight rows: four 16-row MFMA tiles) and column
+// half ch = w%2 (128 routes: eight 16-column tiles); two waves share each SIMD,
+// so one wave's MFMAs run while the other waits on LDS, folds scales or sits at
+// the barrier.  Every operand of a 128-deep K step -- weight rows, activation
+// tile, weight scales, activation scales -- is copied global -> LDS by the
+// LDS-DMA form of the global loads (no register staging) into a ring of
+// kStages stages: the copies of the next kStages-1 steps are in flight while a
+// step computes.  Waits are explicit (vmcnt of one step's copies) and the
+// barrier is a bare s_barrier, so a barrier never drains copies in flight.
 //
-// LDS rows are 128-byte (FP8; 64-byte MXFP4 weights) lines of 16-byte chunks
-// stored XOR-swizzled by the line index, so the MFMA operand reads of eight
-// lanes hit eight different bank groups.
+// LDS lines (a weight row or an activation column of one K step: 128 bytes,
+// 64 for MXFP4 weights) are stored as 16-byte chunks XOR-swizzled by the line
+// index, so the operand reads of eight lanes hit eight different bank groups.
 //
-// Gate/up: wave w owns gate rows n0+32w+[0,32) and up rows I+n0+32w+[0,32), so
-// SwiGLU pairs registers; a workgroup covers 128 intermediate features.
-// Down: rows at or past N (the last tile when N % 256 != 0) are read clamped
-// to row N-1 and never stored.
+// Gate/up: row group rg owns gate rows n0+32rg+[0,32) and up rows
+// I+n0+32rg+[0,32), so SwiGLU pairs registers; a workgroup covers 128
+// intermediate features.  Down: rows at or past N (the last tile when
+// N % 256 != 0) are read clamped to row N-1 and never stored.
 //
 // Schedule (map_tile_q): the active workgroups are laid out XCD-major
 // (workgroup b runs on XCD b % 8), so each XCD works through a contiguous range
-// of the logical order, in which chunks of 4 M blocks of one expert sweep its N
-// tiles: the 32 workgroups an XCD runs at once read 8 weight tiles (many
-// distinct weight bytes in flight, each fetched into the XCD's L2 once per
-// chunk) and share 4 M blocks of activations.
+// of the logical order, in which chunks of kQChunk M blocks of one expert sweep
+// its N tiles: the workgroups an XCD runs at once read several weight tiles and
+// share the activations of a few M blocks.
 // ----------------------------------------------------------------------------
+constexpr int kQBM = 256;     // routes per tile (align block size of the quantised formats)
 constexpr int kQRows = 256;   // weight rows per workgroup
-constexpr int kQStages = 3;
+constexpr int kQThreads = 512;
 constexpr int kXcds = 8;
+constexpr int kQChunk = 4;
 
 template <int FMT>
 struct QLds {
+  static constexpr int kStages = FMT == FMT_FP8 ? 2 : 3;
   static constexpr int kALine = FMT == FMT_FP8 ? 128 : 64;   // weight bytes per row per K step
-  static constexpr int kA = 16 * 16 * kALine;                 // 4 waves x 4 tiles x 16 rows
-  static constexpr int kAS = FMT == FMT_FP8 ? 16 * 16 : 256 * 4;  // fp8: float per tile (16 B per wave); mxfp4: 4 codes per row
-  static constexpr int kB = kPBM * 128;
-  static constexpr int kBS = kPBM * 4;
+  static constexpr int kA = kQRows * kALine;
+  static constexpr int kAS = FMT == FMT_FP8 ? 4 * 16 : kQRows * 4;  // fp8: 4 floats per row group; mxfp4: 4 codes per row
+  static constexpr int kB = kQBM * 128;
+  static constexpr int kBS = kQBM * 4;
   static constexpr int kOffAS = kA, kOffB = kA + kAS, kOffBS = kA + kAS + kB;
   static constexpr int kStage = kA + kAS + kB + kBS;
-  static constexpr int kTotal = kQStages * kStage;
+  static constexpr int kTotal = kStages * kStage;
+  static constexpr int kACopies = kA / 1024 / 8;   // 1 KB copies per wave per step
+  static constexpr int kBCopies = kB / 1024 / 8;
   // LDS-DMA instructions each wave issues per K step (uniform over waves)
-  static constexpr int kDmaPerStep = FMT == FMT_FP8 ? 8 + 1 + 4 + 1 : 4 + 1 + 4 + 1;
+  static constexpr int kDmaPerStep = kACopies + kBCopies + 1;
 };
 
 __device__ __forceinline__ int xcd_major(int b, int n) {
@@ -465,13 +470,8 @@ __device__ __forceinline__ int xcd_major(int b, int n) {
   return x * per + min(x, rem) + i;
 }
 
-// M blocks that run next to each other on one weight tile
-constexpr int kQChunk = 4;
-
 // (M block, N tile) of position `local` in a group of nb M blocks x ntiles:
-// chunks of kQChunk M blocks, each chunk sweeping all N tiles, so a window of
-// 32 consecutive workgroups reads 8 different weight tiles (weights in flight
-// from 8 places) while sharing the activations of 4 M blocks.
+// chunks of kQChunk M blocks, each chunk sweeping all N tiles.
 __device__ __forceinline__ void chunked(int local, int nb, int ntiles, int& m, int& ntile) {
   const int full = nb / kQChunk, rem = nb - full * kQChunk;
   const int span = kQChunk * ntiles;
@@ -492,7 +492,7 @@ __device__ __forceinline__ void chunked(int local, int nb, int ntiles, int& m, i
 // count, so every XCD gets the same share.  Returns false for idle ones.
 __device__ __forceinline__ bool map_tile_q(const PrefillGemmArgs& a, int b, bool& shared, int& expert, int& mblock,
                                            int& ntile) {
-  const int routed = (a.cum[a.num_experts] / kPBM) * a.ntiles;
+  const int routed = (a.cum[a.num_experts] / kQBM) * a.ntiles;
   const int total = routed + a.shared_blocks * a.ntiles;
   if (b >= total) return false;
   const int wg = xcd_major(b, total);
@@ -500,10 +500,10 @@ __device__ __forceinline__ bool map_tile_q(const PrefillGemmArgs& a, int b, bool
     int lo = 0, hi = a.num_experts;  // largest e with cum[e]/BM * ntiles <= wg
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if ((a.cum[mid] / kPBM) * a.ntiles <= wg) lo = mid; else hi = mid;
+      if ((a.cum[mid] / kQBM) * a.ntiles <= wg) lo = mid; else hi = mid;
     }
-    const int b0 = a.cum[lo] / kPBM;
-    const int nb = a.cum[lo + 1] / kPBM - b0;
+    const int b0 = a.cum[lo] / kQBM;
+    const int nb = a.cum[lo + 1] / kQBM - b0;
     int m;
     chunked(wg - b0 * a.ntiles, nb, a.ntiles, m, ntile);
     shared = false;
@@ -543,11 +543,12 @@ __device__ __forceinline__ void lds_copy4(const uint8_t* src, uint8_t* dst) {
 __device__ __forceinline__ void pin(f32x4& v) { asm volatile("" : "+v"(v)); }
 
 template <int FMT, int GATE_UP>
-__global__ void __launch_bounds__(kPThreads) prefill_qgemm_kernel(PrefillGemmArgs a) {
+__global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArgs a) {
   using L = QLds<FMT>;
+  constexpr int D = L::kStages - 1;  // prefetch distance in K steps
   extern __shared__ __attribute__((aligned(16))) uint8_t q_lds[];
-  __shared__ int s_row[kPBM];
-  __shared__ int s_route[kPBM];
+  __shared__ int s_row[kQBM];
+  __shared__ int s_route[kQBM];
 
   bool shared;
   int expert, mblock, ntile;
@@ -556,18 +557,19 @@ __global__ void __launch_bounds__(kPThreads) prefill_qgemm_kernel(PrefillGemmArg
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = tid / kWave;
+  const int rg = wave >> 1, ch = wave & 1;
   const int r16 = lane & 15, g = lane >> 4;
 
-  if (tid < kPBM) {
+  if (tid < kQBM) {
     int row = -1, route = -1;
     if (shared) {
-      const int t = mblock * kPBM + tid;
+      const int t = mblock * kQBM + tid;
       if (t < a.M) {
         route = t;
         row = a.x_token_rows ? t : a.numel + t;
       }
     } else {
-      const int rr = a.sorted[mblock * kPBM + tid];
+      const int rr = a.sorted[mblock * kQBM + tid];
       if (rr < a.numel) {
         route = rr;
         row = a.x_token_rows ? rr / a.k : rr;
@@ -582,76 +584,68 @@ __global__ void __launch_bounds__(kPThreads) prefill_qgemm_kernel(PrefillGemmArg
   const int K = a.K, nkb = K / 128;
   const size_t rb = FMT == FMT_FP8 ? static_cast<size_t>(K) : static_cast<size_t>(K) / 2;
   const uint8_t* wexp = bank.w + static_cast<size_t>(expert) * a.N * rb;
-
-  // the wave's four weight tiles
   const int n0 = GATE_UP ? ntile * (kQRows / 2) : ntile * kQRows;
-  int trow[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (GATE_UP) trow[j] = (j < 2 ? 0 : a.inter) + n0 + 32 * wave + 16 * (j & 1);
-    else trow[j] = n0 + 64 * wave + 16 * j;
-  }
+  // first weight row of tile j of row group q
+  auto trow_of = [&](int q, int j) -> int {
+    if (GATE_UP) return (j < 2 ? 0 : a.inter) + n0 + 32 * q + 16 * (j & 1);
+    return n0 + 64 * q + 16 * j;
+  };
 
   // ---- per-lane sources of the copies (K step 0; step kb adds kb * step bytes)
-  // weights: FP8 tile j is 2 copies of 8 rows x 8 chunks, MXFP4 one copy of 16 rows x 4 chunks
-  constexpr int kACopies = FMT == FMT_FP8 ? 8 : 4;
-  const uint8_t* asrc[kACopies];
+  // weights: copy c of wave w fills LDS rows of 1 KB block i = w*kACopies + c
+  const uint8_t* asrc[L::kACopies];
 #pragma unroll
-  for (int c = 0; c < kACopies; ++c) {
-    int r, q;
+  for (int c = 0; c < L::kACopies; ++c) {
+    const int i = wave * L::kACopies + c;
+    int R, q;
     if constexpr (FMT == FMT_FP8) {
-      const int j = c >> 1, h = c & 1;
-      r = 8 * h + (lane >> 3);
-      q = (lane & 7) ^ (r & 7);
-      asrc[c] = wexp + static_cast<size_t>(min(trow[j] + r, a.N - 1)) * rb + q * 16;
+      R = 8 * i + (lane >> 3);
+      q = (lane & 7) ^ (R & 7);
     } else {
-      const int j = c;
-      r = lane >> 2;
-      q = (lane & 3) ^ ((r >> 1) & 3);
-      asrc[c] = wexp + static_cast<size_t>(min(trow[j] + r, a.N - 1)) * rb + q * 16;
+      R = 16 * i + (lane >> 2);
+      q = (lane & 3) ^ ((R >> 1) & 3);
     }
+    const int row = min(trow_of(R >> 6, (R >> 4) & 3) + (R & 15), a.N - 1);
+    asrc[c] = wexp + static_cast<size_t>(row) * rb + q * 16;
   }
-  // weight scales: FP8 lanes 0..3 -> the float of tile `lane`; MXFP4 lane -> the 4 codes of row 16(lane/16)+lane%16
-  const uint8_t* wssrc;
-  if constexpr (FMT == FMT_FP8) {
-    const int j = lane & 3;
-    wssrc = static_cast<const uint8_t*>(bank.s) +
-            ((static_cast<size_t>(expert) * (a.N / 128) + min(trow[j], a.N - 1) / 128) * nkb) * 4;
+  // scales: waves 0-3 copy their row group's weight scales, waves 4-7 64
+  // activation-scale columns each
+  const uint8_t* ssrc;
+  uint8_t* const sdst_base = q_lds + (wave < 4 ? (FMT == FMT_FP8 ? L::kOffAS + wave * 16 : L::kOffAS + wave * 256)
+                                               : L::kOffBS + (wave - 4) * 256);
+  if (wave < 4) {
+    if constexpr (FMT == FMT_FP8) {
+      const int j = lane & 3;
+      ssrc = static_cast<const uint8_t*>(bank.s) +
+             ((static_cast<size_t>(expert) * (a.N / 128) + min(trow_of(wave, j), a.N - 1) / 128) * nkb) * 4;
+    } else {
+      const int row = min(trow_of(wave, lane >> 4) + (lane & 15), a.N - 1);
+      ssrc = static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(expert) * a.N + row) * (K / 32);
+    }
   } else {
-    const int row = min(trow[lane >> 4] + (lane & 15), a.N - 1);
-    wssrc = static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(expert) * a.N + row) * (K / 32);
+    const int col = 64 * (wave - 4) + lane;
+    ssrc = static_cast<const uint8_t*>(a.xs) + static_cast<size_t>(s_row[col] < 0 ? 0 : s_row[col]) * nkb * 4;
   }
-  // activations: copy c (0..3) of wave w moves 8 columns x 8 chunks
-  const uint8_t* bsrc[4];
+  const bool scopy = wave >= 4 || FMT != FMT_FP8 || lane < 4;
+  // activations: copy c of wave w fills LDS columns of 1 KB block i = w*kBCopies + c
+  const uint8_t* bsrc[L::kBCopies];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int col = 8 * (4 * wave + c) + (lane >> 3);
+  for (int c = 0; c < L::kBCopies; ++c) {
+    const int col = 8 * (wave * L::kBCopies + c) + (lane >> 3);
     const int q = (lane & 7) ^ (col & 7);
     const int row = s_row[col] < 0 ? 0 : s_row[col];  // padding columns compute on row 0, never stored
     bsrc[c] = a.xq + static_cast<size_t>(row) * K + q * 16;
   }
-  // activation scales: lanes 0..31 of wave w -> column 32w + lane
-  const int scol = 32 * wave + (lane & 31);
-  const uint8_t* xssrc =
-      static_cast<const uint8_t*>(a.xs) + static_cast<size_t>(s_row[scol] < 0 ? 0 : s_row[scol]) * nkb * 4;
 
   auto issue = [&](int kb) {
-    uint8_t* st = q_lds + (kb % kQStages) * L::kStage;
+    uint8_t* st = q_lds + (kb % L::kStages) * L::kStage;
     const size_t ka = static_cast<size_t>(kb) * L::kALine;
 #pragma unroll
-    for (int c = 0; c < kACopies; ++c) {
-      uint8_t* dst = st + (FMT == FMT_FP8 ? (wave * 4 + (c >> 1)) * 2048 + (c & 1) * 1024 : (wave * 4 + c) * 1024);
-      lds_copy16(asrc[c] + ka, dst);
-    }
-    if constexpr (FMT == FMT_FP8) {
-      if (lane < 4) lds_copy4(wssrc + kb * 4, st + L::kOffAS + wave * 16);
-    } else {
-      lds_copy4(wssrc + kb * 4, st + L::kOffAS + wave * 256);
-    }
+    for (int c = 0; c < L::kACopies; ++c) lds_copy16(asrc[c] + ka, st + (wave * L::kACopies + c) * 1024);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      lds_copy16(bsrc[c] + static_cast<size_t>(kb) * 128, st + L::kOffB + (4 * wave + c) * 1024);
-    if (lane < 32) lds_copy4(xssrc + kb * 4, st + L::kOffBS + wave * 128);
+    for (int c = 0; c < L::kBCopies; ++c)
+      lds_copy16(bsrc[c] + static_cast<size_t>(kb) * 128, st + L::kOffB + (wave * L::kBCopies + c) * 1024);
+    if (scopy) lds_copy4(ssrc + kb * 4, sdst_base + (kb % L::kStages) * L::kStage);
   };
 
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -662,28 +656,27 @@ __global__ void __launch_bounds__(kPThreads) prefill_qgemm_kernel(PrefillGemmArg
     for (int i = 0; i < 8; ++i) acc[j][i] = zero;
 
   auto compute = [&](int kb) {
-    const uint8_t* st = q_lds + (kb % kQStages) * L::kStage;
-    // weight operands of the four tiles
+    const uint8_t* st = q_lds + (kb % L::kStages) * L::kStage;
     i32x8 wf[4];
     int wcode[4];
     float sw[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const int R = 64 * rg + 16 * j + r16;
       if constexpr (FMT == FMT_FP8) {
-        const uint8_t* p = st + (wave * 4 + j) * 2048 + r16 * 128;
-        const u32x4 lo = *reinterpret_cast<const u32x4*>(p + (((2 * g) ^ (r16 & 7)) * 16));
-        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + (((2 * g + 1) ^ (r16 & 7)) * 16));
+        const uint8_t* p = st + R * 128;
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(p + (((2 * g) ^ (R & 7)) * 16));
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + (((2 * g + 1) ^ (R & 7)) * 16));
         wf[j] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-        sw[j] = *reinterpret_cast<const float*>(st + L::kOffAS + wave * 16 + j * 4);
+        sw[j] = *reinterpret_cast<const float*>(st + L::kOffAS + rg * 16 + j * 4);
       } else {
-        const uint8_t* p = st + (wave * 4 + j) * 1024 + r16 * 64;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(p + ((g ^ ((r16 >> 1) & 3)) * 16));
+        const u32x4 v = *reinterpret_cast<const u32x4*>(st + R * 64 + ((g ^ ((R >> 1) & 3)) * 16));
         wf[j] = i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
-        wcode[j] = st[L::kOffAS + (wave * 64 + 16 * j + r16) * 4 + g];
+        wcode[j] = st[L::kOffAS + R * 4 + g];
       }
     }
     auto read_x = [&](int i, i32x8& xf, uint32_t& xs) {
-      const int col = 16 * i + r16;
+      const int col = 128 * ch + 16 * i + r16;
       const uint8_t* p = st + L::kOffB + col * 128;
       u32x4 lo, hi;
       if constexpr (FMT == FMT_FP8) {
@@ -699,9 +692,8 @@ __global__ void __launch_bounds__(kPThreads) prefill_qgemm_kernel(PrefillGemmArg
       xs = *reinterpret_cast<const uint32_t*>(st + L::kOffBS + col * 4);
     };
     // The next column tile's LDS reads are issued before this tile's MFMAs.
-    // FP8: every MFMA is followed by the scale fold of the previous one; the
-    // empty asm pins each fold there, so the VALU work runs while the matrix
-    // core is busy instead of piling up after the last MFMA.
+    // FP8: every MFMA is followed by the scale fold of the previous one; pin()
+    // keeps each fold there, so the VALU work runs while the matrix core is busy.
     i32x8 xf[2];
     uint32_t xs[2];
     read_x(0, xf[0], xs[0]);
@@ -731,27 +723,28 @@ __global__ void __launch_bounds__(kPThreads) prefill_qgemm_kernel(PrefillGemmArg
     if constexpr (FMT == FMT_FP8) acc[3][7] += tp * fp;
   };
 
-  // K pipeline over a ring of three LDS stages
-  issue(0);
-  if (nkb > 1) issue(1);
-  if (nkb > 1) wait_vm<L::kDmaPerStep>();
+  // K pipeline over a ring of kStages LDS stages: copies run D steps ahead
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (d < nkb) issue(d);
+  if (D == 2 && nkb > 1) wait_vm<L::kDmaPerStep>();
   else wait_vm<0>();
   bare_barrier();
   for (int kb = 0; kb < nkb; ++kb) {
-    if (kb + 2 < nkb) issue(kb + 2);
+    if (kb + D < nkb) issue(kb + D);
     compute(kb);
-    // step kb+1's copies must have landed (step kb+2's may still fly); every
+    // step kb+1's copies must have landed (later ones may still fly); every
     // LDS read of this step has returned before its MFMA used it
-    if (kb + 2 < nkb) wait_vm<L::kDmaPerStep>();
+    if (D == 2 && kb + 2 < nkb) wait_vm<L::kDmaPerStep>();
     else wait_vm<0>();
     wait_lgkm0();
     bare_barrier();
   }
 
-  // ---- epilogue: lane holds rows trow[j] + g*4 + v of route column 16i + r16
+  // ---- epilogue: lane holds rows trow + g*4 + v of route column 128ch + 16i + r16
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int col = 16 * i + r16;
+    const int col = 128 * ch + 16 * i + r16;
     const int route = s_route[col];
     if (route < 0) continue;
     if (GATE_UP) {
@@ -765,7 +758,7 @@ __global__ void __launch_bounds__(kPThreads) prefill_qgemm_kernel(PrefillGemmArg
           const float uu = bf16_round(acc[2 + s2][i][v]);
           o[v] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
         }
-        const int n = n0 + 32 * wave + 16 * s2 + g * 4;
+        const int n = n0 + 32 * rg + 16 * s2 + g * 4;
         uint2 pk;
         pk.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
         pk.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
@@ -776,7 +769,7 @@ __global__ void __launch_bounds__(kPThreads) prefill_qgemm_kernel(PrefillGemmArg
       uint16_t* dst = shared ? a.sh_out + static_cast<size_t>(route) * a.N : a.out + static_cast<size_t>(route) * a.N;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int n = trow[j] + g * 4;
+        const int n = trow_of(rg, j) + g * 4;
         if (n >= a.N) continue;
         uint16_t o[4];
 #pragma unroll
@@ -827,7 +820,7 @@ static hipError_t launch_qgemm_t(PrefillGemmArgs a, hipStream_t stream) {
   }
   a.ntiles = GU ? a.inter / (kQRows / 2) : (a.N + kQRows - 1) / kQRows;
   const int wgs = (a.max_blocks + a.shared_blocks) * a.ntiles;
-  hipLaunchKernelGGL((prefill_qgemm_kernel<FMT, GU>), dim3(wgs), dim3(kPThreads), QLds<FMT>::kTotal, stream, a);
+  hipLaunchKernelGGL((prefill_qgemm_kernel<FMT, GU>), dim3(wgs), dim3(kQThreads), QLds<FMT>::kTotal, stream, a);
   return hipGetLastError();
 }
 
