@@ -356,6 +356,19 @@ def cpu_baseline(layer: DecodeLayer, M: int, budget_s: float, gen, dev):
 
 # ----------------------------------------------------------------------------- main
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_c4_b64_gate_up_traffic.json")
+
+
+def measured_traffic(batch: int):
+    """HBM bytes per launch of the gate_up kernel, from the two rocprofv3 counter
+    runs (FETCH_SIZE, WRITE_SIZE, each scaled by a 1 GiB copy) summarised in
+    profiles/; only for the workload they were measured on, else None."""
+    if batch != 64 or not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as f:
+        return int(json.load(f)["traffic_bytes_per_launch"])
+
+
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -394,7 +407,7 @@ def main() -> int:
     gu_us = head["stage_us"]["gate_up"]
     gu_gbs = head["gate_up_bytes_per_launch"] / (gu_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.batch),
                 "kernel": "decode_stage_kernel<FP8,FP8,0> (gate_up + SwiGLU)",
                 "avg_launch_us": round(gu_us, 2),
                 "algorithmic_bytes_per_launch": int(head["gate_up_bytes_per_launch"])}
