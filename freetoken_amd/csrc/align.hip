@@ -226,6 +226,189 @@ __global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
   }
 }
 
+// ----------------------------------------------------------------------------
+// Multi-workgroup align for large route counts (prefill): the same stable
+// order, with the routes cut into B workgroups x 16 contiguous wave chunks.
+//   align_count_kernel:   per (wave, expert) counts -> wcnt[B*16][eff] and per
+//                         (workgroup, expert) totals -> btot[B][eff]; fills
+//                         sorted_ids with the sentinel.
+//   align_scan_kernel:    one workgroup: per expert, exclusive prefix of the
+//                         workgroup totals; padded region starts; expert_ids;
+//                         btot becomes the absolute base of every workgroup.
+//   align_scatter_kernel: per workgroup, wave bases = workgroup base + prefix
+//                         of the earlier waves' counts; each wave walks its
+//                         chunk in 64-route batches, the 64-key bitonic rank
+//                         giving every route its slot.
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ void chunk_of(int numel, int gw, int waves, int& c0, int& c1) {
+  const int chunk = ((numel + waves - 1) / waves + kWave - 1) / kWave * kWave;
+  c0 = min(numel, gw * chunk);
+  c1 = min(numel, c0 + chunk);
+}
+
+__global__ void __launch_bounds__(kAlignThreads) align_count_kernel(AlignArgs a, int32_t* wcnt, int32_t* btot) {
+  extern __shared__ int lds[];
+  const int eff = a.num_experts + 1;
+  int* wcount = lds;  // [kAlignWaves][eff]
+  const int tid = threadIdx.x, lane = lane_id(), w = tid / kWave;
+  const int waves = gridDim.x * kAlignWaves, gw = blockIdx.x * kAlignWaves + w;
+  for (int i = tid; i < kAlignWaves * eff; i += kAlignThreads) wcount[i] = 0;
+  for (int i = blockIdx.x * kAlignThreads + tid; i < a.max_padded; i += gridDim.x * kAlignThreads)
+    a.sorted_ids[i] = a.numel;
+  __syncthreads();
+  int c0, c1;
+  chunk_of(a.numel, gw, waves, c0, c1);
+  for (int i = c0 + lane; i < c1; i += kWave) {
+    const int e = a.ids[i];
+    if (e >= 0 && e < eff) atomicAdd(&wcount[w * eff + e], 1);
+  }
+  __syncthreads();
+  for (int i = tid; i < kAlignWaves * eff; i += kAlignThreads)
+    wcnt[static_cast<size_t>(blockIdx.x * kAlignWaves) * eff + i] = wcount[i];
+  for (int e = tid; e < eff; e += kAlignThreads) {
+    int t = 0;
+#pragma unroll
+    for (int v = 0; v < kAlignWaves; ++v) t += wcount[v * eff + e];
+    btot[static_cast<size_t>(blockIdx.x) * eff + e] = t;
+  }
+}
+
+__global__ void __launch_bounds__(kAlignThreads) align_scan_kernel(AlignArgs a, int32_t* btot, int blocks) {
+  extern __shared__ int lds[];
+  const int eff = a.num_experts + 1;
+  int* cum = lds;            // [eff + 1]
+  int* cnt = cum + eff + 1;  // [eff]
+  __shared__ int s_tmp[2 * kAlignWaves];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < eff; e += kAlignThreads) {
+    int acc = 0;
+    for (int b = 0; b < blocks; ++b) {
+      const size_t at = static_cast<size_t>(b) * eff + e;
+      const int t = btot[at];
+      btot[at] = acc;
+      acc += t;
+    }
+    cnt[e] = acc;
+  }
+  __syncthreads();
+  const int per = (eff + kAlignThreads - 1) / kAlignThreads;
+  int local = 0;
+  for (int q = 0; q < per; ++q) {
+    const int e = tid * per + q;
+    if (e < eff) local += (cnt[e] + a.block_size - 1) / a.block_size * a.block_size;
+  }
+  int total = 0;
+  int pre = block_exclusive_scan(local, s_tmp, &total);
+  for (int q = 0; q < per; ++q) {
+    const int e = tid * per + q;
+    if (e < eff) {
+      cum[e] = pre;
+      if (a.cum_out) a.cum_out[e] = pre;
+      pre += (cnt[e] + a.block_size - 1) / a.block_size * a.block_size;
+    }
+  }
+  if (tid == 0) {
+    cum[eff] = total;
+    if (a.cum_out) a.cum_out[eff] = total;
+    a.ntpp[0] = total;
+  }
+  __syncthreads();
+  for (int b = tid; b < a.max_blocks; b += kAlignThreads) {
+    int e = -1;
+    if (b * a.block_size < total) {
+      int lo = 0, hi = eff;  // largest e with cum[e] <= b*bs
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (cum[mid] <= b * a.block_size) lo = mid; else hi = mid;
+      }
+      e = lo;
+    }
+    a.expert_ids[b] = e;
+  }
+  for (int i = tid; i < blocks * eff; i += kAlignThreads) btot[i] += cum[i % eff];
+}
+
+__global__ void __launch_bounds__(kAlignThreads) align_scatter_kernel(AlignArgs a, const int32_t* wcnt,
+                                                                      const int32_t* btot) {
+  extern __shared__ int lds[];
+  const int eff = a.num_experts + 1;
+  int* wbase = lds;  // [kAlignWaves][eff]
+  const int tid = threadIdx.x, lane = lane_id(), w = tid / kWave;
+  const int waves = gridDim.x * kAlignWaves, gw = blockIdx.x * kAlignWaves + w;
+  const int32_t* mine = wcnt + static_cast<size_t>(blockIdx.x * kAlignWaves) * eff;
+  for (int e = tid; e < eff; e += kAlignThreads) {
+    int acc = btot[static_cast<size_t>(blockIdx.x) * eff + e];
+#pragma unroll
+    for (int v = 0; v < kAlignWaves; ++v) {
+      wbase[v * eff + e] = acc;
+      acc += mine[v * eff + e];
+    }
+  }
+  __syncthreads();
+  int c0, c1;
+  chunk_of(a.numel, gw, waves, c0, c1);
+  for (int base = c0; base < c1; base += kWave) {
+    const int i = base + lane;
+    const int e = i < c1 ? a.ids[i] : -1;
+    const bool valid = e >= 0 && e < eff;
+    uint32_t key = (static_cast<uint32_t>(valid ? e : 0xFFFFF) << 6) | static_cast<uint32_t>(lane);
+#pragma unroll
+    for (int k = 2; k <= kWave; k <<= 1) {
+#pragma unroll
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const uint32_t other = __shfl_xor(key, j, kWave);
+        const bool up = (lane & k) == 0;
+        const bool lower = (lane & j) == 0;
+        key = (lower == up) ? min(key, other) : max(key, other);
+      }
+    }
+    const int se = static_cast<int>(key >> 6);
+    const int prev = __shfl(se, lane == 0 ? 0 : lane - 1, kWave);
+    const int next = __shfl(se, lane == kWave - 1 ? lane : lane + 1, kWave);
+    const bool head = lane == 0 || prev != se;
+    const bool tail = lane == kWave - 1 || next != se;
+    const unsigned long long heads = __ballot(head);
+    const unsigned long long upto = (lane == kWave - 1) ? ~0ull : ((2ull << lane) - 1ull);
+    const int run_start = kWave - 1 - __clzll(heads & upto);
+    const int rank = lane - run_start;
+    if (se < eff) a.sorted_ids[wbase[w * eff + se] + rank] = base + static_cast<int>(key & 63u);
+    // the wave reads its bases (above) before this write
+    if (se < eff && tail) wbase[w * eff + se] += rank + 1;
+  }
+}
+
+int align_grid_blocks(int numel) {
+  const int b = (numel + 4095) / 4096;  // ~4 K routes per workgroup (256 per wave)
+  return b < 1 ? 1 : (b > 64 ? 64 : b);
+}
+
+size_t align_gcount_ints(int numel, int num_experts) {
+  return static_cast<size_t>(align_grid_blocks(numel)) * (kAlignWaves + 1) * (num_experts + 1);
+}
+
+hipError_t launch_align_large(const AlignArgs& a, int32_t* gcount, hipStream_t stream) {
+  const int eff = a.num_experts + 1;
+  const int blocks = align_grid_blocks(a.numel);
+  int32_t* wcnt = gcount;                                                   // [blocks * 16][eff]
+  int32_t* btot = gcount + static_cast<size_t>(blocks) * kAlignWaves * eff;  // [blocks][eff]
+  const size_t lds_w = sizeof(int) * static_cast<size_t>(kAlignWaves) * eff;
+  const size_t lds_s = sizeof(int) * (2 * static_cast<size_t>(eff) + 1);
+  static bool attr_set = false;
+  if (!attr_set) {
+    for (const void* f : {reinterpret_cast<const void*>(align_count_kernel),
+                          reinterpret_cast<const void*>(align_scatter_kernel)}) {
+      const hipError_t err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
+      if (err != hipSuccess) return err;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(align_count_kernel, dim3(blocks), dim3(kAlignThreads), lds_w, stream, a, wcnt, btot);
+  hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(kAlignThreads), lds_s, stream, a, btot, blocks);
+  hipLaunchKernelGGL(align_scatter_kernel, dim3(blocks), dim3(kAlignThreads), lds_w, stream, a,
+                     static_cast<const int32_t*>(wcnt), static_cast<const int32_t*>(btot));
+  return hipGetLastError();
+}
+
 size_t align_lds_bytes(int num_experts, int table_size, bool stats) {
   const int eff = num_experts + 1;
   return sizeof(int) * (static_cast<size_t>(kAlignWaves) * eff + (eff + 1) + eff + (stats ? table_size : 0));

@@ -142,6 +142,7 @@ struct PrefillLayout {
   int32_t* expert_ids;
   int32_t* ntpp;
   int32_t* cum;
+  int32_t* gcount;  // per-wave counts of the multi-workgroup align
   uint8_t* xq;
   void* xs;
   uint16_t* act;
@@ -163,6 +164,7 @@ PrefillLayout prefill_layout(void* ws, int M, int k, const ftmoe_bank* bank, con
   L.expert_ids = c.take<int32_t>(L.max_blocks);
   L.ntpp = c.take<int32_t>(1);
   L.cum = c.take<int32_t>(bank->num_rows + 2);
+  L.gcount = c.take<int32_t>(ftmoe::align_gcount_ints(numel, bank->num_rows));
   const bool quant = bank->format != FTMOE_FMT_BF16;
   const size_t sc = 4;  // float scale (FP8) or e8m0 code in 32 bits (MXFP4)
   const size_t rows = static_cast<size_t>(numel) + (shared ? M : 0);
@@ -170,10 +172,12 @@ PrefillLayout prefill_layout(void* ws, int M, int k, const ftmoe_bank* bank, con
     L.xq = c.take<uint8_t>(static_cast<size_t>(M) * H);
     L.xs = c.take<uint8_t>(static_cast<size_t>(M) * (H / 128) * sc);
   }
-  L.act = c.take<uint16_t>(rows * I);
-  if (quant) {
+  if (quant) {  // the gate/up GEMM writes the quantised activations directly
+    L.act = nullptr;
     L.actq = c.take<uint8_t>(rows * I);
     L.as = c.take<uint8_t>(rows * (I / 128) * sc);
+  } else {
+    L.act = c.take<uint16_t>(rows * I);
   }
   L.ic3 = c.take<uint16_t>(static_cast<size_t>(numel) * H);
   L.sh_out = shared ? c.take<uint16_t>(static_cast<size_t>(M) * H) : nullptr;
@@ -411,7 +415,7 @@ int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, 
   al.ntpp = L.ntpp;
   al.cum_out = L.cum;
   g_timer.start_call(stream);
-  rc = check_hip(ftmoe::launch_align(al, stream), "experts_prefill align");
+  rc = check_hip(ftmoe::launch_align_large(al, L.gcount, stream), "experts_prefill align");
   if (rc) return rc;
   g_timer.mark();
 
@@ -446,19 +450,15 @@ int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, 
   g.inter = I;
   g.w = {static_cast<const uint8_t*>(bank->gate_up), bank->gate_up_scale};
   if (shared) g.ws = {static_cast<const uint8_t*>(shared->gate_up), shared->gate_up_scale};
-  g.out = L.act;
+  g.out = L.act;  // bf16 act (bf16 format); FP8 / MXFP4 write act_q and act_s
+  g.act_q = L.actq;
+  g.act_s = L.as;
   rc = check_hip(ftmoe::launch_prefill_gemm(fmt, 1, g, stream), "experts_prefill gate_up");
   if (rc) return rc;
   g_timer.mark();
+  g_timer.mark();  // (the activation quantisation is fused into the gate/up epilogue)
 
   // down (x router weight) -> ic3 / shared out
-  const size_t rows = static_cast<size_t>(numel) + (shared ? M : 0);
-  if (fmt != FTMOE_FMT_BF16) {
-    rc = check_hip(ftmoe::launch_act_quant(qmode, L.act, static_cast<int>(rows), I, L.actq, L.as, stream),
-                   "experts_prefill act quant");
-    if (rc) return rc;
-  }
-  g_timer.mark();
   g.xq = fmt == FTMOE_FMT_BF16 ? reinterpret_cast<const uint8_t*>(L.act) : L.actq;
   g.xs = L.as;
   g.x_token_rows = 0;

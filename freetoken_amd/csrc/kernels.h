@@ -71,6 +71,10 @@ hipError_t launch_grouped_sigmoid(const float* logits, const float* bias, int M,
                                   int topk_group, int k, int renorm, float scale, float* w, int32_t* ids,
                                   hipStream_t stream);
 hipError_t launch_align(const AlignArgs& a, hipStream_t stream);
+// Multi-workgroup align for large route counts without slot lookup, stats or
+// segments; gcount: align_gcount_ints(numel, num_experts) ints of workspace.
+size_t align_gcount_ints(int numel, int num_experts);
+hipError_t launch_align_large(const AlignArgs& a, int32_t* gcount, hipStream_t stream);
 hipError_t launch_slot_map(const int32_t* ids, int numel, const int32_t* slot_for_id, int table_size,
                            int32_t* slot_ids, uint8_t* miss_mask, long long* stats, hipStream_t stream);
 hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream);
@@ -95,7 +99,9 @@ struct PrefillGemmArgs {
   BankView w;               // routed weights
   BankView ws;              // shared weights
   // outputs
-  uint16_t* out;            // gate_up: act [numel + M, inter]; down: ic3 [numel, N]
+  uint16_t* out;            // gate_up (bf16): act [numel + M, inter]; down: ic3 [numel, N]
+  uint8_t* act_q;           // gate_up (FP8, MXFP4): e4m3 act [numel + M, inter] ...
+  void* act_s;              // ... and its scales per 128 (float, or uint32 e8m0 codes)
   uint16_t* sh_out;         // down: shared out [M, N]
   const float* topk_w;      // [numel] (down)
   int act_kind;

@@ -43,6 +43,29 @@ constexpr int kPThreads = 256;
 //           codes stored as uint8; MODE 2: the same with codes stored as uint32
 //           (the grouped GEMM copies them to LDS in 4-byte units)
 // ----------------------------------------------------------------------------
+// Scale of one 128-value group with absolute maximum amax, shared by the
+// quantisation kernel and the gate/up epilogue so both give identical bytes.
+// MODE 0: returns s and sets mul = 0 (values are divided by s);
+// MODE 1/2: returns the e8m0 code e+127 as a float and sets mul = 2^-e.
+template <int MODE>
+__device__ __forceinline__ float group_scale(float amax, float& mul) {
+  if (MODE == 0) {
+    mul = 0.f;
+    return fmaxf(amax, 1e-10f) / 448.0f;
+  }
+  const float t = fmaxf(amax, 1e-4f) * 0x1.24924ap-9f;  // * (1/448) rounded to float
+  const uint32_t bits = __float_as_uint(t);
+  const int e = static_cast<int>((bits >> 23) & 0xff) - 127 + ((bits & 0x7fffff) ? 1 : 0);
+  mul = ldexpf(1.0f, -e);
+  return static_cast<float>(e + 127);
+}
+
+template <int MODE>
+__device__ __forceinline__ float quant_value(float x, float s, float mul) {
+  const float y = MODE == 0 ? __fdiv_rn(x, s) : x * mul;
+  return fminf(fmaxf(y, -448.0f), 448.0f);
+}
+
 template <int MODE>
 __global__ void __launch_bounds__(256) act_quant_kernel(const uint16_t* __restrict__ x, int rows, int K,
                                                         uint8_t* __restrict__ q, void* __restrict__ scales) {
@@ -52,31 +75,31 @@ __global__ void __launch_bounds__(256) act_quant_kernel(const uint16_t* __restri
   const uint32_t* xr = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(row) * K);
   uint16_t* qr = reinterpret_cast<uint16_t*>(q + static_cast<size_t>(row) * K);
   const int ng = K / 128;
-  for (int gi = 0; gi < ng; ++gi) {
-    const uint32_t pair = xr[gi * 64 + lane];
+  constexpr int kAhead = 4;  // groups whose loads are in flight together
+  for (int g0 = 0; g0 < ng; g0 += kAhead) {
+    uint32_t pairs[kAhead];
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) pairs[u] = g0 + u < ng ? xr[(g0 + u) * 64 + lane] : 0u;
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) {
+    const int gi = g0 + u;
+    if (gi >= ng) break;
+    const uint32_t pair = pairs[u];
     const float a = bf16_to_f32(static_cast<uint16_t>(pair & 0xffffu));
     const float b = bf16_to_f32(static_cast<uint16_t>(pair >> 16));
     const float amax = wave_max_f32(fmaxf(fabsf(a), fabsf(b)));
-    float qa, qb;
-    if (MODE == 0) {
-      const float s = fmaxf(amax, 1e-10f) / 448.0f;
-      qa = fminf(fmaxf(__fdiv_rn(a, s), -448.0f), 448.0f);
-      qb = fminf(fmaxf(__fdiv_rn(b, s), -448.0f), 448.0f);
-      if (lane == 0) static_cast<float*>(scales)[static_cast<size_t>(row) * ng + gi] = s;
-    } else {
-      const float t = fmaxf(amax, 1e-4f) * 0x1.24924ap-9f;  // * (1/448) rounded to float
-      const uint32_t bits = __float_as_uint(t);
-      const int e = static_cast<int>((bits >> 23) & 0xff) - 127 + ((bits & 0x7fffff) ? 1 : 0);
-      const float inv = ldexpf(1.0f, -e);
-      qa = fminf(fmaxf(a * inv, -448.0f), 448.0f);
-      qb = fminf(fmaxf(b * inv, -448.0f), 448.0f);
-      if (lane == 0) {
-        if (MODE == 1) static_cast<uint8_t*>(scales)[static_cast<size_t>(row) * ng + gi] = static_cast<uint8_t>(e + 127);
-        else static_cast<uint32_t*>(scales)[static_cast<size_t>(row) * ng + gi] = static_cast<uint32_t>(e + 127);
-      }
+    float mul;
+    const float s = group_scale<MODE>(amax, mul);
+    const float qa = quant_value<MODE>(a, s, mul), qb = quant_value<MODE>(b, s, mul);
+    if (lane == 0) {
+      const size_t at = static_cast<size_t>(row) * ng + gi;
+      if (MODE == 0) static_cast<float*>(scales)[at] = s;
+      else if (MODE == 1) static_cast<uint8_t*>(scales)[at] = static_cast<uint8_t>(s);
+      else static_cast<uint32_t*>(scales)[at] = static_cast<uint32_t>(s);
     }
     const uint32_t pk = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(qa, qb, 0, false));
     qr[gi * 64 + lane] = static_cast<uint16_t>(pk & 0xffffu);
+    }
   }
 }
 
@@ -742,13 +765,16 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
   }
 
   // ---- epilogue: lane holds rows trow + g*4 + v of route column 128ch + 16i + r16
+  if constexpr (GATE_UP) {
+    // SwiGLU, then the down GEMM's activation quantisation of this 128-feature
+    // group (one K group of the down GEMM) per route: amax over the 32 features
+    // of the wave (lanes g = 0..3 of a column) and over the 4 row groups (LDS).
+    constexpr int QMODE = FMT == FMT_FP8 ? 0 : 2;
+    uint32_t pk[8][2][2];  // bf16 pairs (v0,v1), (v2,v3) of each column tile and gate/up tile pair
+    float amax[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int col = 128 * ch + 16 * i + r16;
-    const int route = s_route[col];
-    if (route < 0) continue;
-    if (GATE_UP) {
-      const int arow = shared ? a.numel + route : route;
+    for (int i = 0; i < 8; ++i) {
+      float m = 0.f;
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         uint16_t o[4];
@@ -757,14 +783,55 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
           const float gg = bf16_round(acc[s2][i][v]);
           const float uu = bf16_round(acc[2 + s2][i][v]);
           o[v] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
+          m = fmaxf(m, fabsf(bf16_to_f32(o[v])));
         }
-        const int n = n0 + 32 * rg + 16 * s2 + g * 4;
-        uint2 pk;
-        pk.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
-        pk.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
-        *reinterpret_cast<uint2*>(a.out + static_cast<size_t>(arow) * a.inter + n) = pk;
+        pk[i][s2][0] = o[0] | (static_cast<uint32_t>(o[1]) << 16);
+        pk[i][s2][1] = o[2] | (static_cast<uint32_t>(o[3]) << 16);
       }
-    } else {
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      amax[i] = m;
+    }
+    float* s_amax = reinterpret_cast<float*>(q_lds);  // [4 row groups][kQBM columns]; the K ring is idle now
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (g == 0) s_amax[rg * kQBM + 128 * ch + 16 * i + r16] = amax[i];
+    __syncthreads();
+    const int ng = a.inter / 128;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int col = 128 * ch + 16 * i + r16;
+      const int route = s_route[col];
+      if (route < 0) continue;
+      const float m = fmaxf(fmaxf(s_amax[col], s_amax[kQBM + col]), fmaxf(s_amax[2 * kQBM + col], s_amax[3 * kQBM + col]));
+      float mul;
+      const float sc = group_scale<QMODE>(m, mul);
+      const int arow = shared ? a.numel + route : route;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        float vals[4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          vals[2 * h] = quant_value<QMODE>(bf16_to_f32(static_cast<uint16_t>(pk[i][s2][h] & 0xffffu)), sc, mul);
+          vals[2 * h + 1] = quant_value<QMODE>(bf16_to_f32(static_cast<uint16_t>(pk[i][s2][h] >> 16)), sc, mul);
+        }
+        uint32_t q4 = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(vals[0], vals[1], 0, false));
+        q4 = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(vals[2], vals[3], static_cast<int>(q4), true));
+        const int n = n0 + 32 * rg + 16 * s2 + g * 4;
+        *reinterpret_cast<uint32_t*>(a.act_q + static_cast<size_t>(arow) * a.inter + n) = q4;
+      }
+      if (rg == 0 && g == 0) {
+        const size_t at = static_cast<size_t>(arow) * ng + ntile;
+        if (QMODE == 0) static_cast<float*>(a.act_s)[at] = sc;
+        else static_cast<uint32_t*>(a.act_s)[at] = static_cast<uint32_t>(sc);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int col = 128 * ch + 16 * i + r16;
+      const int route = s_route[col];
+      if (route < 0) continue;
       const float wt = shared ? 1.0f : a.topk_w[route];
       uint16_t* dst = shared ? a.sh_out + static_cast<size_t>(route) * a.N : a.out + static_cast<size_t>(route) * a.N;
 #pragma unroll
@@ -774,10 +841,10 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
         uint16_t o[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(acc[j][i][v] * wt);
-        uint2 pk;
-        pk.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
-        pk.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
-        *reinterpret_cast<uint2*>(dst + n) = pk;
+        uint2 pk2;
+        pk2.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
+        pk2.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+        *reinterpret_cast<uint2*>(dst + n) = pk2;
       }
     }
   }
