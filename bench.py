@@ -379,6 +379,8 @@ def main() -> int:
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--prefill-only", choices=("fp8_block", "mxfp4"), default=None,
+                    help="profiling aid: run only the C5 prefill of this format and print its result")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
@@ -399,6 +401,11 @@ def main() -> int:
         b.copy_(a)
         torch.cuda.synchronize()
         del a, b
+
+    if args.prefill_only:
+        res = run_prefill(args.prefill_only, args.steps, args.warmup, gen, dev)
+        print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}), flush=True)
+        return 0
 
     log("[bench] building C4 layer (64 resident FP8 experts + shared)")
     c4 = DecodeLayer(C4, dev, gen)

@@ -451,7 +451,8 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillGemmArgs
 //
 // LDS lines (a weight row or an activation column of one K step: 128 bytes,
 // 64 for MXFP4 weights) are stored as 16-byte chunks XOR-swizzled by the line
-// index, so the operand reads of eight lanes hit eight different bank groups.
+// index (swz_pair, swz_b, swz64: patterns measured free of LDS bank conflicts
+// for the way each operand is read).
 //
 // Gate/up: row group rg owns gate rows n0+32rg+[0,32) and up rows
 // I+n0+32rg+[0,32), so SwiGLU pairs registers; a workgroup covers 128
@@ -561,6 +562,18 @@ __device__ __forceinline__ void lds_copy4(const uint8_t* src, uint8_t* dst) {
   __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
 }
 
+// Chunk swizzles of the LDS lines, chosen by measurement (rocprofv3
+// SQ_LDS_BANK_CONFLICT over ds_read_b128 patterns on gfx950): for 128-byte
+// lines read as chunk pairs (2g, 2g+1) -- the FP8 operands -- position
+// c ^ swz_pair(line) is conflict-free while c ^ (line & 7) is not; for lines
+// read as chunks (g, 4+g) -- the MXFP4 activations -- c ^ (line & 7) is
+// conflict-free; for 64-byte lines read as chunk g -- the MXFP4 weights --
+// c ^ ((line >> 1) & 3) is.
+__device__ __forceinline__ int swz_pair(int line) { return ((line & 3) << 1) | ((line >> 2) & 1); }
+template <int FMT>
+__device__ __forceinline__ int swz_b(int line) { return FMT == FMT_FP8 ? swz_pair(line) : (line & 7); }
+__device__ __forceinline__ int swz64(int line) { return (line >> 1) & 3; }
+
 // Empty asm that keeps the value's update at this point of the instruction
 // stream (no code is emitted).
 __device__ __forceinline__ void pin(f32x4& v) { asm volatile("" : "+v"(v)); }
@@ -623,10 +636,10 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
     int R, q;
     if constexpr (FMT == FMT_FP8) {
       R = 8 * i + (lane >> 3);
-      q = (lane & 7) ^ (R & 7);
+      q = (lane & 7) ^ swz_pair(R);
     } else {
       R = 16 * i + (lane >> 2);
-      q = (lane & 3) ^ ((R >> 1) & 3);
+      q = (lane & 3) ^ swz64(R);
     }
     const int row = min(trow_of(R >> 6, (R >> 4) & 3) + (R & 15), a.N - 1);
     asrc[c] = wexp + static_cast<size_t>(row) * rb + q * 16;
@@ -655,7 +668,7 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
 #pragma unroll
   for (int c = 0; c < L::kBCopies; ++c) {
     const int col = 8 * (wave * L::kBCopies + c) + (lane >> 3);
-    const int q = (lane & 7) ^ (col & 7);
+    const int q = (lane & 7) ^ swz_b<FMT>(col);
     const int row = s_row[col] < 0 ? 0 : s_row[col];  // padding columns compute on row 0, never stored
     bsrc[c] = a.xq + static_cast<size_t>(row) * K + q * 16;
   }
@@ -688,12 +701,12 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
       const int R = 64 * rg + 16 * j + r16;
       if constexpr (FMT == FMT_FP8) {
         const uint8_t* p = st + R * 128;
-        const u32x4 lo = *reinterpret_cast<const u32x4*>(p + (((2 * g) ^ (R & 7)) * 16));
-        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + (((2 * g + 1) ^ (R & 7)) * 16));
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(p + (((2 * g) ^ swz_pair(R)) * 16));
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + (((2 * g + 1) ^ swz_pair(R)) * 16));
         wf[j] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
         sw[j] = *reinterpret_cast<const float*>(st + L::kOffAS + rg * 16 + j * 4);
       } else {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(st + R * 64 + ((g ^ ((R >> 1) & 3)) * 16));
+        const u32x4 v = *reinterpret_cast<const u32x4*>(st + R * 64 + ((g ^ swz64(R)) * 16));
         wf[j] = i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
         wcode[j] = st[L::kOffAS + R * 4 + g];
       }
@@ -703,13 +716,13 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
       const uint8_t* p = st + L::kOffB + col * 128;
       u32x4 lo, hi;
       if constexpr (FMT == FMT_FP8) {
-        lo = *reinterpret_cast<const u32x4*>(p + (((2 * g) ^ (col & 7)) * 16));
-        hi = *reinterpret_cast<const u32x4*>(p + (((2 * g + 1) ^ (col & 7)) * 16));
+        lo = *reinterpret_cast<const u32x4*>(p + (((2 * g) ^ swz_b<FMT>(col)) * 16));
+        hi = *reinterpret_cast<const u32x4*>(p + (((2 * g + 1) ^ swz_b<FMT>(col)) * 16));
       } else {
         // the f8f6f4 MFMA reads an fp8 lane group g as K = 16g+[0,16) and
         // 64+16g+[0,16), an fp4 lane group as the block [32g, 32g+32)
-        lo = *reinterpret_cast<const u32x4*>(p + ((g ^ (col & 7)) * 16));
-        hi = *reinterpret_cast<const u32x4*>(p + (((4 + g) ^ (col & 7)) * 16));
+        lo = *reinterpret_cast<const u32x4*>(p + ((g ^ swz_b<FMT>(col)) * 16));
+        hi = *reinterpret_cast<const u32x4*>(p + (((4 + g) ^ swz_b<FMT>(col)) * 16));
       }
       xf = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
       xs = *reinterpret_cast<const uint32_t*>(st + L::kOffBS + col * 4);
