@@ -9,9 +9,9 @@
 //
 // Weights are the MFMA A operand (rows = output features), activations the B
 // operand (columns = routes).  Lane l supplies row/column l%16 and, for each
-// 128-wide K block, the 32 K values [kb*128 + (l/16)*32, +32): four MFMAs of
-// 8 values each.  A and B use the same K mapping, so the products pair up no
-// matter how the hardware orders K inside an MFMA.
+// 128-wide K block, 32 of its K values: four MFMAs of 8 values each, placed by
+// k_first() below.  A and B use the same K placement, so the products pair up
+// no matter how the hardware orders K inside an MFMA.
 //
 // The 4 waves of a workgroup split K (wave w takes K blocks w, w+4, ...), and
 // their partial sums are reduced through LDS in fixed wave order, so results are
@@ -41,6 +41,32 @@ __device__ __forceinline__ size_t row_bytes(int K) {
   return FMT == FMT_BF16 ? static_cast<size_t>(K) * 2 : FMT == FMT_FP8 ? static_cast<size_t>(K) : static_cast<size_t>(K) / 2;
 }
 
+// K placement inside a 128-wide K block: MFMA j (0..3) of lane group g = l/16
+// takes the 8 values starting at
+//   BF16   32j + 8g                 weights and activations: 16-byte pieces
+//                                   at 64j + 16g, one whole 64-byte line of a
+//                                   row per load instruction
+//   FP8    64(j/2) + 16g + 8(j%2)   weights: 16 bytes at 64i + 16g feed MFMAs
+//                                   2i and 2i+1 (a whole line per instruction);
+//                                   activations: 128(j/2) + 32g + 16(j%2)
+//   MXFP4  32g + 8j                 a lane group's 32 values share one e8m0
+//                                   scale; weights: 16 bytes at 16g
+// The weight side of a lane group starts a_group_bytes * g into the K block's
+// row slice; the activation piece of MFMA j sits at
+// g * b_group_bytes + b_piece_bytes(j).
+template <int FMT>
+constexpr uint32_t a_group_bytes() {
+  return 16;
+}
+template <int FMT>
+constexpr uint32_t b_group_bytes() {
+  return FMT == FMT_BF16 ? 16 : FMT == FMT_FP8 ? 32 : 64;
+}
+template <int FMT>
+constexpr uint32_t b_piece_bytes(int j) {
+  return FMT == FMT_BF16 ? 64 * j : FMT == FMT_FP8 ? 128 * (j >> 1) + 16 * (j & 1) : 16 * j;
+}
+
 // Raw (still quantised) A-operand bytes of one lane for one 128-wide K block.
 template <int FMT>
 struct RawA;
@@ -62,22 +88,25 @@ struct RawA<FMT_MXFP4> {
 // buf_x4): base in SGPRs, 32-bit lane offsets, the K-block offset in soffset.
 
 // Weight bytes of one lane for K block kb: the lane's row starts at voff
-// (row * row_bytes + the lane group's 32-value slice); the K block adds
-// kb * 128 values.
+// (row * row_bytes + a_group_bytes * lane group); the K block adds kb * 128
+// values.  MXFP4: the lane's e8m0 code sits at coff + kb * 4 of the
+// code rows (sr).  `dead` is 0 or kOutOfRange: a dead K block (past the wave's
+// range) is still issued, so every K step issues the same loads and the
+// wait counts stay exact, but it reads zeros without touching memory.
 template <int FMT>
-__device__ __forceinline__ void load_raw(__amdgpu_buffer_rsrc_t wr, uint32_t voff, const uint8_t* srow, int kb, int g,
-                                         RawA<FMT>& r) {
+__device__ __forceinline__ void load_raw(__amdgpu_buffer_rsrc_t wr, __amdgpu_buffer_rsrc_t sr, uint32_t voff,
+                                         uint32_t coff, int kb, uint32_t dead, RawA<FMT>& r) {
   if constexpr (FMT == FMT_BF16) {
     const uint32_t so = static_cast<uint32_t>(kb) * 256;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r.v[j] = __builtin_bit_cast(bf16x8, buf_x4(wr, voff + 16 * j, so));
+    for (int j = 0; j < 4; ++j) r.v[j] = __builtin_bit_cast(bf16x8, buf_x4(wr, (voff | dead) + 64 * j, so));
   } else if constexpr (FMT == FMT_FP8) {
     const uint32_t so = static_cast<uint32_t>(kb) * 128;
-    r.v[0] = buf_x4(wr, voff, so);
-    r.v[1] = buf_x4(wr, voff + 16, so);
+    r.v[0] = buf_x4(wr, voff | dead, so);
+    r.v[1] = buf_x4(wr, (voff | dead) + 64, so);
   } else {
-    r.v[0] = buf_x4(wr, voff, static_cast<uint32_t>(kb) * 64);
-    r.code = srow[kb * 4 + g];
+    r.v[0] = buf_x4(wr, voff | dead, static_cast<uint32_t>(kb) * 64);
+    r.code = buf_u8(sr, coff | dead, static_cast<uint32_t>(kb) * 4);
   }
 }
 
@@ -123,32 +152,33 @@ struct KStage {
 // read zeros (MFMA output column c depends on B column c only, and those
 // columns are never stored).
 // Weight-side addressing of one wave: the expert's matrix (wr), each tile's
-// lane offset (wvoff), and the scales (FP8: scale array sr with each tile's
-// scale row at soff; MXFP4: the lane's row of e8m0 codes).
+// lane offset (wvoff), and the scales: FP8 the expert's scale array sr with
+// each tile's scale row at soff (wave-uniform); MXFP4 the expert's e8m0 code
+// rows sr with the lane's row and lane group at soff.
 template <int NMAT>
 struct WTiles {
   __amdgpu_buffer_rsrc_t wr, sr;
   uint32_t wvoff[NMAT];
   uint32_t soff[NMAT];
-  const uint8_t* srows[NMAT];
 };
 
 template <int FMT, int NMAT, int NCH>
 __device__ __forceinline__ void load_stage(KStage<FMT, NMAT, NCH>& st, const WTiles<NMAT>& wt,
-                                           __amdgpu_buffer_rsrc_t br, const uint32_t (&bvoff)[NCH], int kb, int g) {
+                                           __amdgpu_buffer_rsrc_t br, const uint32_t (&bvoff)[NCH], int kb,
+                                           uint32_t dead) {
 #pragma unroll
-  for (int m = 0; m < NMAT; ++m) load_raw<FMT>(wt.wr, wt.wvoff[m], wt.srows[m], kb, g, st.w[m]);
+  for (int m = 0; m < NMAT; ++m) load_raw<FMT>(wt.wr, wt.sr, wt.wvoff[m], wt.soff[m], kb, dead, st.w[m]);
   if constexpr (FMT == FMT_FP8) {
     // wave-uniform address: one request per tile, in flight with the weights
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
-      st.sc[m] = buf_f32(wt.sr, wt.soff[m], static_cast<uint32_t>(kb) * 4);
+      st.sc[m] = buf_f32(wt.sr, wt.soff[m] | dead, static_cast<uint32_t>(kb) * 4);
   }
   const uint32_t so = static_cast<uint32_t>(kb) * 256;
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) st.b[c][j] = buf_x4(br, bvoff[c] + 16 * j, so);
+    for (int j = 0; j < 4; ++j) st.b[c][j] = buf_x4(br, (bvoff[c] | dead) + b_piece_bytes<FMT>(j), so);
 }
 
 template <int FMT, int NMAT, int NCH>
@@ -181,30 +211,171 @@ __device__ __forceinline__ void compute_stage(const KStage<FMT, NMAT, NCH>& st, 
   }
 }
 
+// K stages kept in flight: as many as fit next to the accumulators in the
+// 256 registers of occupancy 2 (a stage holds NMAT weight tiles, their scales
+// and NCH activation chunks), between 2 and 4.
+template <int FMT, int NMAT, int NCH>
+constexpr int pipeline_depth() {
+  constexpr int wregs = FMT == FMT_BF16 ? 16 : FMT == FMT_FP8 ? 8 : 4;
+  constexpr int per_stage = NMAT * (wregs + 1) + NCH * 16;
+  constexpr int fit = (200 - NMAT * NCH * 4 - 24) / per_stage;
+  return fit < 2 ? 2 : fit > 4 ? 4 : fit;
+}
+
 // Accumulates NMAT 16-row weight tiles against NCH route chunks of 16 over the
-// K blocks [kw*nkb/KS, (kw+1)*nkb/KS) (contiguous per wave), keeping the loads
-// of the next K block in flight while the current one is computed.
+// K blocks [kw*nkb/KS, (kw+1)*nkb/KS) (contiguous per wave) through a ring of
+// S register stages: the loads of the next S-1 K blocks are in flight while one
+// is computed.  Every step issues its loads (dead ones read zeros), so the
+// hardware counters wait for exactly the stage about to be used.
 template <int FMT, int NMAT, int NCH, int KS>
 __device__ __forceinline__ void gemv_tile(const WTiles<NMAT>& wt, int K, int kw, __amdgpu_buffer_rsrc_t br,
                                           const uint32_t (&bvoff)[NCH], f32x4 (&acc)[NMAT][NCH]) {
-  const int g = lane_id() >> 4;
+  constexpr int S = pipeline_depth<FMT, NMAT, NCH>();
   const int nkb = K / 128;
   const int kb_lo = kw * nkb / KS, kb_hi = (kw + 1) * nkb / KS;
+  const int n = kb_hi - kb_lo;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int m = 0; m < NMAT; ++m)
 #pragma unroll
     for (int c = 0; c < NCH; ++c) acc[m][c] = zero;
-  KStage<FMT, NMAT, NCH> s0, s1;
-  if (kb_lo < kb_hi) load_stage(s0, wt, br, bvoff, kb_lo, g);
-  for (int kb = kb_lo; kb < kb_hi; kb += 2) {
-    if (kb + 1 < kb_hi) load_stage(s1, wt, br, bvoff, kb + 1, g);
-    compute_stage(s0, acc);
-    if (kb + 1 < kb_hi) {
-      if (kb + 2 < kb_hi) load_stage(s0, wt, br, bvoff, kb + 2, g);
-      compute_stage(s1, acc);
+  KStage<FMT, NMAT, NCH> st[S];
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s) load_stage(st[s], wt, br, bvoff, kb_lo + s, s < n ? 0u : kOutOfRange);
+  // whole groups of S steps: loads and computes unconditional
+  int i = 0;
+  for (; i + S <= n; i += S) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int ahead = i + s + S - 1;
+      load_stage(st[(s + S - 1) % S], wt, br, bvoff, kb_lo + ahead, ahead < n ? 0u : kOutOfRange);
+      // loads leave in the order the stages are consumed (the counter is
+      // in order): keep the scheduler from mixing one step's loads into another's
+      __builtin_amdgcn_sched_barrier(0);
+      compute_stage(st[s], acc);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
+  // the last n - i < S blocks are already in stages 0.. (loaded above or in
+  // the prologue)
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (i + s < n) compute_stage(st[s], acc);
+}
+
+// FP8 weights stream through LDS instead of registers.  A register load
+// instruction can cover at most 64 bytes of a row (4 lanes of 16 bytes share a
+// row in the MFMA operand layout), so the two halves of each 128-byte line are
+// fetched by different instructions and the line has to stay in L2 between
+// them.  A DMA instruction (buffer load to LDS) is free to give its 64 lanes 8
+// whole rows: each fetches complete lines, which lets the weights use the
+// nontemporal policy (measured on MI355X: 7.1 TB/s against 6.2 TB/s for the
+// default policy on a plain stream).  Each wave owns a ring of two stages in
+// LDS; a stage holds NMAT tiles of 16 rows x 128 bytes (one K block).  Chunk c
+// (16 bytes) of tile row r lands at slot c ^ (r & 7) of the row, spreading the
+// operand reads over the LDS banks.
+constexpr int kTileBytes = 16 * 128;
+constexpr int kNtPolicy = 2;  // cache policy bits of a nontemporal load
+
+template <int NMAT>
+struct DmaTiles {
+  __amdgpu_buffer_rsrc_t wr, sr;
+  uint32_t voff[NMAT][2];  // lane's DMA source in instruction h (rows 8h..8h+7) of tile m
+  uint32_t soff[NMAT];     // tile's scale row (wave-uniform)
+};
+
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0,
+                                           kNtPolicy);
+}
+
+template <int NMAT, int NCH>
+__device__ __forceinline__ void dma_issue(const DmaTiles<NMAT>& dt, __amdgpu_buffer_rsrc_t br,
+                                          const uint32_t (&bvoff)[NCH], uint8_t* stage, int kb, uint32_t dead,
+                                          u32x4 (&b)[NCH][4], float (&sc)[NMAT]) {
+  const uint32_t so = static_cast<uint32_t>(kb) * 128;
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) lds_dma16(dt.wr, stage + m * kTileBytes + h * 1024, dt.voff[m][h] | dead, so);
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m) sc[m] = buf_f32(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(kb) * 4);
+  const uint32_t sb = static_cast<uint32_t>(kb) * 256;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[c][j] = buf_x4(br, (bvoff[c] | dead) + b_piece_bytes<FMT_FP8>(j), sb);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int NMAT, int NCH>
+__device__ __forceinline__ void dma_compute(const uint8_t* stage, uint32_t rd0, uint32_t rd1,
+                                            const u32x4 (&b)[NCH][4], const float (&sc)[NMAT],
+                                            f32x4 (&acc)[NMAT][NCH]) {
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  RawA<FMT_FP8> w[NMAT];
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m) {
+    w[m].v[0] = *reinterpret_cast<const u32x4*>(stage + m * kTileBytes + rd0);
+    w[m].v[1] = *reinterpret_cast<const u32x4*>(stage + m * kTileBytes + rd1);
+  }
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m) {
+    bf16x8 a[4];
+    dequant<FMT_FP8>(w[m], a);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      f32x4 t = zero;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j], __builtin_bit_cast(bf16x8, b[c][j]), t, 0, 0, 0);
+      acc[m][c] += t * sc[m];
+    }
+  }
+}
+
+// FP8 counterpart of gemv_tile: the same K range and accumulation order, the
+// weights through the wave's LDS ring (two stages: the DMA of the next K block
+// is in flight while one is computed; a dead step still issues, reading zeros).
+template <int NMAT, int NCH, int KS>
+__device__ __forceinline__ void gemv_tile_dma(const DmaTiles<NMAT>& dt, int K, int kw, __amdgpu_buffer_rsrc_t br,
+                                              const uint32_t (&bvoff)[NCH], uint8_t* ring,
+                                              f32x4 (&acc)[NMAT][NCH]) {
+  constexpr int kStage = NMAT * kTileBytes;
+  constexpr int kPerStep = 3 * NMAT + 4 * NCH;  // vector memory instructions of one dma_issue
+  const int lane = lane_id(), r16 = lane & 15, g = lane >> 4;
+  const uint32_t rd0 = r16 * 128 + ((g ^ (r16 & 7)) << 4);
+  const uint32_t rd1 = r16 * 128 + (((4 + g) ^ (r16 & 7)) << 4);
+  const int nkb = K / 128;
+  const int kb_lo = kw * nkb / KS, kb_hi = (kw + 1) * nkb / KS;
+  const int n = kb_hi - kb_lo;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) acc[m][c] = zero;
+  u32x4 b0[NCH][4], b1[NCH][4];
+  float sc0[NMAT], sc1[NMAT];
+  dma_issue(dt, br, bvoff, ring, kb_lo, n > 0 ? 0u : kOutOfRange, b0, sc0);
+  int i = 0;
+  for (; i + 2 <= n; i += 2) {
+    dma_issue(dt, br, bvoff, ring + kStage, kb_lo + i + 1, 0u, b1, sc1);
+    wait_vmcnt<kPerStep>();
+    __builtin_amdgcn_sched_barrier(0);
+    dma_compute(ring, rd0, rd1, b0, sc0, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    dma_issue(dt, br, bvoff, ring, kb_lo + i + 2, i + 2 < n ? 0u : kOutOfRange, b0, sc0);
+    wait_vmcnt<kPerStep>();
+    __builtin_amdgcn_sched_barrier(0);
+    dma_compute(ring + kStage, rd0, rd1, b1, sc1, acc);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wait_vmcnt<0>();
+  if (i < n) dma_compute(ring, rd0, rd1, b0, sc0, acc);
 }
 
 // Where a segment's column lives.  Routed segments: column col is route
@@ -258,10 +429,11 @@ __device__ __forceinline__ void tile_epilogue(const DecodeArgs& a, const SegView
 // and are added in fixed wave order, so results do not depend on timing.
 template <int FMT, int STAGE, int RT, int KS, int NCH>
 __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView& bank, const SegView& sv, int base,
-                                            int row0, int inter, f32x4* red) {
+                                            int row0, int inter, uint8_t* smem) {
+  f32x4* red = reinterpret_cast<f32x4*>(smem);
   constexpr int NMAT = STAGE == 0 ? 2 * RT : RT;
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
   const int kw = wave % KS, rg = wave / KS;
   const int r16 = lane & 15, g = lane >> 4;
   const int N = STAGE == 0 ? 2 * inter : a.H;
@@ -283,7 +455,7 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
       int row;
       if (STAGE == 0) row = sv.shared ? sv.start + col : a.sorted[sv.start + col] / a.k;
       else row = sv.shared ? a.M * a.k + sv.start + col : a.sorted[sv.start + col];
-      bvoff[c] = static_cast<uint32_t>(row) * bstride * 2 + g * 64;
+      bvoff[c] = static_cast<uint32_t>(row) * bstride * 2 + g * b_group_bytes<FMT>();
     } else {
       bvoff[c] = kOutOfRange;
     }
@@ -294,26 +466,40 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
   if constexpr (FMT == FMT_FP8) {
     const uint32_t sbytes = static_cast<uint32_t>(N / 128) * (K / 128) * 4;
     wt.sr = make_rsrc(static_cast<const uint8_t*>(bank.s) + static_cast<size_t>(sv.expert) * sbytes, sbytes);
+  } else if constexpr (FMT == FMT_MXFP4) {
+    const uint32_t cbytes = static_cast<uint32_t>(N) * (K / 32);
+    wt.sr = make_rsrc(static_cast<const uint8_t*>(bank.s) + static_cast<size_t>(sv.expert) * cbytes, cbytes);
   } else {
     wt.sr = wt.wr;
   }
-  const uint32_t gbytes = FMT == FMT_BF16 ? 64 : FMT == FMT_FP8 ? 32 : 16;  // a lane group's 32 values
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) {
     // matrix m: gate tiles then up tiles (stage 0); down tiles (stage 1)
     const int tile_row = (STAGE == 0 && m >= RT) ? inter + wrow0 + 16 * (m - RT) : wrow0 + 16 * m;
     const int ridx = tile_row + r16;
-    wt.wvoff[m] = static_cast<uint32_t>(ridx) * rb + g * gbytes;
-    // a 16-row tile lies inside one 128-row scale block
-    wt.soff[m] = static_cast<uint32_t>(tile_row / 128) * (K / 128) * 4;
-    if constexpr (FMT == FMT_MXFP4) {
-      wt.srows[m] = static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(sv.expert) * N + ridx) * (K / 32);
-    } else {
-      wt.srows[m] = nullptr;
-    }
+    wt.wvoff[m] = static_cast<uint32_t>(ridx) * rb + g * a_group_bytes<FMT>();
+    if constexpr (FMT == FMT_MXFP4)
+      wt.soff[m] = static_cast<uint32_t>(ridx) * (K / 32) + g;
+    else  // a 16-row tile lies inside one 128-row scale block
+      wt.soff[m] = static_cast<uint32_t>(tile_row / 128) * (K / 128) * 4;
   }
   f32x4 acc[NMAT][NCH];
-  gemv_tile<FMT, NMAT, NCH, KS>(wt, K, kw, br, bvoff, acc);
+  if constexpr (FMT == FMT_FP8) {
+    DmaTiles<NMAT> dt;
+    dt.wr = wt.wr;
+    dt.sr = wt.sr;
+    const int dr = lane >> 3, dc = (lane & 7) ^ dr;  // DMA lane: row dr of 8, stored at slot lane & 7
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) {
+      const int tile_row = (STAGE == 0 && m >= RT) ? inter + wrow0 + 16 * (m - RT) : wrow0 + 16 * m;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) dt.voff[m][h] = static_cast<uint32_t>(tile_row + 8 * h + dr) * rb + dc * 16;
+      dt.soff[m] = wt.soff[m];
+    }
+    gemv_tile_dma<NMAT, NCH, KS>(dt, K, kw, br, bvoff, smem + wave * 2 * NMAT * kTileBytes, acc);
+  } else {
+    gemv_tile<FMT, NMAT, NCH, KS>(wt, K, kw, br, bvoff, acc);
+  }
 
   if constexpr (KS == 1) {
 #pragma unroll
@@ -325,6 +511,7 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
           tile_epilogue<STAGE>(a, sv, col, wrow0 + 16 * t + g * 4, acc[t][c], acc[STAGE == 0 ? RT + t : t][c]);
       }
   } else {
+    if constexpr (FMT == FMT_FP8) __syncthreads();  // red overlays the waves' LDS rings
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
@@ -355,19 +542,19 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
 template <int FMT, int STAGE, int RT>
 constexpr int chunks_per_pass() {
   if constexpr (STAGE == 0) return RT == 1 ? 2 : (FMT == FMT_BF16 ? 1 : 2);
-  return RT == 1 ? 2 : 2;
+  return RT == 4 && FMT == FMT_BF16 ? 1 : 2;
 }
 
 template <int FMT, int STAGE, int RT, int KS>
 __device__ __forceinline__ void decode_segment(const DecodeArgs& a, const BankView& bank, const SegView& sv, int row0,
-                                               int inter, f32x4* red) {
+                                               int inter, uint8_t* smem) {
   constexpr int CMAX = chunks_per_pass<FMT, STAGE, RT>();
   for (int base = 0; base < sv.count; base += 16 * CMAX) {
     if constexpr (CMAX == 1) {
-      decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, red);
+      decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, smem);
     } else {
-      if (sv.count - base <= 16) decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, red);
-      else decode_pass<FMT, STAGE, RT, KS, 2>(a, bank, sv, base, row0, inter, red);
+      if (sv.count - base <= 16) decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, smem);
+      else decode_pass<FMT, STAGE, RT, KS, 2>(a, bank, sv, base, row0, inter, smem);
     }
   }
 }
@@ -379,7 +566,11 @@ constexpr int kRedFloats4 = kDecWaves * 8 * kWave;  // NMAT * chunks_per_pass <=
 // pieces of seg_cap tokens.
 template <int FMT_R, int FMT_S, int STAGE, int RT, int KS>
 __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) decode_stage_kernel(DecodeArgs a) {
-  __shared__ f32x4 red[KS > 1 ? kRedFloats4 : 1];
+  constexpr int kNmat = STAGE == 0 ? 2 * RT : RT;
+  constexpr int kRing = (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? kDecWaves * 2 * kNmat * kTileBytes : 0;
+  constexpr int kRed = KS > 1 ? kRedFloats4 * 16 : 0;
+  constexpr int kSmem = kRing > kRed ? kRing : kRed > 16 ? kRed : 16;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kSmem];
   const int seg = blockIdx.y;
   SegView sv;
   sv.shared = seg >= a.max_seg;
@@ -408,13 +599,13 @@ __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves
   const int fmt = sv.shared ? FMT_S : FMT_R;
   if (fmt == FMT_BF16) {
     if constexpr (FMT_R == FMT_BF16 || FMT_S == FMT_BF16)
-      decode_segment<FMT_BF16, STAGE, RT, KS>(a, bank, sv, row0, inter, red);
+      decode_segment<FMT_BF16, STAGE, RT, KS>(a, bank, sv, row0, inter, smem);
   } else if (fmt == FMT_FP8) {
     if constexpr (FMT_R == FMT_FP8 || FMT_S == FMT_FP8)
-      decode_segment<FMT_FP8, STAGE, RT, KS>(a, bank, sv, row0, inter, red);
+      decode_segment<FMT_FP8, STAGE, RT, KS>(a, bank, sv, row0, inter, smem);
   } else {
     if constexpr (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4)
-      decode_segment<FMT_MXFP4, STAGE, RT, KS>(a, bank, sv, row0, inter, red);
+      decode_segment<FMT_MXFP4, STAGE, RT, KS>(a, bank, sv, row0, inter, smem);
   }
 }
 
@@ -475,11 +666,11 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
 
 // Launch shapes.  Stage 0 (K = hidden, long rows): the 4 waves split K and a
 // workgroup covers RT tiles of gate and of up.  Stage 1 (K = intermediate,
-// short rows): each wave owns RT whole tiles.  RT = 2 halves the activation
-// loads per weight byte and is faster at every measured batch except when its
-// grid leaves the resident slots much emptier than RT = 1's (b = 1 gate_up:
-// 1.1 rounds against 2.25), so RT = 1 is used only when it fills the slots at
-// least 15 points better.
+// short rows): each wave owns RT whole tiles.  A larger RT cuts the activation
+// loads per weight byte and the workgroups' fixed costs, and is faster at every
+// measured batch unless its grid leaves the resident slots much emptier than a
+// smaller RT's (b = 1 gate_up: 1.1 rounds against 2.25), so the largest RT
+// whose slot fill is within 15 points of the best is used.
 
 // Resident workgroups per CU of a kernel (runtime occupancy query, cached).
 template <auto KERNEL>
@@ -514,16 +705,14 @@ static double fill(long long wgs, long long slots) {
   return static_cast<double>(wgs) / static_cast<double>(rounds * slots);
 }
 
-template <auto K1, auto K2>
-static hipError_t launch_pick(long long n1, long long n2, dim3 g1, dim3 g2, const DecodeArgs& a, hipStream_t stream) {
-  const int cus = cu_count();
-  const double f1 = fill(n1, static_cast<long long>(cus) * resident_per_cu<K1>());
-  const double f2 = fill(n2, static_cast<long long>(cus) * resident_per_cu<K2>());
-  const dim3 block(kDecWaves * kWave);
-  if (f2 >= f1 - 0.15)
-    hipLaunchKernelGGL(K2, g2, block, 0, stream, a);
-  else
-    hipLaunchKernelGGL(K1, g1, block, 0, stream, a);
+template <auto KERNEL>
+static double fill_of(dim3 g) {
+  return fill(static_cast<long long>(g.x) * g.y, static_cast<long long>(cu_count()) * resident_per_cu<KERNEL>());
+}
+
+template <auto KERNEL>
+static hipError_t launch_one(dim3 g, const DecodeArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL(KERNEL, g, dim3(kDecWaves * kWave), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -531,14 +720,23 @@ template <int FR, int FS>
 static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared, hipStream_t stream) {
   const int gy = a.max_seg + (has_shared ? (a.M + a.seg_cap - 1) / a.seg_cap : 0);
   const int imax = has_shared ? max(a.I, a.Is) : a.I;
+  constexpr double kSlack = 0.15;
   if (stage == 0) {
+    constexpr auto k1 = decode_stage_kernel<FR, FS, 0, 1, 4>;
+    constexpr auto k2 = decode_stage_kernel<FR, FS, 0, 2, 4>;
     const dim3 g1((imax + 15) / 16, gy), g2((imax + 31) / 32, gy);
-    return launch_pick<decode_stage_kernel<FR, FS, 0, 1, 4>, decode_stage_kernel<FR, FS, 0, 2, 4>>(
-        static_cast<long long>(g1.x) * gy, static_cast<long long>(g2.x) * gy, g1, g2, a, stream);
+    if (fill_of<k2>(g2) >= fill_of<k1>(g1) - kSlack) return launch_one<k2>(g2, a, stream);
+    return launch_one<k1>(g1, a, stream);
   }
-  const dim3 g1(a.H / 64, gy), g2(a.H / 128, gy);
-  return launch_pick<decode_stage_kernel<FR, FS, 1, 1, 1>, decode_stage_kernel<FR, FS, 1, 2, 1>>(
-      static_cast<long long>(g1.x) * gy, static_cast<long long>(g2.x) * gy, g1, g2, a, stream);
+  constexpr auto k1 = decode_stage_kernel<FR, FS, 1, 1, 1>;
+  constexpr auto k2 = decode_stage_kernel<FR, FS, 1, 2, 1>;
+  constexpr auto k4 = decode_stage_kernel<FR, FS, 1, 4, 1>;
+  const dim3 g1(a.H / 64, gy), g2(a.H / 128, gy), g4(a.H / 256, gy);
+  const double f1 = fill_of<k1>(g1), f2 = fill_of<k2>(g2), f4 = a.H % 256 == 0 ? fill_of<k4>(g4) : -1.0;
+  const double best = max(f1, max(f2, f4));
+  if (f4 >= best - kSlack) return launch_one<k4>(g4, a, stream);
+  if (f2 >= best - kSlack) return launch_one<k2>(g2, a, stream);
+  return launch_one<k1>(g1, a, stream);
 }
 
 hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream) {
