@@ -46,9 +46,10 @@ __device__ __forceinline__ size_t row_bytes(int K) {
 //   BF16   32j + 8g                 weights and activations: 16-byte pieces
 //                                   at 64j + 16g, one whole 64-byte line of a
 //                                   row per load instruction
-//   FP8    64(j/2) + 16g + 8(j%2)   weights: 16 bytes at 64i + 16g feed MFMAs
-//                                   2i and 2i+1 (a whole line per instruction);
+//   FP8    64(j/2) + 16g + 8(j%2)   weights (from LDS, see dma_compute): the
+//                                   16 bytes at 64i + 16g feed MFMAs 2i, 2i+1;
 //                                   activations: 128(j/2) + 32g + 16(j%2)
+//                                   (measured faster than 32j + 8g here)
 //   MXFP4  32g + 8j                 a lane group's 32 values share one e8m0
 //                                   scale; weights: 16 bytes at 16g
 // The weight side of a lane group starts a_group_bytes * g into the K block's
@@ -100,11 +101,8 @@ __device__ __forceinline__ void load_raw(__amdgpu_buffer_rsrc_t wr, __amdgpu_buf
     const uint32_t so = static_cast<uint32_t>(kb) * 256;
 #pragma unroll
     for (int j = 0; j < 4; ++j) r.v[j] = __builtin_bit_cast(bf16x8, buf_x4(wr, (voff | dead) + 64 * j, so));
-  } else if constexpr (FMT == FMT_FP8) {
-    const uint32_t so = static_cast<uint32_t>(kb) * 128;
-    r.v[0] = buf_x4(wr, voff | dead, so);
-    r.v[1] = buf_x4(wr, (voff | dead) + 64, so);
   } else {
+    static_assert(FMT == FMT_MXFP4, "FP8 weights take the LDS path (gemv_tile_dma)");
     r.v[0] = buf_x4(wr, voff | dead, static_cast<uint32_t>(kb) * 64);
     r.code = buf_u8(sr, coff | dead, static_cast<uint32_t>(kb) * 4);
   }
@@ -312,6 +310,8 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// The lane's operand bytes sit at rd0 (MFMAs 0, 1) and rd1 (MFMAs 2, 3) inside
+// a tile: row r16, chunks g and 4 + g.
 template <int NMAT, int NCH>
 __device__ __forceinline__ void dma_compute(const uint8_t* stage, uint32_t rd0, uint32_t rd1,
                                             const u32x4 (&b)[NCH][4], const float (&sc)[NMAT],
@@ -385,36 +385,58 @@ struct SegView {
   int expert, start, count;
 };
 
-// Epilogue of one 16-row output tile for one lane (4 consecutive rows
-// rows_at..rows_at+3, column col < count).  Stage 0: g, u are the gate and up
-// sums; stage 1: g is the down sum (u unused).
+// Where a lane's column goes, read before the K loop so that the epilogue
+// issues no dependent loads.  Stage 0: the act row and the router weight
+// applied to the input (1 unless weight_on_input); stage 1: the ic3 row (the
+// route) or the sh_out row (the token) and the router weight applied to the
+// output.
+struct ColDst {
+  int row;
+  float w;
+};
+
 template <int STAGE>
-__device__ __forceinline__ void tile_epilogue(const DecodeArgs& a, const SegView& sv, int col, int rows_at, f32x4 g,
+__device__ __forceinline__ ColDst col_dst(const DecodeArgs& a, const SegView& sv, int col, int route) {
+  ColDst d;
+  if constexpr (STAGE == 0) {
+    d.row = sv.shared ? a.M * a.k + sv.start + col : route;
+    d.w = (!sv.shared && a.weight_on_input) ? a.topk_w[route] : 1.0f;
+  } else {
+    d.row = sv.shared ? sv.start + col : route;
+    d.w = (!sv.shared && !a.weight_on_input) ? a.topk_w[route] : 1.0f;
+  }
+  return d;
+}
+
+template <int N>
+__device__ __forceinline__ ColDst pick(const ColDst (&d)[N], int c) {
+  ColDst r = d[0];
+#pragma unroll
+  for (int i = 1; i < N; ++i)
+    if (c == i) r = d[i];
+  return r;
+}
+
+// Epilogue of one 16-row output tile for one lane (4 consecutive rows
+// rows_at..rows_at+3 of its column).  Stage 0: g, u are the gate and up sums;
+// stage 1: g is the down sum (u unused).
+template <int STAGE>
+__device__ __forceinline__ void tile_epilogue(const DecodeArgs& a, const SegView& sv, ColDst d, int rows_at, f32x4 g,
                                               f32x4 u) {
   uint16_t o[4];
   uint16_t* dst;
   if constexpr (STAGE == 0) {
-    const int route = sv.shared ? -1 : a.sorted[sv.start + col];
-    const float win = (!sv.shared && a.weight_on_input) ? a.topk_w[route] : 1.0f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const float gg = bf16_round(g[v] * win);
-      const float uu = bf16_round(u[v] * win);
+      const float gg = bf16_round(g[v] * d.w);
+      const float uu = bf16_round(u[v] * d.w);
       o[v] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
     }
-    const int arow = sv.shared ? a.M * a.k + sv.start + col : route;
-    dst = a.act + static_cast<size_t>(arow) * a.act_stride + rows_at;
+    dst = a.act + static_cast<size_t>(d.row) * a.act_stride + rows_at;
   } else {
-    float wt = 1.0f;
-    if (sv.shared) {
-      dst = a.sh_out + static_cast<size_t>(sv.start + col) * a.H + rows_at;
-    } else {
-      const int route = a.sorted[sv.start + col];
-      if (!a.weight_on_input) wt = a.topk_w[route];
-      dst = a.ic3 + static_cast<size_t>(route) * a.H + rows_at;
-    }
+    dst = (sv.shared ? a.sh_out : a.ic3) + static_cast<size_t>(d.row) * a.H + rows_at;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(g[v] * wt);
+    for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(g[v] * d.w);
   }
   uint2 pk;
   pk.x = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
@@ -448,16 +470,20 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
   const uint32_t bstride = STAGE == 0 ? static_cast<uint32_t>(a.H) : static_cast<uint32_t>(a.act_stride);
   const __amdgpu_buffer_rsrc_t br = make_rsrc(bbase, brows * bstride * 2);
   uint32_t bvoff[NCH];
+  ColDst cd[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int col = base + c * 16 + r16;
     if (col < sv.count) {
+      const int route = sv.shared ? -1 : a.sorted[sv.start + col];
       int row;
-      if (STAGE == 0) row = sv.shared ? sv.start + col : a.sorted[sv.start + col] / a.k;
-      else row = sv.shared ? a.M * a.k + sv.start + col : a.sorted[sv.start + col];
+      if (STAGE == 0) row = sv.shared ? sv.start + col : route / a.k;
+      else row = sv.shared ? a.M * a.k + sv.start + col : route;
       bvoff[c] = static_cast<uint32_t>(row) * bstride * 2 + g * b_group_bytes<FMT>();
+      cd[c] = col_dst<STAGE>(a, sv, col, route);
     } else {
       bvoff[c] = kOutOfRange;
+      cd[c] = ColDst{0, 0.0f};
     }
   }
   const uint32_t rb = static_cast<uint32_t>(row_bytes<FMT>(K));
@@ -508,7 +534,7 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
       for (int c = 0; c < NCH; ++c) {
         const int col = base + c * 16 + r16;
         if (c < nch && col < sv.count)
-          tile_epilogue<STAGE>(a, sv, col, wrow0 + 16 * t + g * 4, acc[t][c], acc[STAGE == 0 ? RT + t : t][c]);
+          tile_epilogue<STAGE>(a, sv, cd[c], wrow0 + 16 * t + g * 4, acc[t][c], acc[STAGE == 0 ? RT + t : t][c]);
       }
   } else {
     if constexpr (FMT == FMT_FP8) __syncthreads();  // red overlays the waves' LDS rings
@@ -531,7 +557,7 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
         sg += red[(((w0 + v) * NMAT + mg) * NCH + c) * kWave + lane];
         if (STAGE == 0) su += red[(((w0 + v) * NMAT + mu) * NCH + c) * kWave + lane];
       }
-      if (col < sv.count) tile_epilogue<STAGE>(a, sv, col, wrow0 + 16 * t + g * 4, sg, su);
+      if (col < sv.count) tile_epilogue<STAGE>(a, sv, pick(cd, c), wrow0 + 16 * t + g * 4, sg, su);
     }
     __syncthreads();
   }
@@ -542,7 +568,7 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
 template <int FMT, int STAGE, int RT>
 constexpr int chunks_per_pass() {
   if constexpr (STAGE == 0) return RT == 1 ? 2 : (FMT == FMT_BF16 ? 1 : 2);
-  return RT == 4 && FMT == FMT_BF16 ? 1 : 2;
+  return 2;
 }
 
 template <int FMT, int STAGE, int RT, int KS>
@@ -666,11 +692,12 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
 
 // Launch shapes.  Stage 0 (K = hidden, long rows): the 4 waves split K and a
 // workgroup covers RT tiles of gate and of up.  Stage 1 (K = intermediate,
-// short rows): each wave owns RT whole tiles.  A larger RT cuts the activation
-// loads per weight byte and the workgroups' fixed costs, and is faster at every
-// measured batch unless its grid leaves the resident slots much emptier than a
-// smaller RT's (b = 1 gate_up: 1.1 rounds against 2.25), so the largest RT
-// whose slot fill is within 15 points of the best is used.
+// short rows): each wave owns RT whole tiles.  RT = 2 halves the activation
+// loads per weight byte and is faster at every measured batch except when its
+// grid leaves the resident slots much emptier than RT = 1's (b = 1 gate_up:
+// 1.1 rounds against 2.25), so RT = 1 is used only when it fills the slots at
+// least 15 points better.  (RT = 4 down tiles measured no faster than RT = 2
+// once the weights come through LDS.)
 
 // Resident workgroups per CU of a kernel (runtime occupancy query, cached).
 template <auto KERNEL>
@@ -730,12 +757,8 @@ static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared
   }
   constexpr auto k1 = decode_stage_kernel<FR, FS, 1, 1, 1>;
   constexpr auto k2 = decode_stage_kernel<FR, FS, 1, 2, 1>;
-  constexpr auto k4 = decode_stage_kernel<FR, FS, 1, 4, 1>;
-  const dim3 g1(a.H / 64, gy), g2(a.H / 128, gy), g4(a.H / 256, gy);
-  const double f1 = fill_of<k1>(g1), f2 = fill_of<k2>(g2), f4 = a.H % 256 == 0 ? fill_of<k4>(g4) : -1.0;
-  const double best = max(f1, max(f2, f4));
-  if (f4 >= best - kSlack) return launch_one<k4>(g4, a, stream);
-  if (f2 >= best - kSlack) return launch_one<k2>(g2, a, stream);
+  const dim3 g1(a.H / 64, gy), g2(a.H / 128, gy);
+  if (fill_of<k2>(g2) >= fill_of<k1>(g1) - kSlack) return launch_one<k2>(g2, a, stream);
   return launch_one<k1>(g1, a, stream);
 }
 
