@@ -268,8 +268,8 @@ __device__ __forceinline__ void gemv_tile(const WTiles<NMAT>& wt, int K, int kw,
 // them.  A DMA instruction (buffer load to LDS) is free to give its 64 lanes 8
 // whole rows: each fetches complete lines, which lets the weights use the
 // nontemporal policy (measured on MI355X: 7.1 TB/s against 6.2 TB/s for the
-// default policy on a plain stream).  Each wave owns a ring of two stages in
-// LDS; a stage holds NMAT tiles of 16 rows x 128 bytes (one K block).  Chunk c
+// default policy on a plain stream).  Each wave owns a ring of stages in LDS
+// (dma_depth); a stage holds NMAT tiles of 16 rows x 128 bytes (one K block).  Chunk c
 // (16 bytes) of tile row r lands at slot c ^ (r & 7) of the row, spreading the
 // operand reads over the LDS banks.
 constexpr int kTileBytes = 16 * 128;
@@ -338,13 +338,38 @@ __device__ __forceinline__ void dma_compute(const uint8_t* stage, uint32_t rd0, 
   }
 }
 
+// Computes the stages T.. of the last `left` K blocks of a ring of S stages,
+// waiting for each stage alone (the S-2-T stages behind it stay in flight).
+template <int S, int T, int NMAT, int NCH>
+__device__ __forceinline__ void dma_tail(int left, const uint8_t* ring, uint32_t rd0, uint32_t rd1,
+                                         const u32x4 (&b)[S][NCH][4], const float (&sc)[S][NMAT],
+                                         f32x4 (&acc)[NMAT][NCH]) {
+  if constexpr (T < S - 1) {
+    if (left > T) {
+      wait_vmcnt<(S - 2 - T) * (3 * NMAT + 4 * NCH)>();
+      dma_compute(ring + T * NMAT * kTileBytes, rd0, rd1, b[T], sc[T], acc);
+      dma_tail<S, T + 1, NMAT, NCH>(left, ring, rd0, rd1, b, sc, acc);
+    }
+  }
+}
+
+// Ring depth of the LDS path: 2 stages of 4 tiles (64 KiB of LDS per
+// workgroup, two resident per CU) or 3 stages of 2 (measured against 2 and 4:
+// 3 is the fastest at b = 1 and no slower at b = 8 and 64).
+template <int NMAT>
+constexpr int dma_depth() {
+  return NMAT >= 4 ? 2 : 3;
+}
+
 // FP8 counterpart of gemv_tile: the same K range and accumulation order, the
-// weights through the wave's LDS ring (two stages: the DMA of the next K block
-// is in flight while one is computed; a dead step still issues, reading zeros).
+// weights through the wave's LDS ring of S stages (the DMA of the next S-1 K
+// blocks is in flight while one is computed; a dead step still issues,
+// reading zeros, so every step's wait count is exact).
 template <int NMAT, int NCH, int KS>
 __device__ __forceinline__ void gemv_tile_dma(const DmaTiles<NMAT>& dt, int K, int kw, __amdgpu_buffer_rsrc_t br,
                                               const uint32_t (&bvoff)[NCH], uint8_t* ring,
                                               f32x4 (&acc)[NMAT][NCH]) {
+  constexpr int S = dma_depth<NMAT>();
   constexpr int kStage = NMAT * kTileBytes;
   constexpr int kPerStep = 3 * NMAT + 4 * NCH;  // vector memory instructions of one dma_issue
   const int lane = lane_id(), r16 = lane & 15, g = lane >> 4;
@@ -358,24 +383,26 @@ __device__ __forceinline__ void gemv_tile_dma(const DmaTiles<NMAT>& dt, int K, i
   for (int m = 0; m < NMAT; ++m)
 #pragma unroll
     for (int c = 0; c < NCH; ++c) acc[m][c] = zero;
-  u32x4 b0[NCH][4], b1[NCH][4];
-  float sc0[NMAT], sc1[NMAT];
-  dma_issue(dt, br, bvoff, ring, kb_lo, n > 0 ? 0u : kOutOfRange, b0, sc0);
+  u32x4 b[S][NCH][4];
+  float sc[S][NMAT];
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    dma_issue(dt, br, bvoff, ring + s * kStage, kb_lo + s, s < n ? 0u : kOutOfRange, b[s], sc[s]);
   int i = 0;
-  for (; i + 2 <= n; i += 2) {
-    dma_issue(dt, br, bvoff, ring + kStage, kb_lo + i + 1, 0u, b1, sc1);
-    wait_vmcnt<kPerStep>();
-    __builtin_amdgcn_sched_barrier(0);
-    dma_compute(ring, rd0, rd1, b0, sc0, acc);
-    __builtin_amdgcn_sched_barrier(0);
-    dma_issue(dt, br, bvoff, ring, kb_lo + i + 2, i + 2 < n ? 0u : kOutOfRange, b0, sc0);
-    wait_vmcnt<kPerStep>();
-    __builtin_amdgcn_sched_barrier(0);
-    dma_compute(ring + kStage, rd0, rd1, b1, sc1, acc);
-    __builtin_amdgcn_sched_barrier(0);
+  for (; i + S <= n; i += S) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int ahead = i + s + S - 1;
+      dma_issue(dt, br, bvoff, ring + ((s + S - 1) % S) * kStage, kb_lo + ahead, ahead < n ? 0u : kOutOfRange,
+                b[(s + S - 1) % S], sc[(s + S - 1) % S]);
+      wait_vmcnt<(S - 1) * kPerStep>();
+      __builtin_amdgcn_sched_barrier(0);
+      dma_compute(ring + s * kStage, rd0, rd1, b[s], sc[s], acc);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
-  wait_vmcnt<0>();
-  if (i < n) dma_compute(ring, rd0, rd1, b0, sc0, acc);
+  // the last n - i < S blocks sit in stages 0.. (loaded above)
+  dma_tail<S, 0, NMAT, NCH>(n - i, ring, rd0, rd1, b, sc, acc);
 }
 
 // Where a segment's column lives.  Routed segments: column col is route
@@ -522,7 +549,7 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
       for (int h = 0; h < 2; ++h) dt.voff[m][h] = static_cast<uint32_t>(tile_row + 8 * h + dr) * rb + dc * 16;
       dt.soff[m] = wt.soff[m];
     }
-    gemv_tile_dma<NMAT, NCH, KS>(dt, K, kw, br, bvoff, smem + wave * 2 * NMAT * kTileBytes, acc);
+    gemv_tile_dma<NMAT, NCH, KS>(dt, K, kw, br, bvoff, smem + wave * dma_depth<NMAT>() * NMAT * kTileBytes, acc);
   } else {
     gemv_tile<FMT, NMAT, NCH, KS>(wt, K, kw, br, bvoff, acc);
   }
@@ -593,7 +620,7 @@ constexpr int kRedFloats4 = kDecWaves * 8 * kWave;  // NMAT * chunks_per_pass <=
 template <int FMT_R, int FMT_S, int STAGE, int RT, int KS>
 __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) decode_stage_kernel(DecodeArgs a) {
   constexpr int kNmat = STAGE == 0 ? 2 * RT : RT;
-  constexpr int kRing = (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? kDecWaves * 2 * kNmat * kTileBytes : 0;
+  constexpr int kRing = (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? kDecWaves * dma_depth<kNmat>() * kNmat * kTileBytes : 0;
   constexpr int kRed = KS > 1 ? kRedFloats4 * 16 : 0;
   constexpr int kSmem = kRing > kRed ? kRing : kRed > 16 ? kRed : 16;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kSmem];
