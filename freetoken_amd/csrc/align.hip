@@ -64,11 +64,14 @@ __global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int w = tid / kWave;
-  const int chunk = ((a.numel + kAlignWaves - 1) / kAlignWaves + kWave - 1) / kWave * kWave;
-  const int c0 = w * chunk;
+  // routes go to the first nw waves (64 or more each); the others only help
+  // with the per-expert work
+  const int nw = min(kAlignWaves, max(1, (a.numel + kWave - 1) / kWave));
+  const int chunk = ((a.numel + nw - 1) / nw + kWave - 1) / kWave * kWave;
+  const int c0 = min(a.numel, w * chunk);
   const int c1 = min(a.numel, c0 + chunk);
 
-  for (int i = tid; i < kAlignWaves * eff; i += kAlignThreads) wcount[i] = 0;
+  for (int i = tid; i < nw * eff; i += kAlignThreads) wcount[i] = 0;
   if (a.stats)
     for (int i = tid; i < a.table_size; i += kAlignThreads) seen[i] = 0;
   __syncthreads();
@@ -97,7 +100,7 @@ __global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
     const int e = tid * per + q;
     if (e < eff) {
       int acc = 0;
-      for (int v = 0; v < kAlignWaves; ++v) {
+      for (int v = 0; v < nw; ++v) {
         const int t = wcount[v * eff + e];
         wcount[v * eff + e] = acc;
         acc += t;
@@ -136,8 +139,9 @@ __global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
   // sentinel fill (ordered before the scatter by the barrier below)
   for (int i = tid; i < a.max_padded; i += kAlignThreads) a.sorted_ids[i] = a.numel;
   __syncthreads();
-  // expert id of every used block; -1 for unused blocks
-  for (int b = tid; b < a.max_blocks; b += kAlignThreads) {
+  // expert id of every used block; -1 for unused blocks (callers that read only
+  // the segments pass no expert_ids)
+  for (int b = tid; a.expert_ids && b < a.max_blocks; b += kAlignThreads) {
     int e = -1;
     if (b * a.block_size < total) {
       int lo = 0, hi = eff;  // largest e with cum[e] <= b*bs and cnt[e] > 0
@@ -438,12 +442,10 @@ namespace ftmoe {
 __global__ void __launch_bounds__(1024) slot_map_kernel(const int32_t* ids, int numel, const int32_t* slot_for_id,
                                                         int table_size, int32_t* slot_ids, uint8_t* miss_mask,
                                                         long long* stats) {
-  extern __shared__ int seen[];
-  __shared__ unsigned long long s_missed;
+  extern __shared__ int seen[];  // per expert: 0 unseen, 1 resident, 2 missing
   const int tid = threadIdx.x;
   if (stats) {
     for (int i = tid; i < table_size; i += blockDim.x) seen[i] = 0;
-    if (tid == 0) s_missed = 0;
     __syncthreads();
   }
   unsigned long long missed = 0;
@@ -453,31 +455,24 @@ __global__ void __launch_bounds__(1024) slot_map_kernel(const int32_t* ids, int 
     const int s = valid ? slot_for_id[e] : -1;
     slot_ids[i] = s;
     if (miss_mask) miss_mask[i] = (valid && s < 0) ? 1 : 0;
-    if (stats && valid) seen[e] = 1;
+    if (stats && valid) seen[e] = s < 0 ? 2 : 1;  // every writer of e stores the same value
     missed += (valid && s < 0) ? 1 : 0;
   }
   if (!stats) return;
-  __shared__ unsigned long long s_act, s_miss;
-  if (tid == 0) {
-    s_act = 0;
-    s_miss = 0;
-  }
-  if (missed) atomicAdd(&s_missed, missed);
   __syncthreads();
   unsigned long long act = 0, miss = 0;
-  for (int e = tid; e < table_size; e += blockDim.x)
-    if (seen[e]) {
-      ++act;
-      miss += slot_for_id[e] < 0 ? 1 : 0;
-    }
-  if (act) atomicAdd(&s_act, act);
-  if (miss) atomicAdd(&s_miss, miss);
-  __syncthreads();
-  if (tid == 0) {
-    stats[0] += static_cast<long long>(s_act);
-    stats[1] += static_cast<long long>(s_miss);
-    stats[2] += 1;
-    stats[3] += static_cast<long long>(s_missed);
+  for (int e = tid; e < table_size; e += blockDim.x) {
+    act += seen[e] != 0;
+    miss += seen[e] == 2;
+  }
+  // order-free integer sums straight into the counters (no read-back)
+  const unsigned long long t_act = wave_sum_u64(act), t_miss = wave_sum_u64(miss), t_missed = wave_sum_u64(missed);
+  auto* st = reinterpret_cast<unsigned long long*>(stats);
+  if (lane_id() == 0) {
+    if (t_act) atomicAdd(st + 0, t_act);
+    if (t_miss) atomicAdd(st + 1, t_miss);
+    if (t_missed) atomicAdd(st + 3, t_missed);
+    if (tid == 0) atomicAdd(st + 2, 1ull);
   }
 }
 

@@ -63,7 +63,6 @@ int check_bank(const ftmoe_bank* b, const char* name, bool shared) {
 
 struct DecodeLayout {
   int32_t* sorted;
-  int32_t* expert_ids;
   int32_t* ntpp;
   int32_t* seg_expert;
   int32_t* seg_start;
@@ -81,7 +80,6 @@ DecodeLayout decode_layout(void* ws, int M, int k, const ftmoe_bank* bank, const
   Carver c{static_cast<uint8_t*>(ws)};
   const int numel = M * k;
   L.sorted = c.take<int32_t>(numel);
-  L.expert_ids = c.take<int32_t>(numel);
   L.ntpp = c.take<int32_t>(1);
   const int max_seg = ftmoe::decode_max_segments(numel, bank->num_rows);
   L.seg_expert = c.take<int32_t>(max_seg);
@@ -317,8 +315,11 @@ int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, c
   al.num_experts = bank->num_rows;
   al.block_size = 1;
   al.sorted_ids = L.sorted;
-  ftmoe_align_sizes(numel, bank->num_rows, 1, &al.max_padded, &al.max_blocks);
-  al.expert_ids = L.expert_ids;
+  // the decode kernels read the segments only: no block expert ids, no
+  // sentinel fill of the unused tail
+  al.max_padded = 0;
+  al.max_blocks = 0;
+  al.expert_ids = nullptr;
   al.ntpp = L.ntpp;
   al.seg_expert = L.seg_expert;
   al.seg_start = L.seg_start;

@@ -675,7 +675,9 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
   const int t = idx / per_tok;
   const int h = (idx - t * per_tok) * 8;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  // routes in groups of 8: all loads of a group are issued before the adds
+  // routes in groups of 8: all loads of a group, ids and ic3 rows alike, are
+  // issued before the adds (the ic3 row of route r is t*k + r whatever its id;
+  // rows of skipped routes hold stale data and are dropped by the id test)
   for (int r0 = 0; r0 < k; r0 += 8) {
     u32x4 v[8];
     bool ok[8];
@@ -684,7 +686,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
       const int r = r0 + q;
       const int e = r < k ? ids[t * k + r] : -1;
       ok[q] = e >= 0 && e < num_rows;
-      if (ok[q]) v[q] = *reinterpret_cast<const u32x4*>(ic3 + static_cast<size_t>(t * k + r) * H + h);
+      v[q] = r < k ? *reinterpret_cast<const u32x4*>(ic3 + static_cast<size_t>(t * k + r) * H + h) : u32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int q = 0; q < 8; ++q) {

@@ -132,6 +132,14 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return (a + b) + (c + d);
 }
 
+// Wave-wide sum of small non-negative counts (the result is uniform).
+__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
+  uint32_t x = static_cast<uint32_t>(v);
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) x += static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), off, kWave));
+  return x;
+}
+
 __device__ __forceinline__ float wave_max_f32(float v) {
   v = fmaxf(v, dpp_f32<0xB1>(v));
   v = fmaxf(v, dpp_f32<0x4E>(v));

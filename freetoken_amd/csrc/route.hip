@@ -85,12 +85,40 @@ __global__ void __launch_bounds__(kRouteWaves * kWave) softmax_topk_kernel(const
   }
 }
 
+// Multiset top-2 of two disjoint sets given as (largest, second largest).
+__device__ __forceinline__ void top2_merge(float& a1, float& a2, float b1, float b2) {
+  const float lo = fminf(a1, b1);
+  a1 = fmaxf(a1, b1);
+  a2 = fmaxf(lo, fmaxf(a2, b2));
+}
+
+template <int CTRL>
+__device__ __forceinline__ void top2_dpp(float& a1, float& a2) {
+  top2_merge(a1, a2, dpp_f32<CTRL>(a1), dpp_f32<CTRL>(a2));
+}
+
+// Top-2 of every aligned block of `per` lanes (per a power of two <= 64), left
+// in all lanes of the block: butterflies over disjoint halves (DPP inside a
+// 16-lane row, lane shuffles across rows).
+__device__ __forceinline__ void block_top2(float& a1, float& a2, int per) {
+  if (per >= 2) top2_dpp<0xB1>(a1, a2);   // quad_perm [1,0,3,2]
+  if (per >= 4) top2_dpp<0x4E>(a1, a2);   // quad_perm [2,3,0,1]
+  if (per >= 8) top2_dpp<0x141>(a1, a2);  // row_half_mirror
+  if (per >= 16) top2_dpp<0x140>(a1, a2); // row_mirror
+  if (per >= 32) top2_merge(a1, a2, __shfl_xor(a1, 16), __shfl_xor(a2, 16));
+  if (per >= 64) top2_merge(a1, a2, __shfl_xor(a1, 32), __shfl_xor(a2, 32));
+}
+
 // Grouped sigmoid router (reference models/glm4_moe/moe.py:53-75):
 //   s = sigmoid(l); c = s + bias; group score = top1(c) + top2(c) in the group;
 //   keep topk_group groups; top-k of c over kept groups; w = s[id];
 //   renorm w / (sum + 1e-20); times scale.  Uses det_sigmoid so the selection
-//   is bit-identical to the CPU oracle.  Group scores: the wave stages c in LDS
-//   and lane g scans group g.
+//   is bit-identical to the CPU oracle.  Group scores: when the group size is a
+//   power of two dividing 64 (DeepSeek-V3: 32) and E is a multiple of 64, a
+//   group is an aligned lane block of one register slot and its top-2 is a
+//   butterfly (block_top2); otherwise the wave stages c in LDS and lane g scans
+//   group g.  The weights s[id] come from the lanes holding them (shuffles),
+//   not from a second read of the logits.
 template <int PER>
 __global__ void __launch_bounds__(kRouteWaves * kWave) grouped_sigmoid_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int M, int E, int n_group, int topk_group,
@@ -102,19 +130,44 @@ __global__ void __launch_bounds__(kRouteWaves * kWave) grouped_sigmoid_kernel(
   if (tok >= M) return;
   const float* row = logits + static_cast<size_t>(tok) * E;
   const int per = E / n_group;
-  float c[PER];
+  float sg[PER], c[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int e = lane + j * kWave;
     if (e < E) {
-      const float s = det_sigmoid(row[e]);
-      c[j] = bias ? s + bias[e] : s;
+      sg[j] = det_sigmoid(row[e]);
+      c[j] = bias ? sg[j] + bias[e] : sg[j];
     } else {
+      sg[j] = 0.0f;
       c[j] = -INFINITY;
     }
   }
   uint64_t gmask = ~0ull;
-  if (n_group > 1) {
+  const bool lane_groups = (E % kWave) == 0 && per <= kWave && (per & (per - 1)) == 0;
+  if (n_group > 1 && lane_groups) {
+    // group of (lane, slot j) = j * (64 / per) + lane / per
+    const int gpl = kWave / per;
+    uint64_t gk[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      float a1 = c[j], a2 = -INFINITY;
+      block_top2(a1, a2, per);
+      const int grp = j * gpl + lane / per;
+      gk[j] = (lane % per == 0 && lane + j * kWave < E) ? pack_key(a1 + a2, grp) : 0;
+    }
+    gmask = 0;
+    for (int r = 0; r < topk_group; ++r) {
+      uint64_t best = 0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) best = max_u64(best, gk[j]);
+      best = wave_max_u64(best);
+      const int win = static_cast<int>(~static_cast<uint32_t>(best));
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (gk[j] == best) gk[j] = 0;
+      gmask |= 1ull << win;
+    }
+  } else if (n_group > 1) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) s_c[wave][lane + j * kWave] = c[j];
     __builtin_amdgcn_wave_barrier();
@@ -150,7 +203,12 @@ __global__ void __launch_bounds__(kRouteWaves * kWave) grouped_sigmoid_kernel(
     keys[j] = (e < E) ? pack_key(kept ? c[j] : -INFINITY, e) : 0;
   }
   const int my_idx = select_topk<PER>(keys, k);
-  float w = (lane < k) ? det_sigmoid(row[my_idx]) : 0.0f;
+  float w = 0.0f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const float t = __shfl(sg[j], my_idx & (kWave - 1));
+    if (lane < k && (my_idx >> 6) == j) w = t;
+  }
   if (renorm) {
     float tot = 0.0f;  // sequential sum in rank order, as the oracle does
     for (int r = 0; r < k; ++r) tot += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(w), r));

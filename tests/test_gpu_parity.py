@@ -58,6 +58,24 @@ def test_grouped_sigmoid_exact(dev, M, with_bias):
     np.testing.assert_allclose(to_np(w), w_ref, rtol=1e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("E,n_group,topk_group,k", [
+    (64, 32, 8, 8), (128, 16, 4, 8), (256, 16, 4, 8), (256, 8, 4, 8), (128, 2, 1, 8), (320, 5, 2, 8),
+    (1024, 64, 8, 16),  # group sizes 2..64, a power of two dividing the wave: lane-block butterflies
+    (96, 8, 4, 8), (160, 5, 2, 8), (40, 4, 2, 4),  # other group sizes or E: the LDS scan
+])
+def test_grouped_sigmoid_group_shapes(dev, E, n_group, topk_group, k):
+    rng = np.random.default_rng(E * 131 + n_group)
+    lg = synth.tied_logits(rng, 33, E, bf16=False)
+    lg[0] = 0.25  # every group and expert tied
+    bias = synth.normal(rng, (E,), 0.05)
+    for b in (None, bias):
+        w_ref, ids_ref = oracle.routing.grouped_sigmoid_topk(lg, b, n_group, topk_group, k, True, 2.5)
+        tb = None if b is None else torch.from_numpy(b).to(dev)
+        w, ids = ops.route_grouped_sigmoid(torch.from_numpy(lg).to(dev), tb, n_group, topk_group, k, True, 2.5)
+        np.testing.assert_array_equal(to_np(ids), ids_ref)
+        np.testing.assert_allclose(to_np(w), w_ref, rtol=1e-6, atol=1e-7)
+
+
 def test_grouped_sigmoid_ties_and_flips(dev):
     E, G = 64, 8
     lg = np.zeros((4, E), dtype=np.float32)  # all equal: lowest groups, lowest experts
