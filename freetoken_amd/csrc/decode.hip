@@ -261,25 +261,56 @@ __device__ __forceinline__ void gemv_tile(const WTiles<NMAT>& wt, int K, int kw,
     if (i + s < n) compute_stage(st[s], acc);
 }
 
-// FP8 weights stream through LDS instead of registers.  A register load
-// instruction can cover at most 64 bytes of a row (4 lanes of 16 bytes share a
-// row in the MFMA operand layout), so the two halves of each 128-byte line are
-// fetched by different instructions and the line has to stay in L2 between
-// them.  A DMA instruction (buffer load to LDS) is free to give its 64 lanes 8
-// whole rows: each fetches complete lines, which lets the weights use the
-// nontemporal policy (measured on MI355X: 7.1 TB/s against 6.2 TB/s for the
-// default policy on a plain stream).  Each wave owns a ring of stages in LDS
-// (dma_depth); a stage holds NMAT tiles of 16 rows x 128 bytes (one K block).  Chunk c
-// (16 bytes) of tile row r lands at slot c ^ (r & 7) of the row, spreading the
-// operand reads over the LDS banks.
+// Quantised weights (FP8, MXFP4) stream through LDS instead of registers.  A
+// register load instruction can cover at most 64 bytes of a row (4 lanes of
+// 16 bytes share a row in the MFMA operand layout), so the two halves of each
+// 128-byte line are fetched by different instructions and the line has to
+// stay in L2 between them.  A DMA instruction (buffer load to LDS) is free to
+// give its 64 lanes 8 whole rows: each fetches complete lines, which lets the
+// weights use the nontemporal policy (measured on MI355X: 7.1 TB/s against
+// 6.2 TB/s for the default policy on a plain stream).  A K step covers 128
+// bytes of every row: one K block of FP8, two of MXFP4.  Each wave owns a ring
+// of stages in LDS (dma_depth); a stage holds NMAT tiles of 16 rows x 128
+// bytes.  Chunk c (16 bytes) of tile row r lands at slot c ^ (r & 7) of the
+// row, spreading the operand reads over the LDS banks.  A lane's operands are
+// chunks g and 4 + g of its row: FP8 values 16g.. and 64 + 16g.. of the K
+// block (MFMAs 0, 1 and 2, 3); MXFP4 values 32g.. of the first and of the
+// second K block of the step.
 constexpr int kTileBytes = 16 * 128;
 constexpr int kNtPolicy = 2;  // cache policy bits of a nontemporal load
+
+template <int FMT>
+constexpr int dma_kstep() {  // K values per step
+  return FMT == FMT_FP8 ? 128 : 256;
+}
+template <int FMT>
+constexpr int dma_pieces() {  // activation loads (16 bytes) per chunk and step
+  return FMT == FMT_FP8 ? 4 : 8;
+}
+template <int FMT, int NMAT, int NCH>
+constexpr int dma_per_step() {  // vector memory instructions of one dma_issue
+  return 3 * NMAT + dma_pieces<FMT>() * NCH;
+}
+
+// Per-step side data of a tile: FP8 the 128x128 block scale (wave-uniform);
+// MXFP4 the lane's row of e8m0 codes for the step's two K blocks (byte g of
+// each word is the lane group's code).
+template <int FMT>
+struct DmaSide;
+template <>
+struct DmaSide<FMT_FP8> {
+  float s;
+};
+template <>
+struct DmaSide<FMT_MXFP4> {
+  uint2 codes;
+};
 
 template <int NMAT>
 struct DmaTiles {
   __amdgpu_buffer_rsrc_t wr, sr;
   uint32_t voff[NMAT][2];  // lane's DMA source in instruction h (rows 8h..8h+7) of tile m
-  uint32_t soff[NMAT];     // tile's scale row (wave-uniform)
+  uint32_t soff[NMAT];     // FP8: tile's scale row (wave-uniform); MXFP4: lane's code row
 };
 
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, uint32_t soff) {
@@ -287,22 +318,30 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds
                                            kNtPolicy);
 }
 
-template <int NMAT, int NCH>
+template <int FMT, int NMAT, int NCH>
 __device__ __forceinline__ void dma_issue(const DmaTiles<NMAT>& dt, __amdgpu_buffer_rsrc_t br,
-                                          const uint32_t (&bvoff)[NCH], uint8_t* stage, int kb, uint32_t dead,
-                                          u32x4 (&b)[NCH][4], float (&sc)[NMAT]) {
-  const uint32_t so = static_cast<uint32_t>(kb) * 128;
+                                          const uint32_t (&bvoff)[NCH], uint8_t* stage, int step, uint32_t dead,
+                                          u32x4 (&b)[NCH][dma_pieces<FMT>()], DmaSide<FMT> (&side)[NMAT]) {
+  const uint32_t so = static_cast<uint32_t>(step) * 128;
 #pragma unroll
   for (int m = 0; m < NMAT; ++m)
 #pragma unroll
     for (int h = 0; h < 2; ++h) lds_dma16(dt.wr, stage + m * kTileBytes + h * 1024, dt.voff[m][h] | dead, so);
 #pragma unroll
-  for (int m = 0; m < NMAT; ++m) sc[m] = buf_f32(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(kb) * 4);
-  const uint32_t sb = static_cast<uint32_t>(kb) * 256;
+  for (int m = 0; m < NMAT; ++m) {
+    if constexpr (FMT == FMT_FP8)
+      side[m].s = buf_f32(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(step) * 4);
+    else
+      side[m].codes = buf_x2(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(step) * 8);
+  }
+  const uint32_t sb = static_cast<uint32_t>(step) * dma_kstep<FMT>() * 2;
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) b[c][j] = buf_x4(br, (bvoff[c] | dead) + b_piece_bytes<FMT_FP8>(j), sb);
+    for (int j = 0; j < dma_pieces<FMT>(); ++j) {
+      const uint32_t piece = FMT == FMT_FP8 ? b_piece_bytes<FMT_FP8>(j) : 256 * (j >> 2) + b_piece_bytes<FMT_MXFP4>(j & 3);
+      b[c][j] = buf_x4(br, (bvoff[c] | dead) + piece, sb);
+    }
 }
 
 template <int N>
@@ -310,99 +349,129 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// The lane's operand bytes sit at rd0 (MFMAs 0, 1) and rd1 (MFMAs 2, 3) inside
-// a tile: row r16, chunks g and 4 + g.
-template <int NMAT, int NCH>
-__device__ __forceinline__ void dma_compute(const uint8_t* stage, uint32_t rd0, uint32_t rd1,
-                                            const u32x4 (&b)[NCH][4], const float (&sc)[NMAT],
-                                            f32x4 (&acc)[NMAT][NCH]) {
+// One step of one stage: operands from LDS at rd0, rd1 (chunks g and 4 + g of
+// row r16), dequantised exactly to bf16, then the MFMAs (FP8: the block scale
+// folds each K block's partial into acc; MXFP4: the e8m0 scale is exact in the
+// dequant, acc chains through both K blocks in order).
+template <int FMT, int NMAT, int NCH>
+__device__ __forceinline__ void dma_compute(const uint8_t* stage, uint32_t rd0, uint32_t rd1, int gsh,
+                                            const u32x4 (&b)[NCH][dma_pieces<FMT>()],
+                                            const DmaSide<FMT> (&side)[NMAT], f32x4 (&acc)[NMAT][NCH]) {
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  RawA<FMT_FP8> w[NMAT];
+  u32x4 w0[NMAT], w1[NMAT];
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) {
-    w[m].v[0] = *reinterpret_cast<const u32x4*>(stage + m * kTileBytes + rd0);
-    w[m].v[1] = *reinterpret_cast<const u32x4*>(stage + m * kTileBytes + rd1);
+    w0[m] = *reinterpret_cast<const u32x4*>(stage + m * kTileBytes + rd0);
+    w1[m] = *reinterpret_cast<const u32x4*>(stage + m * kTileBytes + rd1);
   }
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) {
-    bf16x8 a[4];
-    dequant<FMT_FP8>(w[m], a);
+    if constexpr (FMT == FMT_FP8) {
+      RawA<FMT_FP8> r;
+      r.v[0] = w0[m];
+      r.v[1] = w1[m];
+      bf16x8 a[4];
+      dequant<FMT_FP8>(r, a);
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      f32x4 t = zero;
+      for (int c = 0; c < NCH; ++c) {
+        f32x4 t = zero;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j], __builtin_bit_cast(bf16x8, b[c][j]), t, 0, 0, 0);
-      acc[m][c] += t * sc[m];
+        for (int j = 0; j < 4; ++j)
+          t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j], __builtin_bit_cast(bf16x8, b[c][j]), t, 0, 0, 0);
+        acc[m][c] += t * side[m].s;
+      }
+    } else {
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        RawA<FMT_MXFP4> r;
+        r.v[0] = blk == 0 ? w0[m] : w1[m];
+        r.code = ((blk == 0 ? side[m].codes.x : side[m].codes.y) >> gsh) & 0xffu;
+        bf16x8 a[4];
+        dequant<FMT_MXFP4>(r, a);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[m][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                a[j], __builtin_bit_cast(bf16x8, b[c][4 * blk + j]), acc[m][c], 0, 0, 0);
+      }
     }
   }
 }
 
-// Computes the stages T.. of the last `left` K blocks of a ring of S stages,
+// Computes the stages T.. of the last `left` steps of a ring of S stages,
 // waiting for each stage alone (the S-2-T stages behind it stay in flight).
-template <int S, int T, int NMAT, int NCH>
-__device__ __forceinline__ void dma_tail(int left, const uint8_t* ring, uint32_t rd0, uint32_t rd1,
-                                         const u32x4 (&b)[S][NCH][4], const float (&sc)[S][NMAT],
-                                         f32x4 (&acc)[NMAT][NCH]) {
+template <int FMT, int S, int T, int NMAT, int NCH>
+__device__ __forceinline__ void dma_tail(int left, const uint8_t* ring, uint32_t rd0, uint32_t rd1, int gsh,
+                                         const u32x4 (&b)[S][NCH][dma_pieces<FMT>()],
+                                         const DmaSide<FMT> (&side)[S][NMAT], f32x4 (&acc)[NMAT][NCH]) {
   if constexpr (T < S - 1) {
     if (left > T) {
-      wait_vmcnt<(S - 2 - T) * (3 * NMAT + 4 * NCH)>();
-      dma_compute(ring + T * NMAT * kTileBytes, rd0, rd1, b[T], sc[T], acc);
-      dma_tail<S, T + 1, NMAT, NCH>(left, ring, rd0, rd1, b, sc, acc);
+      wait_vmcnt<(S - 2 - T) * dma_per_step<FMT, NMAT, NCH>()>();
+      dma_compute<FMT, NMAT, NCH>(ring + T * NMAT * kTileBytes, rd0, rd1, gsh, b[T], side[T], acc);
+      dma_tail<FMT, S, T + 1, NMAT, NCH>(left, ring, rd0, rd1, gsh, b, side, acc);
     }
   }
 }
 
 // Ring depth of the LDS path: 2 stages of 4 tiles (64 KiB of LDS per
-// workgroup, two resident per CU) or 3 stages of 2 (measured against 2 and 4:
-// 3 is the fastest at b = 1 and no slower at b = 8 and 64).
-template <int NMAT>
+// workgroup, two resident per CU) or 3 stages of 2 (FP8 measured against 2
+// and 4: 3 is the fastest at b = 1 and no slower at b = 8 and 64; MXFP4 keeps
+// 2 when two route chunks make a stage's registers large).
+template <int FMT, int NMAT, int NCH>
 constexpr int dma_depth() {
-  return NMAT >= 4 ? 2 : 3;
+  return NMAT >= 4 ? 2 : (FMT == FMT_MXFP4 && NCH > 1) ? 2 : 3;
+}
+template <int FMT, int NMAT>
+constexpr int dma_ring_bytes() {  // per wave, the larger of the NCH variants
+  return (dma_depth<FMT, NMAT, 1>() > dma_depth<FMT, NMAT, 2>() ? dma_depth<FMT, NMAT, 1>()
+                                                                  : dma_depth<FMT, NMAT, 2>()) *
+         NMAT * kTileBytes;
 }
 
-// FP8 counterpart of gemv_tile: the same K range and accumulation order, the
-// weights through the wave's LDS ring of S stages (the DMA of the next S-1 K
-// blocks is in flight while one is computed; a dead step still issues,
-// reading zeros, so every step's wait count is exact).
-template <int NMAT, int NCH, int KS>
+// Counterpart of gemv_tile for FP8 and MXFP4: the same K range and
+// accumulation order, the weights through the wave's LDS ring of S stages (the
+// DMA of the next S-1 steps is in flight while one is computed; a dead step
+// still issues, reading zeros, so every step's wait count is exact).
+template <int FMT, int NMAT, int NCH, int KS>
 __device__ __forceinline__ void gemv_tile_dma(const DmaTiles<NMAT>& dt, int K, int kw, __amdgpu_buffer_rsrc_t br,
                                               const uint32_t (&bvoff)[NCH], uint8_t* ring,
                                               f32x4 (&acc)[NMAT][NCH]) {
-  constexpr int S = dma_depth<NMAT>();
+  constexpr int S = dma_depth<FMT, NMAT, NCH>();
+  constexpr int P = dma_pieces<FMT>();
   constexpr int kStage = NMAT * kTileBytes;
-  constexpr int kPerStep = 3 * NMAT + 4 * NCH;  // vector memory instructions of one dma_issue
   const int lane = lane_id(), r16 = lane & 15, g = lane >> 4;
   const uint32_t rd0 = r16 * 128 + ((g ^ (r16 & 7)) << 4);
   const uint32_t rd1 = r16 * 128 + (((4 + g) ^ (r16 & 7)) << 4);
-  const int nkb = K / 128;
-  const int kb_lo = kw * nkb / KS, kb_hi = (kw + 1) * nkb / KS;
-  const int n = kb_hi - kb_lo;
+  const int gsh = 8 * g;
+  const int nst = K / dma_kstep<FMT>();
+  const int st_lo = kw * nst / KS, st_hi = (kw + 1) * nst / KS;
+  const int n = st_hi - st_lo;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int m = 0; m < NMAT; ++m)
 #pragma unroll
     for (int c = 0; c < NCH; ++c) acc[m][c] = zero;
-  u32x4 b[S][NCH][4];
-  float sc[S][NMAT];
+  u32x4 b[S][NCH][P];
+  DmaSide<FMT> side[S][NMAT];
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
-    dma_issue(dt, br, bvoff, ring + s * kStage, kb_lo + s, s < n ? 0u : kOutOfRange, b[s], sc[s]);
+    dma_issue<FMT, NMAT, NCH>(dt, br, bvoff, ring + s * kStage, st_lo + s, s < n ? 0u : kOutOfRange, b[s], side[s]);
   int i = 0;
   for (; i + S <= n; i += S) {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       const int ahead = i + s + S - 1;
-      dma_issue(dt, br, bvoff, ring + ((s + S - 1) % S) * kStage, kb_lo + ahead, ahead < n ? 0u : kOutOfRange,
-                b[(s + S - 1) % S], sc[(s + S - 1) % S]);
-      wait_vmcnt<(S - 1) * kPerStep>();
+      dma_issue<FMT, NMAT, NCH>(dt, br, bvoff, ring + ((s + S - 1) % S) * kStage, st_lo + ahead,
+                                ahead < n ? 0u : kOutOfRange, b[(s + S - 1) % S], side[(s + S - 1) % S]);
+      wait_vmcnt<(S - 1) * dma_per_step<FMT, NMAT, NCH>()>();
       __builtin_amdgcn_sched_barrier(0);
-      dma_compute(ring + s * kStage, rd0, rd1, b[s], sc[s], acc);
+      dma_compute<FMT, NMAT, NCH>(ring + s * kStage, rd0, rd1, gsh, b[s], side[s], acc);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  // the last n - i < S blocks sit in stages 0.. (loaded above)
-  dma_tail<S, 0, NMAT, NCH>(n - i, ring, rd0, rd1, b, sc, acc);
+  // the last n - i < S steps sit in stages 0.. (loaded above)
+  dma_tail<FMT, S, 0, NMAT, NCH>(n - i, ring, rd0, rd1, gsh, b, side, acc);
 }
 
 // Where a segment's column lives.  Routed segments: column col is route
@@ -537,21 +606,26 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
       wt.soff[m] = static_cast<uint32_t>(tile_row / 128) * (K / 128) * 4;
   }
   f32x4 acc[NMAT][NCH];
-  if constexpr (FMT == FMT_FP8) {
-    DmaTiles<NMAT> dt;
-    dt.wr = wt.wr;
-    dt.sr = wt.sr;
-    const int dr = lane >> 3, dc = (lane & 7) ^ dr;  // DMA lane: row dr of 8, stored at slot lane & 7
+  // FP8 always, MXFP4 when a K step (two K blocks) divides K: the LDS path
+  constexpr bool kDma = FMT == FMT_FP8 || FMT == FMT_MXFP4;
+  if (kDma && K % dma_kstep<FMT>() == 0) {
+    if constexpr (kDma) {
+      DmaTiles<NMAT> dt;
+      dt.wr = wt.wr;
+      dt.sr = wt.sr;
+      const int dr = lane >> 3, dc = (lane & 7) ^ dr;  // DMA lane: row dr of 8, stored at slot lane & 7
 #pragma unroll
-    for (int m = 0; m < NMAT; ++m) {
-      const int tile_row = (STAGE == 0 && m >= RT) ? inter + wrow0 + 16 * (m - RT) : wrow0 + 16 * m;
+      for (int m = 0; m < NMAT; ++m) {
+        const int tile_row = (STAGE == 0 && m >= RT) ? inter + wrow0 + 16 * (m - RT) : wrow0 + 16 * m;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) dt.voff[m][h] = static_cast<uint32_t>(tile_row + 8 * h + dr) * rb + dc * 16;
-      dt.soff[m] = wt.soff[m];
+        for (int h = 0; h < 2; ++h) dt.voff[m][h] = static_cast<uint32_t>(tile_row + 8 * h + dr) * rb + dc * 16;
+        dt.soff[m] = FMT == FMT_FP8 ? wt.soff[m] : static_cast<uint32_t>(tile_row + r16) * (K / 32);
+      }
+      gemv_tile_dma<FMT, NMAT, NCH, KS>(dt, K, kw, br, bvoff, smem + wave * dma_ring_bytes<FMT, NMAT>(), acc);
     }
-    gemv_tile_dma<NMAT, NCH, KS>(dt, K, kw, br, bvoff, smem + wave * dma_depth<NMAT>() * NMAT * kTileBytes, acc);
   } else {
-    gemv_tile<FMT, NMAT, NCH, KS>(wt, K, kw, br, bvoff, acc);
+    if constexpr (FMT != FMT_FP8)  // FP8 K is a multiple of 128: never here
+      gemv_tile<FMT, NMAT, NCH, KS>(wt, K, kw, br, bvoff, acc);
   }
 
   if constexpr (KS == 1) {
@@ -564,7 +638,7 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
           tile_epilogue<STAGE>(a, sv, cd[c], wrow0 + 16 * t + g * 4, acc[t][c], acc[STAGE == 0 ? RT + t : t][c]);
       }
   } else {
-    if constexpr (FMT == FMT_FP8) __syncthreads();  // red overlays the waves' LDS rings
+    if constexpr (kDma) __syncthreads();  // red overlays the waves' LDS rings
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
@@ -620,7 +694,9 @@ constexpr int kRedFloats4 = kDecWaves * 8 * kWave;  // NMAT * chunks_per_pass <=
 template <int FMT_R, int FMT_S, int STAGE, int RT, int KS>
 __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) decode_stage_kernel(DecodeArgs a) {
   constexpr int kNmat = STAGE == 0 ? 2 * RT : RT;
-  constexpr int kRing = (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? kDecWaves * dma_depth<kNmat>() * kNmat * kTileBytes : 0;
+  constexpr int kRingF8 = (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? dma_ring_bytes<FMT_FP8, kNmat>() : 0;
+  constexpr int kRingF4 = (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4) ? dma_ring_bytes<FMT_MXFP4, kNmat>() : 0;
+  constexpr int kRing = kDecWaves * (kRingF8 > kRingF4 ? kRingF8 : kRingF4);
   constexpr int kRed = KS > 1 ? kRedFloats4 * 16 : 0;
   constexpr int kSmem = kRing > kRed ? kRing : kRed > 16 ? kRed : 16;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kSmem];

@@ -173,6 +173,11 @@ __device__ __forceinline__ float buf_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 
+__device__ __forceinline__ uint2 buf_x2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+  return uint2{static_cast<uint32_t>(v[0]), static_cast<uint32_t>(v[1])};
+}
+
 __device__ __forceinline__ uint32_t buf_u8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, 0));
 }
