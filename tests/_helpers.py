@@ -11,6 +11,28 @@ from oracle.experts import Bank
 _FMT = {"bf16": "bf16", "fp8": "fp8_block", "mxfp4": "mxfp4"}
 
 
+def code_bank(fmt: str, rows: int, hidden: int, inter: int, rng: np.random.Generator) -> Bank:
+    """A quantised bank straight from random codes (every e4m3 code but NaN,
+    every e2m1 code) and random positive scales: full-size shapes in seconds,
+    where quantising normal weights takes minutes.  The oracle dequantises the
+    same bytes, so the comparison is unchanged."""
+    shapes = ((rows, 2 * inter, hidden), (rows, hidden, inter))
+    if fmt == "fp8":
+        mats, scales = [], []
+        for n, k in ((2 * inter, hidden), (hidden, inter)):
+            q = rng.integers(0, 256, size=(rows, n, k), dtype=np.uint8)
+            q[(q & 0x7F) == 0x7F] -= 1  # no NaN codes
+            mats.append(q)
+            scales.append(rng.uniform(0.5e-4, 1.5e-4, size=(rows, n // 128, k // 128)).astype(np.float32))
+        return Bank("fp8", mats[0], mats[1], scales[0], scales[1])
+    assert fmt == "mxfp4", fmt
+    mats, codes = [], []
+    for r, n, k in shapes:
+        mats.append(rng.integers(0, 256, size=(r, n, k // 2), dtype=np.uint8))
+        codes.append(rng.integers(118, 122, size=(r, n, k // 32), dtype=np.uint8))
+    return Bank("mxfp4", mats[0], mats[1], codes[0], codes[1])
+
+
 def to_device_bank(bank: Bank, dev, rows=None) -> ExpertBank:
     sl = slice(None) if rows is None else rows
 

@@ -12,7 +12,7 @@ from oracle import synth
 from oracle.numerics import bf16_round
 from freetoken_amd import ops
 
-from _helpers import bf16_dev, sub_bank, to_device_bank, to_np
+from _helpers import bf16_dev, code_bank, sub_bank, to_device_bank, to_np
 from conftest import COS_TOL, MAX_REL_TOL, cosine, max_rel
 
 pytestmark = pytest.mark.gpu
@@ -170,6 +170,39 @@ def test_decode_parity(dev, case, M):
     y_ref = oracle.experts.moe_layer("decode", x, w, ids, bank, shared)
     y = ops.experts_decode(bf16_dev(x, dev), torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev),
                            to_device_bank(bank, dev), to_device_bank(shared, dev) if shared else None)
+    got = to_np(y)
+    assert max_rel(got, y_ref) <= MAX_REL_TOL, (name, M, max_rel(got, y_ref))
+    assert cosine(got, y_ref) >= COS_TOL, (name, M, cosine(got, y_ref))
+
+
+# Full-size C4 and C3 matrices on a few experts: long K loops through the
+# weight rings (steady rounds and tails of every ring depth), two route chunks
+# at M = 40 (40 routes per expert: pieces of 32 and 8).
+FULL_SHAPE_CASES = [
+    ("c4_fp8_full_shape", "fp8", 10, 7168, 2048, 8, "fp8", 2048),
+    ("c3_mxfp4_full_shape", "mxfp4", 10, 5120, 1536, 8, "bf16", 1536),
+]
+_full_banks: dict = {}
+
+
+@pytest.mark.parametrize("case", FULL_SHAPE_CASES, ids=[c[0] for c in FULL_SHAPE_CASES])
+@pytest.mark.parametrize("M", [4, 40])
+def test_decode_parity_full_shapes(dev, case, M):
+    name, fmt, rows, H, I, k, sfmt, sI = case
+    if name not in _full_banks:
+        rng = np.random.default_rng(77)
+        bank = code_bank(fmt, rows, H, I, rng)
+        shared = code_bank(sfmt, 1, H, sI, rng) if sfmt != "bf16" else synth.make_bank("bf16", 1, H, sI, rng)
+        _full_banks.clear()
+        _full_banks[name] = (bank, shared, to_device_bank(bank, dev), to_device_bank(shared, dev))
+    bank, shared, dbank, dshared = _full_banks[name]
+    rng = np.random.default_rng(M)
+    x = synth.activations(rng, M, H)
+    ids = np.stack([rng.choice(rows, k, replace=False) for _ in range(M)]).astype(np.int32)
+    w = rng.random((M, k), dtype=np.float32)
+    w = (w / w.sum(1, keepdims=True)).astype(np.float32)
+    y_ref = oracle.experts.moe_layer("decode", x, w, ids, bank, shared)
+    y = ops.experts_decode(bf16_dev(x, dev), torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev), dbank, dshared)
     got = to_np(y)
     assert max_rel(got, y_ref) <= MAX_REL_TOL, (name, M, max_rel(got, y_ref))
     assert cosine(got, y_ref) >= COS_TOL, (name, M, cosine(got, y_ref))
