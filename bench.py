@@ -148,9 +148,10 @@ class DecodeLayer:
         return ops.route_grouped_sigmoid(logits, self.bias, c["n_group"], c["topk_group"], c["k"], True, c["scale"])
 
     def step(self, logits, x, out):
+        """Router, then the offload layer's decode: expert ids -> slot ids
+        (ensure_experts) and the experts in one call."""
         w, ids = self.route(logits)
-        ops.slot_map(ids, self.table, out=ids, stats=self.stats)
-        ops.experts_decode(x, w, ids, self.bank, shared=self.shared, out=out)
+        ops.experts_decode(x, w, ids, self.bank, shared=self.shared, out=out, slot_for_id=self.table, stats=self.stats)
         return ids
 
     def step_bytes(self, ids: torch.Tensor, M: int) -> tuple[int, int, int]:

@@ -52,6 +52,8 @@ SIGNATURES = {
     "ftmoe_act_quant_fp8": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "ftmoe_experts_decode_workspace": (_sz, [_i, _i, _bp, _bp]),
     "ftmoe_experts_decode": (_i, [_vp, _i, _i, _vp, _vp, _bp, _bp, _i, _i, _vp, _vp, _sz, _vp]),
+    "ftmoe_experts_decode_cached": (_i, [_vp, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _bp, _bp, _i, _i, _vp, _vp, _sz,
+                                         _vp]),
     "ftmoe_experts_prefill_workspace": (_sz, [_i, _i, _bp, _bp]),
     "ftmoe_experts_prefill": (_i, [_vp, _i, _i, _vp, _vp, _bp, _bp, _i, _vp, _vp, _sz, _vp]),
     "ftmoe_stage_timing_begin": (_i, []),

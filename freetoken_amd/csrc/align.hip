@@ -85,7 +85,7 @@ __global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
       const int s = valid ? a.slot_for_id[e] : -1;
       if (a.slot_ids) a.slot_ids[i] = s;
       if (a.miss_mask) a.miss_mask[i] = (valid && s < 0) ? 1 : 0;
-      if (a.stats && valid) seen[e] = 1;
+      if (a.stats && valid) seen[e] = s < 0 ? 2 : 1;  // every writer of e stores the same value
       if (valid && s < 0) ++missed;
       e = s;
     }
@@ -154,26 +154,21 @@ __global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
     a.expert_ids[b] = e;
   }
   if (a.stats) {
-    // distinct active / missing experts, counted in parallel
-    __shared__ unsigned long long s_act, s_miss;
-    if (tid == 0) {
-      s_act = 0;
-      s_miss = 0;
-    }
-    __syncthreads();
+    // distinct active / missing experts (seen since the barrier after pass 1)
+    // and missed routes: order-free integer sums straight into the counters
     unsigned long long act = 0, miss = 0;
-    for (int e = tid; e < a.table_size; e += kAlignThreads)
-      if (seen[e]) {
-        ++act;
-        miss += (a.slot_for_id[e] < 0) ? 1 : 0;
-      }
-    if (act) atomicAdd(&s_act, act);
-    if (miss) atomicAdd(&s_miss, miss);
-    __syncthreads();
-    if (tid == 0) {
-      a.stats[0] += static_cast<long long>(s_act);
-      a.stats[1] += static_cast<long long>(s_miss);
-      a.stats[2] += 1;
+    for (int e = tid; e < a.table_size; e += kAlignThreads) {
+      act += seen[e] != 0;
+      miss += seen[e] == 2;
+    }
+    const unsigned long long t_act = wave_sum_u64(act), t_miss = wave_sum_u64(miss);
+    const unsigned long long t_missed = wave_sum_u64(static_cast<unsigned long long>(missed));
+    auto* st = reinterpret_cast<unsigned long long*>(a.stats);
+    if (lane == 0) {
+      if (t_act) atomicAdd(st + 0, t_act);
+      if (t_miss) atomicAdd(st + 1, t_miss);
+      if (t_missed) atomicAdd(st + 3, t_missed);
+      if (tid == 0) atomicAdd(st + 2, 1ull);
     }
   }
 
@@ -218,15 +213,6 @@ __global__ void __launch_bounds__(kAlignThreads) align_kernel(AlignArgs a) {
     // A wave issues its LDS reads (above) before this write, so every lane saw
     // the base from before this batch.
     if (se < eff && tail) wcount[w * eff + se] += rank + 1;
-  }
-  if (a.stats) {
-    // routes that missed, summed over the workgroup
-    __shared__ long long s_missed;
-    if (tid == 0) s_missed = 0;
-    __syncthreads();
-    if (missed) atomicAdd(reinterpret_cast<unsigned long long*>(&s_missed), static_cast<unsigned long long>(missed));
-    __syncthreads();
-    if (tid == 0) a.stats[3] += s_missed;
   }
 }
 

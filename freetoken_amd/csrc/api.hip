@@ -273,10 +273,21 @@ size_t ftmoe_experts_decode_workspace(int M, int top_k, const ftmoe_bank* bank, 
   return decode_layout(nullptr, M, top_k, bank, shared).bytes;
 }
 
-int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
-                         const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
-                         int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
-                         ftmoe_stream_t stream) {
+namespace {
+
+// Optional expert-slot lookup in front of the decode permutation.
+struct SlotLookup {
+  const int32_t* slot_for_id;
+  int num_experts;
+  int32_t* slot_ids;
+  uint8_t* miss_mask;
+  int64_t* stats;
+};
+
+int experts_decode_impl(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
+                        const SlotLookup* slots, const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
+                        int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
+                        ftmoe_stream_t stream) {
   int rc = check_bank(bank, "routed", false);
   if (rc) return rc;
   if (shared) {
@@ -326,6 +337,15 @@ int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, c
   al.seg_count = L.seg_count;
   al.n_seg = L.n_seg;
   al.seg_cap = ftmoe::kDecodeSegCap;
+  if (slots) {
+    al.slot_for_id = slots->slot_for_id;
+    al.table_size = slots->num_experts;
+    al.slot_ids = slots->slot_ids;
+    al.miss_mask = slots->miss_mask;
+    al.stats = reinterpret_cast<long long*>(slots->stats);
+  }
+  // ids the later kernels see: slot ids when the lookup ran here
+  const int32_t* route_ids = slots ? slots->slot_ids : topk_ids;
   g_timer.start_call(stream);
   rc = check_hip(ftmoe::launch_align(al, stream), "experts_decode align");
   if (rc) return rc;
@@ -366,12 +386,35 @@ int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, c
                  "experts_decode down");
   if (rc) return rc;
   g_timer.mark();
-  rc = check_hip(ftmoe::launch_combine(L.ic3, topk_ids, bank->num_rows, L.sh_out, M, top_k, bank->hidden,
+  rc = check_hip(ftmoe::launch_combine(L.ic3, route_ids, bank->num_rows, L.sh_out, M, top_k, bank->hidden,
                                        static_cast<uint16_t*>(y), stream),
                  "experts_decode combine");
   g_timer.mark();
   g_timer.end_call();
   return rc;
+}
+
+}  // namespace
+
+int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
+                         const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
+                         int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
+                         ftmoe_stream_t stream) {
+  return experts_decode_impl(x, M, top_k, topk_w, topk_ids, nullptr, bank, shared, activation,
+                             apply_router_weight_on_input, y, workspace, workspace_bytes, stream);
+}
+
+int ftmoe_experts_decode_cached(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
+                                const int32_t* slot_for_id, int num_experts, int32_t* slot_ids, uint8_t* miss_mask,
+                                int64_t* stats, const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
+                                int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
+                                ftmoe_stream_t stream) {
+  if (!slot_for_id || !slot_ids) return fail(FTMOE_ERR_INVALID, "experts_decode_cached: NULL slot table or slot ids");
+  if (num_experts <= 0 || num_experts > 16384)
+    return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode_cached: num_experts=%d", num_experts);
+  const SlotLookup sl{slot_for_id, num_experts, slot_ids, miss_mask, stats};
+  return experts_decode_impl(x, M, top_k, topk_w, topk_ids, &sl, bank, shared, activation,
+                             apply_router_weight_on_input, y, workspace, workspace_bytes, stream);
 }
 
 size_t ftmoe_experts_prefill_workspace(int M, int top_k, const ftmoe_bank* bank, const ftmoe_bank* shared) {

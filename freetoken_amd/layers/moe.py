@@ -180,9 +180,11 @@ class OffloadMoELayer(MoELayer):
     def _decode_routed(self, hidden_states, topk_weights, topk_ids) -> torch.Tensor:
         cache = self.offload_cache
         assert cache is not None
-        cache.ensure_experts(self.layer_id, topk_ids)  # in place: expert ids -> slot ids
+        # ensure_experts (expert ids -> slot ids, in place) fused into the decode call
+        table, stats = cache.slot_lookup(self.layer_id)
         return ops.experts_decode(hidden_states, topk_weights, topk_ids, self._views_bank(cache.bank_views()),
-                                  shared=self.shared_expert, activation=self.activation)
+                                  shared=self.shared_expert, activation=self.activation, slot_for_id=table,
+                                  stats=stats)
 
     def _prefill_routed(self, hidden_states, topk_weights, topk_ids) -> torch.Tensor:
         cache = self.offload_cache

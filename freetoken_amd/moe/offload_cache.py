@@ -73,6 +73,12 @@ class ExpertSlotCache:
         ops.slot_map(expert_ids, self.slot_for_id[layer_id], out=expert_ids, miss_mask=miss_mask, stats=stats)
         return expert_ids
 
+    def slot_lookup(self, layer_id: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """(slot table, stats counters or None) of a layer, for decode calls that
+        do the ``ensure_experts`` rewrite themselves (``ops.experts_decode``
+        with ``slot_for_id``)."""
+        return self.slot_for_id[layer_id], (self.lru_stats[layer_id] if self.collect_stats else None)
+
     # -------------------------------------------------------------- statistics
     def reset_stats(self) -> None:
         self.lru_stats.zero_()

@@ -213,8 +213,15 @@ _WS = _Workspace()
 
 def experts_decode(x: torch.Tensor, topk_w: torch.Tensor, topk_ids: torch.Tensor, bank: ExpertBank,
                    shared: ExpertBank | None = None, activation: str = "silu",
-                   apply_router_weight_on_input: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
-    """Decode-regime experts (+ optional shared expert) for a precomputed routing."""
+                   apply_router_weight_on_input: bool = False, out: torch.Tensor | None = None,
+                   slot_for_id: torch.Tensor | None = None, miss_mask: torch.Tensor | None = None,
+                   stats: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode-regime experts (+ optional shared expert) for a precomputed routing.
+
+    With ``slot_for_id`` the bank rows are expert-cache slots and ``topk_ids``
+    holds expert ids: they are rewritten to slot ids in place (as ``slot_map``,
+    with the optional ``miss_mask`` and accumulated ``stats``) by the same call.
+    """
     if x.dtype != torch.bfloat16:
         raise ValueError("hidden_states must be bfloat16")
     if topk_w.dtype != torch.float32 or topk_ids.dtype != torch.int32:
@@ -234,11 +241,25 @@ def experts_decode(x: torch.Tensor, topk_w: torch.Tensor, topk_ids: torch.Tensor
     nbytes = lib().ftmoe_experts_decode_workspace(m, k, bp, sp)
     ws = _WS.get(x.device, nbytes)
     y = out if out is not None else torch.empty_like(x)
+    if slot_for_id is None:
+        check(
+            lib().ftmoe_experts_decode(_ptr(x), m, k, _ptr(topk_w), _ptr(topk_ids), bp, sp, _lib.ACT[activation],
+                                       int(apply_router_weight_on_input), _ptr(y), _ptr(ws), ws.numel(),
+                                       _stream(x.device)),
+            "experts_decode",
+        )
+        return y
+    if slot_for_id.dtype != torch.int32:
+        raise ValueError("slot_for_id must be int32")
+    if stats is not None and stats.dtype != torch.int64:
+        raise ValueError("stats must be int64[4]")
+    _require_gpu(slot_for_id, miss_mask, stats)
     check(
-        lib().ftmoe_experts_decode(_ptr(x), m, k, _ptr(topk_w), _ptr(topk_ids), bp, sp, _lib.ACT[activation],
-                                   int(apply_router_weight_on_input), _ptr(y), _ptr(ws), ws.numel(),
-                                   _stream(x.device)),
-        "experts_decode",
+        lib().ftmoe_experts_decode_cached(_ptr(x), m, k, _ptr(topk_w), _ptr(topk_ids), _ptr(slot_for_id),
+                                          slot_for_id.numel(), _ptr(topk_ids), _ptr(miss_mask), _ptr(stats), bp, sp,
+                                          _lib.ACT[activation], int(apply_router_weight_on_input), _ptr(y), _ptr(ws),
+                                          ws.numel(), _stream(x.device)),
+        "experts_decode_cached",
     )
     return y
 

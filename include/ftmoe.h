@@ -137,6 +137,20 @@ int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, c
                          int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
                          ftmoe_stream_t stream);
 
+/* Decode over an expert-slot cache in one call: the id -> slot rewrite of
+ * OffloadMoeCache.ensure_experts (moe/offload_cache.py:800-810, as
+ * ftmoe_slot_map: slot_ids[i] = slot_for_id[topk_ids[i]], -1 when absent or
+ * out of range, optional miss_mask and accumulated stats) followed by
+ * OffloadMoELayer.routed_forward (layers/moe.py:234-252) on the slot bank.
+ * The lookup rides in the permutation step, saving a launch per layer.
+ *   topk_ids: expert ids in [0, num_experts); slot_ids: int32 [M,k] out (may
+ *   alias topk_ids); bank rows are slots.  Workspace as ftmoe_experts_decode. */
+int ftmoe_experts_decode_cached(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
+                                const int32_t* slot_for_id, int num_experts, int32_t* slot_ids, uint8_t* miss_mask,
+                                int64_t* stats, const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
+                                int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
+                                ftmoe_stream_t stream);
+
 /* Prefill (grouped GEMM) expert computation for a precomputed routing;
  * replaces fused_experts_fp8_block (moe/fused_fp8_block.py:16-29 ->
  * kernel/triton/fp8_blockscale_moe.py:218-256, W8A8 with per-token per-128

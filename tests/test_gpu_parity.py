@@ -248,6 +248,47 @@ def test_decode_deterministic(dev):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("M", [1, 16, 64])
+def test_decode_cached_matches_slot_map_then_decode(dev, M):
+    """ftmoe_experts_decode_cached (slot lookup inside the decode permutation)
+    equals slot_map followed by experts_decode: slot ids, miss mask and
+    counters exactly, the output bit for bit; out-of-range ids included."""
+    rng = np.random.default_rng(23 + M)
+    E, S, H, I = 64, 16, 1024, 256
+    full = synth.make_bank("fp8", E, H, I, rng)
+    shared = synth.make_bank("fp8", 1, H, I, rng)
+    resident = np.sort(rng.choice(E, S, replace=False))
+    table = np.full(E, -1, dtype=np.int32)
+    table[resident] = np.arange(S, dtype=np.int32)
+    ids = np.stack([rng.choice(E, 8, replace=False) for _ in range(M)]).astype(np.int32)
+    ids[0, 0] = -1
+    if M > 1:
+        ids[1, 3] = E + 5
+    w = rng.random((M, 8), dtype=np.float32)
+    w = (w / w.sum(1, keepdims=True)).astype(np.float32)
+    x = bf16_dev(synth.activations(rng, M, H), dev)
+    bank, sh = to_device_bank(full, dev, resident), to_device_bank(shared, dev)
+    t_table, t_w = torch.from_numpy(table).to(dev), torch.from_numpy(w).to(dev)
+
+    ids_a = torch.from_numpy(ids).to(dev)
+    miss_a = torch.empty(ids.shape, dtype=torch.uint8, device=dev)
+    stats_a = torch.zeros(4, dtype=torch.int64, device=dev)
+    ops.slot_map(ids_a, t_table, out=ids_a, miss_mask=miss_a, stats=stats_a)
+    y_a = ops.experts_decode(x, t_w, ids_a, bank, sh)
+
+    ids_b = torch.from_numpy(ids).to(dev)
+    miss_b = torch.empty(ids.shape, dtype=torch.uint8, device=dev)
+    stats_b = torch.zeros(4, dtype=torch.int64, device=dev)
+    y_b = ops.experts_decode(x, t_w, ids_b, bank, sh, slot_for_id=t_table, miss_mask=miss_b, stats=stats_b)
+
+    slots_ref, miss_ref, stats_ref = oracle.slots.slot_map(ids, table)
+    np.testing.assert_array_equal(to_np(ids_b), slots_ref)
+    np.testing.assert_array_equal(to_np(miss_b), miss_ref)
+    np.testing.assert_array_equal(to_np(stats_b), stats_ref)
+    np.testing.assert_array_equal(to_np(stats_a), stats_ref)
+    assert torch.equal(y_a, y_b)
+
+
 def test_decode_slot_cache_misses(dev):
     """C4-style expert cache: routing over 64 experts, 16 resident slots; the
     non-resident routes are reported and excluded."""
