@@ -349,6 +349,10 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// s_barrier without the release fence of __syncthreads (which would wait for
+// every copy in flight); the clobber keeps LDS accesses on their side of it.
+__device__ __forceinline__ void bare_barrier_dec() { asm volatile("s_barrier" ::: "memory"); }
+
 // One step of one stage: operands from LDS at rd0, rd1 (chunks g and 4 + g of
 // row r16), dequantised exactly to bf16, then the MFMAs (FP8: the block scale
 // folds each K block's partial into acc; MXFP4: the e8m0 scale is exact in the
@@ -474,6 +478,147 @@ __device__ __forceinline__ void gemv_tile_dma(const DmaTiles<NMAT>& dt, int K, i
   dma_tail<FMT, S, 0, NMAT, NCH>(n - i, ring, rd0, rd1, gsh, b, side, acc);
 }
 
+// ---- Down stage: activations shared through LDS ----------------------------
+// In the down stage (KS = 1) the 4 waves of a workgroup walk the same K range
+// with the same route columns, so the activation chunks of a step are copied
+// once per workgroup (each wave DMAs a quarter of the columns) into a shared
+// ring of S + 1 slots instead of being loaded by every wave (measured: the
+// per-wave activation loads cost ~12% of the b = 64 down kernel).  A slot
+// holds NCH chunks of 16 columns x CB bytes (the step's K values in bf16);
+// 16-byte piece p of column c sits at slot position p ^ c, so the 16 columns
+// of one MFMA operand read hit distinct banks.  One barrier per step makes
+// every wave's copies visible; the extra slot means a refill never lands on a
+// slot another wave may still be reading (it was last read two steps before).
+template <int FMT>
+constexpr int act_col_bytes() {
+  return dma_kstep<FMT>() * 2;
+}
+template <int FMT>
+constexpr int act_copies() {  // 1 KB copies per wave per chunk and step
+  return 16 * act_col_bytes<FMT>() / 1024 / kDecWaves;
+}
+template <int FMT, int NCH>
+constexpr int act_slot_bytes() {
+  return NCH * 16 * act_col_bytes<FMT>();
+}
+template <int FMT, int NMAT, int NCH>
+constexpr int sh_per_step() {  // vector memory instructions of one sh_issue
+  return 3 * NMAT + NCH * act_copies<FMT>();
+}
+template <int FMT, int NMAT>
+constexpr int sh_act_ring_bytes() {  // the larger of the NCH variants (MXFP4 down runs one chunk per pass)
+  constexpr int one = (dma_depth<FMT, NMAT, 1>() + 1) * act_slot_bytes<FMT, 1>();
+  constexpr int two = (dma_depth<FMT, NMAT, 2>() + 1) * act_slot_bytes<FMT, 2>();
+  return FMT == FMT_MXFP4 || one > two ? one : two;
+}
+
+__device__ __forceinline__ void lds_dma16_cached(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+template <int FMT, int NMAT, int NCH>
+__device__ __forceinline__ void sh_issue(const DmaTiles<NMAT>& dt, __amdgpu_buffer_rsrc_t br,
+                                         const uint32_t (&avoff)[NCH][act_copies<FMT>()], uint8_t* wstage,
+                                         uint8_t* aslot, int wave, int step, uint32_t dead,
+                                         DmaSide<FMT> (&side)[NMAT]) {
+  constexpr int CB = act_col_bytes<FMT>();
+  const uint32_t so = static_cast<uint32_t>(step) * 128;
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) lds_dma16(dt.wr, wstage + m * kTileBytes + h * 1024, dt.voff[m][h] | dead, so);
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m) {
+    if constexpr (FMT == FMT_FP8)
+      side[m].s = buf_f32(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(step) * 4);
+    else
+      side[m].codes = buf_x2(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(step) * 8);
+  }
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+#pragma unroll
+    for (int v = 0; v < act_copies<FMT>(); ++v)
+      lds_dma16_cached(br, aslot + c * 16 * CB + (wave * act_copies<FMT>() + v) * 1024, avoff[c][v] | dead,
+                       static_cast<uint32_t>(step) * CB);
+}
+
+template <int FMT, int NMAT, int NCH>
+__device__ __forceinline__ void sh_compute(const uint8_t* wstage, const uint8_t* aslot, uint32_t rd0, uint32_t rd1,
+                                           int r16, int g, const DmaSide<FMT> (&side)[NMAT],
+                                           f32x4 (&acc)[NMAT][NCH]) {
+  constexpr int CB = act_col_bytes<FMT>();
+  constexpr int P = dma_pieces<FMT>();
+  u32x4 b[NCH][P];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      // piece (16 bytes) of the lane's MFMA operand j, then its swizzled position
+      const int pp = FMT == FMT_FP8 ? 8 * (j >> 1) + 2 * g + (j & 1) : 16 * (j >> 2) + 4 * g + (j & 3);
+      b[c][j] = *reinterpret_cast<const u32x4*>(aslot + c * 16 * CB + r16 * CB + ((pp ^ r16) << 4));
+    }
+  dma_compute<FMT, NMAT, NCH>(wstage, rd0, rd1, 8 * g, b, side, acc);
+}
+
+template <int FMT, int S, int SA, int T, int NMAT, int NCH>
+__device__ __forceinline__ void sh_tail(int left, int i, const uint8_t* ring, const uint8_t* aring, uint32_t rd0,
+                                        uint32_t rd1, int r16, int g, const DmaSide<FMT> (&side)[S][NMAT],
+                                        f32x4 (&acc)[NMAT][NCH]) {
+  if constexpr (T < S - 1) {
+    if (left > T) {
+      wait_vmcnt<(S - 2 - T) * sh_per_step<FMT, NMAT, NCH>()>();
+      bare_barrier_dec();
+      sh_compute<FMT, NMAT, NCH>(ring + T * NMAT * kTileBytes, aring + ((i + T) % SA) * act_slot_bytes<FMT, NCH>(),
+                                 rd0, rd1, r16, g, side[T], acc);
+      sh_tail<FMT, S, SA, T + 1, NMAT, NCH>(left, i, ring, aring, rd0, rd1, r16, g, side, acc);
+    }
+  }
+}
+
+// gemv_tile_dma for the down stage with the activations in the shared ring
+// (aring); route column col of chunk c reads activation row arow[c][...]
+// through the per-lane copy offsets avoff (kOutOfRange past the segment).
+template <int FMT, int NMAT, int NCH>
+__device__ __forceinline__ void gemv_tile_dma_sh(const DmaTiles<NMAT>& dt, int K, int wave,
+                                                 __amdgpu_buffer_rsrc_t br,
+                                                 const uint32_t (&avoff)[NCH][act_copies<FMT>()], uint8_t* ring,
+                                                 uint8_t* aring, f32x4 (&acc)[NMAT][NCH]) {
+  constexpr int S = dma_depth<FMT, NMAT, NCH>();
+  constexpr int SA = S + 1;
+  constexpr int kStage = NMAT * kTileBytes;
+  constexpr int kSlot = act_slot_bytes<FMT, NCH>();
+  const int lane = lane_id(), r16 = lane & 15, g = lane >> 4;
+  const uint32_t rd0 = r16 * 128 + ((g ^ (r16 & 7)) << 4);
+  const uint32_t rd1 = r16 * 128 + (((4 + g) ^ (r16 & 7)) << 4);
+  const int n = K / dma_kstep<FMT>();
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) acc[m][c] = zero;
+  DmaSide<FMT> side[S][NMAT];
+  bare_barrier_dec();  // the previous pass's last slots have been read by every wave
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    sh_issue<FMT, NMAT, NCH>(dt, br, avoff, ring + s * kStage, aring + s * kSlot, wave, s, s < n ? 0u : kOutOfRange,
+                             side[s]);
+  int i = 0;
+  for (; i + S <= n; i += S) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int t = i + s, ahead = t + S - 1;
+      sh_issue<FMT, NMAT, NCH>(dt, br, avoff, ring + ((s + S - 1) % S) * kStage, aring + (ahead % SA) * kSlot, wave,
+                               ahead, ahead < n ? 0u : kOutOfRange, side[(s + S - 1) % S]);
+      wait_vmcnt<(S - 1) * sh_per_step<FMT, NMAT, NCH>()>();
+      bare_barrier_dec();  // every wave's copies of step t have landed
+      __builtin_amdgcn_sched_barrier(0);
+      sh_compute<FMT, NMAT, NCH>(ring + s * kStage, aring + (t % SA) * kSlot, rd0, rd1, r16, g, side[s], acc);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  sh_tail<FMT, S, SA, 0, NMAT, NCH>(n - i, i, ring, aring, rd0, rd1, r16, g, side, acc);
+}
+
 // Where a segment's column lives.  Routed segments: column col is route
 // sorted[start + col]; shared pieces: column col is token start + col.
 struct SegView {
@@ -547,7 +692,7 @@ __device__ __forceinline__ void tile_epilogue(const DecodeArgs& a, const SegView
 // and are added in fixed wave order, so results do not depend on timing.
 template <int FMT, int STAGE, int RT, int KS, int NCH>
 __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView& bank, const SegView& sv, int base,
-                                            int row0, int inter, uint8_t* smem) {
+                                            int row0, int inter, uint8_t* smem, uint8_t* aring) {
   f32x4* red = reinterpret_cast<f32x4*>(smem);
   constexpr int NMAT = STAGE == 0 ? 2 * RT : RT;
   const int lane = lane_id();
@@ -621,7 +766,30 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
         for (int h = 0; h < 2; ++h) dt.voff[m][h] = static_cast<uint32_t>(tile_row + 8 * h + dr) * rb + dc * 16;
         dt.soff[m] = FMT == FMT_FP8 ? wt.soff[m] : static_cast<uint32_t>(tile_row + r16) * (K / 32);
       }
-      gemv_tile_dma<FMT, NMAT, NCH, KS>(dt, K, kw, br, bvoff, smem + wave * dma_ring_bytes<FMT, NMAT>(), acc);
+      uint8_t* ring = smem + wave * dma_ring_bytes<FMT, NMAT>();
+      if constexpr (STAGE == 1 && KS == 1) {
+        // activation copies: copy v of chunk c of this wave covers columns
+        // q * (1024 / CB) + lane / (CB / 16), q = wave * act_copies + v
+        constexpr int CB = act_col_bytes<FMT>();
+        uint32_t avoff[NCH][act_copies<FMT>()];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+          for (int v = 0; v < act_copies<FMT>(); ++v) {
+            const int colc = (wave * act_copies<FMT>() + v) * (1024 / CB) + lane / (CB / 16);
+            const int piece = (lane % (CB / 16)) ^ colc;
+            const int col = base + c * 16 + colc;
+            if (col < sv.count) {
+              const int row = sv.shared ? a.M * a.k + sv.start + col : a.sorted[sv.start + col];
+              avoff[c][v] = static_cast<uint32_t>(row) * bstride * 2 + piece * 16;
+            } else {
+              avoff[c][v] = kOutOfRange;
+            }
+          }
+        gemv_tile_dma_sh<FMT, NMAT, NCH>(dt, K, wave, br, avoff, ring, aring, acc);
+      } else {
+        gemv_tile_dma<FMT, NMAT, NCH, KS>(dt, K, kw, br, bvoff, ring, acc);
+      }
     }
   } else {
     if constexpr (FMT != FMT_FP8)  // FP8 K is a multiple of 128: never here
@@ -669,19 +837,19 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
 template <int FMT, int STAGE, int RT>
 constexpr int chunks_per_pass() {
   if constexpr (STAGE == 0) return RT == 1 ? 2 : (FMT == FMT_BF16 ? 1 : 2);
-  return 2;
+  return FMT == FMT_MXFP4 ? 1 : 2;  // MXFP4 down: one chunk keeps LDS at 80 KB (two workgroups per CU)
 }
 
 template <int FMT, int STAGE, int RT, int KS>
 __device__ __forceinline__ void decode_segment(const DecodeArgs& a, const BankView& bank, const SegView& sv, int row0,
-                                               int inter, uint8_t* smem) {
+                                               int inter, uint8_t* smem, uint8_t* aring) {
   constexpr int CMAX = chunks_per_pass<FMT, STAGE, RT>();
   for (int base = 0; base < sv.count; base += 16 * CMAX) {
     if constexpr (CMAX == 1) {
-      decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, smem);
+      decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, smem, aring);
     } else {
-      if (sv.count - base <= 16) decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, smem);
-      else decode_pass<FMT, STAGE, RT, KS, 2>(a, bank, sv, base, row0, inter, smem);
+      if (sv.count - base <= 16) decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, smem, aring);
+      else decode_pass<FMT, STAGE, RT, KS, 2>(a, bank, sv, base, row0, inter, smem, aring);
     }
   }
 }
@@ -697,8 +865,13 @@ __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves
   constexpr int kRingF8 = (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? dma_ring_bytes<FMT_FP8, kNmat>() : 0;
   constexpr int kRingF4 = (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4) ? dma_ring_bytes<FMT_MXFP4, kNmat>() : 0;
   constexpr int kRing = kDecWaves * (kRingF8 > kRingF4 ? kRingF8 : kRingF4);
+  // the down stage's shared activation ring follows the waves' weight rings
+  constexpr bool kShAct = STAGE == 1 && KS == 1;
+  constexpr int kActF8 = kShAct && (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? sh_act_ring_bytes<FMT_FP8, kNmat>() : 0;
+  constexpr int kActF4 = kShAct && (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4) ? sh_act_ring_bytes<FMT_MXFP4, kNmat>() : 0;
+  constexpr int kAct = kActF8 > kActF4 ? kActF8 : kActF4;
   constexpr int kRed = KS > 1 ? kRedFloats4 * 16 : 0;
-  constexpr int kSmem = kRing > kRed ? kRing : kRed > 16 ? kRed : 16;
+  constexpr int kSmem = kRing + kAct > kRed ? kRing + kAct : kRed > 16 ? kRed : 16;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kSmem];
   const int seg = blockIdx.y;
   SegView sv;
@@ -728,13 +901,13 @@ __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves
   const int fmt = sv.shared ? FMT_S : FMT_R;
   if (fmt == FMT_BF16) {
     if constexpr (FMT_R == FMT_BF16 || FMT_S == FMT_BF16)
-      decode_segment<FMT_BF16, STAGE, RT, KS>(a, bank, sv, row0, inter, smem);
+      decode_segment<FMT_BF16, STAGE, RT, KS>(a, bank, sv, row0, inter, smem, smem + kRing);
   } else if (fmt == FMT_FP8) {
     if constexpr (FMT_R == FMT_FP8 || FMT_S == FMT_FP8)
-      decode_segment<FMT_FP8, STAGE, RT, KS>(a, bank, sv, row0, inter, smem);
+      decode_segment<FMT_FP8, STAGE, RT, KS>(a, bank, sv, row0, inter, smem, smem + kRing);
   } else {
     if constexpr (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4)
-      decode_segment<FMT_MXFP4, STAGE, RT, KS>(a, bank, sv, row0, inter, smem);
+      decode_segment<FMT_MXFP4, STAGE, RT, KS>(a, bank, sv, row0, inter, smem, smem + kRing);
   }
 }
 
