@@ -913,7 +913,10 @@ __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves
 
 // y[t] = bf16( bf16(sum_r ic3[t,r]) + sh_out[t] ), routes with ids outside
 // [0, num_rows) skipped; sum in route order r = 0..k-1 in float32 (reference
-// moe_sum_reduce_kernel, kernel/triton/fused_moe.py:142-153).
+// moe_sum_reduce_kernel, kernel/triton/fused_moe.py:142-153).  STREAM: ic3 is
+// read once and is far larger than L2 (prefill), so its loads are nontemporal;
+// decode's ic3 was just written and is still in L2.
+template <bool STREAM>
 __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict__ ic3,
                                                       const int32_t* __restrict__ ids, int num_rows,
                                                       const uint16_t* __restrict__ sh_out, int M, int k, int H,
@@ -935,7 +938,8 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
       const int r = r0 + q;
       const int e = r < k ? ids[t * k + r] : -1;
       ok[q] = e >= 0 && e < num_rows;
-      v[q] = r < k ? *reinterpret_cast<const u32x4*>(ic3 + static_cast<size_t>(t * k + r) * H + h) : u32x4{0, 0, 0, 0};
+      const u32x4* src = reinterpret_cast<const u32x4*>(ic3 + static_cast<size_t>(t * k + r) * H + h);
+      v[q] = r >= k ? u32x4{0, 0, 0, 0} : STREAM ? __builtin_nontemporal_load(src) : *src;
     }
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
@@ -1061,8 +1065,13 @@ hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs
 hipError_t launch_combine(const uint16_t* ic3, const int32_t* ids, int num_rows, const uint16_t* sh_out, int M,
                           int k, int H, uint16_t* y, hipStream_t stream) {
   const int n = M * (H / 8);
-  hipLaunchKernelGGL(combine_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, ic3, ids, num_rows, sh_out, M, k,
-                     H, y);
+  // ic3 well beyond the 32 MB of L2 (prefill): stream it
+  if (static_cast<size_t>(M) * k * H * 2 > (size_t{64} << 20))
+    hipLaunchKernelGGL(combine_kernel<true>, dim3((n + 255) / 256), dim3(256), 0, stream, ic3, ids, num_rows, sh_out,
+                       M, k, H, y);
+  else
+    hipLaunchKernelGGL(combine_kernel<false>, dim3((n + 255) / 256), dim3(256), 0, stream, ic3, ids, num_rows, sh_out,
+                       M, k, H, y);
   return hipGetLastError();
 }
 

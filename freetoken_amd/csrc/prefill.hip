@@ -66,39 +66,71 @@ __device__ __forceinline__ float quant_value(float x, float s, float mul) {
   return fminf(fmaxf(y, -448.0f), 448.0f);
 }
 
+// Maximum over each 16-lane row of the wave (DPP inside the row), in every lane.
+__device__ __forceinline__ float row16_max_f32(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
+  return fmaxf(v, dpp_f32<0x140>(v));  // row_mirror
+}
+
+// One wave per row.  Lane l of load i holds 8 values (16 bytes) at
+// 8 * (64 i + l): the 16 lanes of a row of the wave cover one 128-value group,
+// whose amax is a DPP reduction inside the row.  kAhead loads of the row are
+// in flight together; x is read once (nontemporal).
 template <int MODE>
 __global__ void __launch_bounds__(256) act_quant_kernel(const uint16_t* __restrict__ x, int rows, int K,
                                                         uint8_t* __restrict__ q, void* __restrict__ scales) {
   const int lane = lane_id();
   const int row = blockIdx.x * 4 + threadIdx.x / kWave;
   if (row >= rows) return;
-  const uint32_t* xr = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(row) * K);
-  uint16_t* qr = reinterpret_cast<uint16_t*>(q + static_cast<size_t>(row) * K);
+  const u32x4* xr = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(row) * K);
+  uint2* qr = reinterpret_cast<uint2*>(q + static_cast<size_t>(row) * K);
   const int ng = K / 128;
-  constexpr int kAhead = 4;  // groups whose loads are in flight together
-  for (int g0 = 0; g0 < ng; g0 += kAhead) {
-    uint32_t pairs[kAhead];
-#pragma unroll
-    for (int u = 0; u < kAhead; ++u) pairs[u] = g0 + u < ng ? xr[(g0 + u) * 64 + lane] : 0u;
+  const int nv = K / 8;                  // 16-byte pieces of the row
+  const int nload = (nv + kWave - 1) / kWave;
+  constexpr int kAhead = 8;
+  for (int i0 = 0; i0 < nload; i0 += kAhead) {
+    u32x4 v[kAhead];
 #pragma unroll
     for (int u = 0; u < kAhead; ++u) {
-    const int gi = g0 + u;
-    if (gi >= ng) break;
-    const uint32_t pair = pairs[u];
-    const float a = bf16_to_f32(static_cast<uint16_t>(pair & 0xffffu));
-    const float b = bf16_to_f32(static_cast<uint16_t>(pair >> 16));
-    const float amax = wave_max_f32(fmaxf(fabsf(a), fabsf(b)));
-    float mul;
-    const float s = group_scale<MODE>(amax, mul);
-    const float qa = quant_value<MODE>(a, s, mul), qb = quant_value<MODE>(b, s, mul);
-    if (lane == 0) {
-      const size_t at = static_cast<size_t>(row) * ng + gi;
-      if (MODE == 0) static_cast<float*>(scales)[at] = s;
-      else if (MODE == 1) static_cast<uint8_t*>(scales)[at] = static_cast<uint8_t>(s);
-      else static_cast<uint32_t*>(scales)[at] = static_cast<uint32_t>(s);
+      const int p = (i0 + u) * kWave + lane;
+      v[u] = (i0 + u < nload && p < nv) ? __builtin_nontemporal_load(xr + p) : u32x4{0u, 0u, 0u, 0u};
     }
-    const uint32_t pk = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(qa, qb, 0, false));
-    qr[gi * 64 + lane] = static_cast<uint16_t>(pk & 0xffffu);
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) {
+      if (i0 + u >= nload) break;
+      const int p = (i0 + u) * kWave + lane;
+      const int gi = p / 16;  // the row's 16 lanes form group gi (uniform inside the row)
+      float f[8];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        f[2 * w] = bf16_to_f32(static_cast<uint16_t>(v[u][w] & 0xffffu));
+        f[2 * w + 1] = bf16_to_f32(static_cast<uint16_t>(v[u][w] >> 16));
+      }
+      float m = 0.f;
+#pragma unroll
+      for (int w = 0; w < 8; ++w) m = fmaxf(m, fabsf(f[w]));
+      const float amax = row16_max_f32(m);
+      if (p >= nv) continue;  // whole rows of lanes past the end (K not a multiple of 512)
+      float mul;
+      const float sc = group_scale<MODE>(amax, mul);
+      uint32_t pk[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float q0 = quant_value<MODE>(f[4 * h], sc, mul), q1 = quant_value<MODE>(f[4 * h + 1], sc, mul);
+        const float q2 = quant_value<MODE>(f[4 * h + 2], sc, mul), q3 = quant_value<MODE>(f[4 * h + 3], sc, mul);
+        uint32_t w4 = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0, false));
+        w4 = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(q2, q3, static_cast<int>(w4), true));
+        pk[h] = w4;
+      }
+      qr[p] = uint2{pk[0], pk[1]};
+      if ((lane & 15) == 0) {
+        const size_t at = static_cast<size_t>(row) * ng + gi;
+        if (MODE == 0) static_cast<float*>(scales)[at] = sc;
+        else if (MODE == 1) static_cast<uint8_t*>(scales)[at] = static_cast<uint8_t>(sc);
+        else static_cast<uint32_t*>(scales)[at] = static_cast<uint32_t>(sc);
+      }
     }
   }
 }
