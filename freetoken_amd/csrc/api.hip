@@ -445,6 +445,12 @@ int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, 
   const int numel = M * top_k;
   const int H = bank->hidden, I = bank->inter;
   const int fmt = bank->format;
+  // the quantised GEMMs address each operand (activations, one expert's
+  // weights) through a buffer descriptor with 31-bit offsets
+  if (fmt != FTMOE_FMT_BF16 && (static_cast<int64_t>(numel + M) * I > INT32_MAX ||
+                                static_cast<int64_t>(M) * H > INT32_MAX || 2 * static_cast<int64_t>(I) * H > INT32_MAX))
+    return fail(FTMOE_ERR_UNSUPPORTED, "experts_prefill: an operand beyond 2 GiB (M=%d top_k=%d H=%d I=%d)", M,
+                top_k, H, I);
 
   ftmoe::AlignArgs al{};
   al.ids = topk_ids;

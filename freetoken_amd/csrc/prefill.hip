@@ -28,6 +28,8 @@
 // all M blocks of that expert -- so the blocks sharing a weight tile run together
 // and read it from HBM about once; the expert's activation rows stay hot in the
 // memory-side cache across its N tiles.  Shared-expert blocks come last.
+#include <algorithm>
+
 #include "kernels.h"
 
 namespace ftmoe {
@@ -573,6 +575,24 @@ __device__ __forceinline__ bool map_tile_q(const PrefillGemmArgs& a, int b, bool
   return true;
 }
 
+// Lane index as an asm result: the compiler can neither hoist nor merge it,
+// so per-tile set-up code recomputes its lane-derived values instead of keeping
+// them live (or spilled) across the K loop.
+__device__ __forceinline__ int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+struct QTile {
+  bool shared;  // the shared expert's blocks (tokens in order) instead of a routed expert's
+  int expert, mblock, ntile;
+};
+
+__device__ __forceinline__ bool map_tile_q(const PrefillGemmArgs& a, int b, QTile& t) {
+  return map_tile_q(a, b, t.shared, t.expert, t.mblock, t.ntile);
+}
+
 // s_barrier without the memory fence of __syncthreads (which would wait for
 // every copy in flight); the clobber keeps the compiler from moving LDS
 // accesses across it.
@@ -585,13 +605,15 @@ __device__ __forceinline__ void wait_vm() {
 
 __device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// LDS-DMA copies: each lane's `bytes` from src land at dst + lane * bytes
-// (dst is wave-uniform).
-__device__ __forceinline__ void lds_copy16(const uint8_t* src, uint8_t* dst) {
-  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+// LDS-DMA copies through a buffer descriptor: each lane's 16 (4) bytes at lane
+// offset voff plus the wave-uniform soff land at dst + lane * 16 (4), dst
+// wave-uniform; a lane offset at or past the descriptor's range reads zeros
+// without memory traffic.
+__device__ __forceinline__ void lds_buf16(__amdgpu_buffer_rsrc_t r, uint8_t* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
 }
-__device__ __forceinline__ void lds_copy4(const uint8_t* src, uint8_t* dst) {
-  __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
+__device__ __forceinline__ void lds_buf4(__amdgpu_buffer_rsrc_t r, uint8_t* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, voff, soff, 0, 0);
 }
 
 // Chunk swizzles of the LDS lines, chosen by measurement (rocprofv3
@@ -613,55 +635,60 @@ __device__ __forceinline__ void pin(f32x4& v) { asm volatile("" : "+v"(v)); }
 template <int FMT, int GATE_UP>
 __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArgs a) {
   using L = QLds<FMT>;
-  constexpr int D = L::kStages - 1;  // prefetch distance in K steps
+  constexpr int S = L::kStages;
+  constexpr int D = S - 1;  // prefetch distance in K steps
   extern __shared__ __attribute__((aligned(16))) uint8_t q_lds[];
-  __shared__ int s_row[kQBM];
-  __shared__ int s_route[kQBM];
+  __shared__ int s_row[2][kQBM];    // per tile parity: activation row of each route column (-1: padding)
+  __shared__ int s_route[2][kQBM];  // per tile parity: route of each column (-1: padding)
+  __shared__ float s_amax[GATE_UP ? 4 * kQBM : 1];  // gate_up epilogue: [row group][column] amax
 
-  bool shared;
-  int expert, mblock, ntile;
-  if (!map_tile_q(a, blockIdx.x, shared, expert, mblock, ntile)) return;
+  int v = blockIdx.x;
+  QTile cur;
+  if (!map_tile_q(a, v, cur)) return;
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int rg = wave >> 1, ch = wave & 1;
   const int r16 = lane & 15, g = lane >> 4;
-
-  if (tid < kQBM) {
-    int row = -1, route = -1;
-    if (shared) {
-      const int t = mblock * kQBM + tid;
-      if (t < a.M) {
-        route = t;
-        row = a.x_token_rows ? t : a.numel + t;
-      }
-    } else {
-      const int rr = a.sorted[mblock * kQBM + tid];
-      if (rr < a.numel) {
-        route = rr;
-        row = a.x_token_rows ? rr / a.k : rr;
-      }
-    }
-    s_row[tid] = row;
-    s_route[tid] = route;
-  }
-  __syncthreads();
-
-  const BankView bank = shared ? a.ws : a.w;
   const int K = a.K, nkb = K / 128;
-  const size_t rb = FMT == FMT_FP8 ? static_cast<size_t>(K) : static_cast<size_t>(K) / 2;
-  const uint8_t* wexp = bank.w + static_cast<size_t>(expert) * a.N * rb;
-  const int n0 = GATE_UP ? ntile * (kQRows / 2) : ntile * kQRows;
-  // first weight row of tile j of row group q
-  auto trow_of = [&](int q, int j) -> int {
-    if (GATE_UP) return (j < 2 ? 0 : a.inter) + n0 + 32 * q + 16 * (j & 1);
-    return n0 + 64 * q + 16 * j;
+  const uint32_t rb = FMT == FMT_FP8 ? static_cast<uint32_t>(K) : static_cast<uint32_t>(K) / 2;
+
+  // column tid of tile t from its align entry `raw` (routed tiles)
+  auto put_rows = [&](const QTile& t, int raw, int b) {
+    const int tid = wave * kWave + fresh_lane();
+    int row = -1, route = -1;
+    if (t.shared) {
+      const int tk = t.mblock * kQBM + tid;
+      if (tk < a.M) {
+        route = tk;
+        row = a.x_token_rows ? tk : a.numel + tk;
+      }
+    } else if (raw < a.numel) {
+      route = raw;
+      row = a.x_token_rows ? raw / a.k : raw;
+    }
+    s_row[b][tid] = row;
+    s_route[b][tid] = route;
+  };
+  auto raw_of = [&](const QTile& t) -> int { return t.shared ? 0 : a.sorted[t.mblock * kQBM + tid]; };
+  auto n0_of = [&](const QTile& t) -> int { return GATE_UP ? t.ntile * (kQRows / 2) : t.ntile * kQRows; };
+  // first weight row of tile j of row group q, relative to the tile's first row n0
+  auto trow_rel = [&](int q, int j) -> int {
+    if (GATE_UP) return (j < 2 ? 0 : a.inter) + 32 * q + 16 * (j & 1);
+    return 64 * q + 16 * j;
   };
 
-  // ---- per-lane sources of the copies (K step 0; step kb adds kb * step bytes)
+  // ---- sources of the copies: buffer descriptors + 32-bit lane offsets of K
+  // step 0 (step kb adds kb * step bytes as the scalar offset).  Weight rows,
+  // weight scales and activation rows past their range (the last down tile's
+  // rows past N, padding route columns) read zeros without memory traffic.
+  const int xrows = a.x_token_rows ? a.M : a.numel + a.M;
+  const __amdgpu_buffer_rsrc_t rsrc_x = make_rsrc(a.xq, static_cast<uint32_t>(xrows) * K);
+  __amdgpu_buffer_rsrc_t rsrc_w;
+  __amdgpu_buffer_rsrc_t rsrc_s = make_rsrc(a.xs, static_cast<uint32_t>(xrows) * nkb * 4);
   // weights: copy c of wave w fills LDS rows of 1 KB block i = w*kACopies + c
-  const uint8_t* asrc[L::kACopies];
+  uint32_t avoff[L::kACopies];
 #pragma unroll
   for (int c = 0; c < L::kACopies; ++c) {
     const int i = wave * L::kACopies + c;
@@ -673,58 +700,63 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
       R = 16 * i + (lane >> 2);
       q = (lane & 3) ^ swz64(R);
     }
-    const int row = min(trow_of(R >> 6, (R >> 4) & 3) + (R & 15), a.N - 1);
-    asrc[c] = wexp + static_cast<size_t>(row) * rb + q * 16;
+    avoff[c] = static_cast<uint32_t>(trow_rel(R >> 6, (R >> 4) & 3) + (R & 15)) * rb + q * 16;
   }
-  // scales: waves 0-3 copy their row group's weight scales, waves 4-7 64
-  // activation-scale columns each
-  const uint8_t* ssrc;
+  // scales: waves 0-3 copy their row group's weight scales (offsets fixed
+  // relative to the tile), waves 4-7 64 activation-scale columns each
+  uint32_t svoff = 0;
+  if (wave < 4) {
+    if constexpr (FMT == FMT_FP8) svoff = static_cast<uint32_t>(trow_rel(wave, lane & 3) / 128) * nkb * 4;
+    else svoff = static_cast<uint32_t>(trow_rel(wave, lane >> 4) + (lane & 15)) * (K / 32);
+  }
   uint8_t* const sdst_base = q_lds + (wave < 4 ? (FMT == FMT_FP8 ? L::kOffAS + wave * 16 : L::kOffAS + wave * 256)
                                                : L::kOffBS + (wave - 4) * 256);
-  if (wave < 4) {
-    if constexpr (FMT == FMT_FP8) {
-      const int j = lane & 3;
-      ssrc = static_cast<const uint8_t*>(bank.s) +
-             ((static_cast<size_t>(expert) * (a.N / 128) + min(trow_of(wave, j), a.N - 1) / 128) * nkb) * 4;
-    } else {
-      const int row = min(trow_of(wave, lane >> 4) + (lane & 15), a.N - 1);
-      ssrc = static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(expert) * a.N + row) * (K / 32);
-    }
-  } else {
-    const int col = 64 * (wave - 4) + lane;
-    ssrc = static_cast<const uint8_t*>(a.xs) + static_cast<size_t>(s_row[col] < 0 ? 0 : s_row[col]) * nkb * 4;
-  }
   const bool scopy = wave >= 4 || FMT != FMT_FP8 || lane < 4;
   // activations: copy c of wave w fills LDS columns of 1 KB block i = w*kBCopies + c
-  const uint8_t* bsrc[L::kBCopies];
+  uint32_t xvoff[L::kBCopies];
+  auto setup = [&](const QTile& t, int b) {
+    const BankView bank = t.shared ? a.ws : a.w;
+    const int n0 = n0_of(t);
+    rsrc_w = make_rsrc(bank.w + (static_cast<size_t>(t.expert) * a.N + n0) * rb, static_cast<uint32_t>(a.N - n0) * rb);
+    if (wave < 4) {
+      if constexpr (FMT == FMT_FP8)
+        rsrc_s = make_rsrc(static_cast<const uint8_t*>(bank.s) +
+                               (static_cast<size_t>(t.expert) * (a.N / 128) + n0 / 128) * nkb * 4,
+                           static_cast<uint32_t>((a.N - n0) / 128) * nkb * 4);
+      else
+        rsrc_s = make_rsrc(static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(t.expert) * a.N + n0) * (K / 32),
+                           static_cast<uint32_t>(a.N - n0) * (K / 32));
+    }
+    const int ln = fresh_lane();
+    if (wave >= 4) {
+      const int row = s_row[b][64 * (wave - 4) + ln];
+      svoff = row < 0 ? kOutOfRange : static_cast<uint32_t>(row) * nkb * 4;
+    }
 #pragma unroll
-  for (int c = 0; c < L::kBCopies; ++c) {
-    const int col = 8 * (wave * L::kBCopies + c) + (lane >> 3);
-    const int q = (lane & 7) ^ swz_b<FMT>(col);
-    const int row = s_row[col] < 0 ? 0 : s_row[col];  // padding columns compute on row 0, never stored
-    bsrc[c] = a.xq + static_cast<size_t>(row) * K + q * 16;
-  }
+    for (int c = 0; c < L::kBCopies; ++c) {
+      const int col = 8 * (wave * L::kBCopies + c) + (ln >> 3);
+      const int q = (ln & 7) ^ swz_b<FMT>(col);
+      const int row = s_row[b][col];
+      xvoff[c] = row < 0 ? kOutOfRange : static_cast<uint32_t>(row) * K + q * 16;
+    }
+  };
 
-  auto issue = [&](int kb) {
-    uint8_t* st = q_lds + (kb % L::kStages) * L::kStage;
-    const size_t ka = static_cast<size_t>(kb) * L::kALine;
+  auto issue = [&](int kb, int stg) {
+    uint8_t* st = q_lds + stg * L::kStage;
 #pragma unroll
-    for (int c = 0; c < L::kACopies; ++c) lds_copy16(asrc[c] + ka, st + (wave * L::kACopies + c) * 1024);
+    for (int c = 0; c < L::kACopies; ++c)
+      lds_buf16(rsrc_w, st + (wave * L::kACopies + c) * 1024, avoff[c], static_cast<uint32_t>(kb) * L::kALine);
 #pragma unroll
     for (int c = 0; c < L::kBCopies; ++c)
-      lds_copy16(bsrc[c] + static_cast<size_t>(kb) * 128, st + L::kOffB + (wave * L::kBCopies + c) * 1024);
-    if (scopy) lds_copy4(ssrc + kb * 4, sdst_base + (kb % L::kStages) * L::kStage);
+      lds_buf16(rsrc_x, st + L::kOffB + (wave * L::kBCopies + c) * 1024, xvoff[c], static_cast<uint32_t>(kb) * 128);
+    if (scopy) lds_buf4(rsrc_s, sdst_base + stg * L::kStage, svoff, static_cast<uint32_t>(kb) * 4);
   };
 
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   f32x4 acc[4][8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[j][i] = zero;
 
-  auto compute = [&](int kb) {
-    const uint8_t* st = q_lds + (kb % L::kStages) * L::kStage;
+  auto compute = [&](int stg) {
+    const uint8_t* st = q_lds + stg * L::kStage;
     i32x8 wf[4];
     int wcode[4];
     float sw[4];
@@ -738,8 +770,8 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
         wf[j] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
         sw[j] = *reinterpret_cast<const float*>(st + L::kOffAS + rg * 16 + j * 4);
       } else {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(st + R * 64 + ((g ^ swz64(R)) * 16));
-        wf[j] = i32x8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
+        const u32x4 v4 = *reinterpret_cast<const u32x4*>(st + R * 64 + ((g ^ swz64(R)) * 16));
+        wf[j] = i32x8{(int)v4[0], (int)v4[1], (int)v4[2], (int)v4[3], 0, 0, 0, 0};
         wcode[j] = st[L::kOffAS + R * 4 + g];
       }
     }
@@ -791,107 +823,166 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
     if constexpr (FMT == FMT_FP8) acc[3][7] += tp * fp;
   };
 
-  // K pipeline over a ring of kStages LDS stages: copies run D steps ahead
-#pragma unroll
-  for (int d = 0; d < D; ++d)
-    if (d < nkb) issue(d);
-  if (D == 2 && nkb > 1) wait_vm<L::kDmaPerStep>();
-  else wait_vm<0>();
-  bare_barrier();
-  for (int kb = 0; kb < nkb; ++kb) {
-    if (kb + D < nkb) issue(kb + D);
-    compute(kb);
-    // step kb+1's copies must have landed (later ones may still fly); every
-    // LDS read of this step has returned before its MFMA used it
-    if (D == 2 && kb + 2 < nkb) wait_vm<L::kDmaPerStep>();
-    else wait_vm<0>();
-    wait_lgkm0();
-    bare_barrier();
-  }
-
   // ---- epilogue: lane holds rows trow + g*4 + v of route column 128ch + 16i + r16
-  if constexpr (GATE_UP) {
-    // SwiGLU, then the down GEMM's activation quantisation of this 128-feature
-    // group (one K group of the down GEMM) per route: amax over the 32 features
-    // of the wave (lanes g = 0..3 of a column) and over the 4 row groups (LDS).
-    constexpr int QMODE = FMT == FMT_FP8 ? 0 : 2;
-    uint32_t pk[8][2][2];  // bf16 pairs (v0,v1), (v2,v3) of each column tile and gate/up tile pair
-    float amax[8];
+  auto epilogue = [&](const QTile& t, int b) {
+    const int n0 = n0_of(t);
+    if constexpr (GATE_UP) {
+      // SwiGLU, then the down GEMM's activation quantisation of this 128-feature
+      // group (one K group of the down GEMM) per route: amax over the 32 features
+      // of the wave (lanes g = 0..3 of a column) and over the 4 row groups (LDS).
+      constexpr int QMODE = FMT == FMT_FP8 ? 0 : 2;
+      uint32_t pk[8][2][2];  // bf16 pairs (v0,v1), (v2,v3) of each column tile and gate/up tile pair
+      float amax[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float m = 0.f;
+      for (int i = 0; i < 8; ++i) {
+        float m = 0.f;
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        uint16_t o[4];
+        for (int s2 = 0; s2 < 2; ++s2) {
+          uint16_t o[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float gg = bf16_round(acc[s2][i][v]);
-          const float uu = bf16_round(acc[2 + s2][i][v]);
-          o[v] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
-          m = fmaxf(m, fabsf(bf16_to_f32(o[v])));
+          for (int v4 = 0; v4 < 4; ++v4) {
+            const float gg = bf16_round(acc[s2][i][v4]);
+            const float uu = bf16_round(acc[2 + s2][i][v4]);
+            o[v4] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
+            m = fmaxf(m, fabsf(bf16_to_f32(o[v4])));
+          }
+          pk[i][s2][0] = o[0] | (static_cast<uint32_t>(o[1]) << 16);
+          pk[i][s2][1] = o[2] | (static_cast<uint32_t>(o[3]) << 16);
         }
-        pk[i][s2][0] = o[0] | (static_cast<uint32_t>(o[1]) << 16);
-        pk[i][s2][1] = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        amax[i] = m;
       }
-      m = fmaxf(m, __shfl_xor(m, 16));
-      m = fmaxf(m, __shfl_xor(m, 32));
-      amax[i] = m;
-    }
-    float* s_amax = reinterpret_cast<float*>(q_lds);  // [4 row groups][kQBM columns]; the K ring is idle now
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (g == 0) s_amax[rg * kQBM + 128 * ch + 16 * i + r16] = amax[i];
-    __syncthreads();
-    const int ng = a.inter / 128;
+      for (int i = 0; i < 8; ++i)
+        if (g == 0) s_amax[rg * kQBM + 128 * ch + 16 * i + r16] = amax[i];
+      // publish the amax (LDS only: the next tile's copies stay in flight)
+      wait_lgkm0();
+      bare_barrier();
+      const int ng = a.inter / 128;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int col = 128 * ch + 16 * i + r16;
-      const int route = s_route[col];
-      if (route < 0) continue;
-      const float m = fmaxf(fmaxf(s_amax[col], s_amax[kQBM + col]), fmaxf(s_amax[2 * kQBM + col], s_amax[3 * kQBM + col]));
-      float mul;
-      const float sc = group_scale<QMODE>(m, mul);
-      const int arow = shared ? a.numel + route : route;
+      for (int i = 0; i < 8; ++i) {
+        const int col = 128 * ch + 16 * i + r16;
+        const int route = s_route[b][col];
+        if (route < 0) continue;
+        const float m =
+            fmaxf(fmaxf(s_amax[col], s_amax[kQBM + col]), fmaxf(s_amax[2 * kQBM + col], s_amax[3 * kQBM + col]));
+        float mul;
+        const float sc = group_scale<QMODE>(m, mul);
+        const int arow = t.shared ? a.numel + route : route;
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        float vals[4];
+        for (int s2 = 0; s2 < 2; ++s2) {
+          float vals[4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          vals[2 * h] = quant_value<QMODE>(bf16_to_f32(static_cast<uint16_t>(pk[i][s2][h] & 0xffffu)), sc, mul);
-          vals[2 * h + 1] = quant_value<QMODE>(bf16_to_f32(static_cast<uint16_t>(pk[i][s2][h] >> 16)), sc, mul);
+          for (int h = 0; h < 2; ++h) {
+            vals[2 * h] = quant_value<QMODE>(bf16_to_f32(static_cast<uint16_t>(pk[i][s2][h] & 0xffffu)), sc, mul);
+            vals[2 * h + 1] = quant_value<QMODE>(bf16_to_f32(static_cast<uint16_t>(pk[i][s2][h] >> 16)), sc, mul);
+          }
+          uint32_t q4 = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(vals[0], vals[1], 0, false));
+          q4 = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(vals[2], vals[3], static_cast<int>(q4), true));
+          const int n = n0 + 32 * rg + 16 * s2 + g * 4;
+          *reinterpret_cast<uint32_t*>(a.act_q + static_cast<size_t>(arow) * a.inter + n) = q4;
         }
-        uint32_t q4 = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(vals[0], vals[1], 0, false));
-        q4 = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(vals[2], vals[3], static_cast<int>(q4), true));
-        const int n = n0 + 32 * rg + 16 * s2 + g * 4;
-        *reinterpret_cast<uint32_t*>(a.act_q + static_cast<size_t>(arow) * a.inter + n) = q4;
+        if (rg == 0 && g == 0) {
+          const size_t at = static_cast<size_t>(arow) * ng + t.ntile;
+          if (QMODE == 0) static_cast<float*>(a.act_s)[at] = sc;
+          else static_cast<uint32_t*>(a.act_s)[at] = static_cast<uint32_t>(sc);
+        }
       }
-      if (rg == 0 && g == 0) {
-        const size_t at = static_cast<size_t>(arow) * ng + ntile;
-        if (QMODE == 0) static_cast<float*>(a.act_s)[at] = sc;
-        else static_cast<uint32_t*>(a.act_s)[at] = static_cast<uint32_t>(sc);
-      }
-    }
-  } else {
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int col = 128 * ch + 16 * i + r16;
-      const int route = s_route[col];
-      if (route < 0) continue;
-      const float wt = shared ? 1.0f : a.topk_w[route];
-      uint16_t* dst = shared ? a.sh_out + static_cast<size_t>(route) * a.N : a.out + static_cast<size_t>(route) * a.N;
+      for (int i = 0; i < 8; ++i) {
+        const int col = 128 * ch + 16 * i + r16;
+        const int route = s_route[b][col];
+        if (route < 0) continue;
+        const float wt = t.shared ? 1.0f : a.topk_w[route];
+        uint16_t* dst = t.shared ? a.sh_out + static_cast<size_t>(route) * a.N : a.out + static_cast<size_t>(route) * a.N;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = trow_of(rg, j) + g * 4;
-        if (n >= a.N) continue;
-        uint16_t o[4];
+        for (int j = 0; j < 4; ++j) {
+          const int n = n0 + trow_rel(rg, j) + g * 4;
+          if (n >= a.N) continue;
+          uint16_t o[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(acc[j][i][v] * wt);
-        uint2 pk2;
-        pk2.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
-        pk2.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
-        *reinterpret_cast<uint2*>(dst + n) = pk2;
+          for (int v4 = 0; v4 < 4; ++v4) o[v4] = f32_to_bf16(acc[j][i][v4] * wt);
+          uint2 pk2;
+          pk2.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
+          pk2.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+          *reinterpret_cast<uint2*>(dst + n) = pk2;
+        }
       }
     }
+  };
+
+  // ---- persistent loop over this workgroup's tiles (v, v + grid, ...).  The
+  // K pipeline runs over a ring of S LDS stages with copies D steps ahead; the
+  // ring continues across tiles (global step g0 + kb), so the last D steps of a
+  // tile issue the next tile's first D steps, which land while this tile's
+  // epilogue runs.  The next tile's align entries are loaded at the start of
+  // a tile and published before its last D steps.
+  if (tid < kQBM) put_rows(cur, raw_of(cur), 0);
+  __syncthreads();
+  setup(cur, 0);
+  int buf = 0, g0 = 0;
+  bool ahead = false;  // this tile's first D steps were issued during the previous tile
+  for (;;) {
+    if (!ahead) {
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+        if (d < nkb) issue(d, (g0 + d) % S);
+    }
+    QTile nxt;
+    const bool has_next = map_tile_q(a, v + static_cast<int>(gridDim.x), nxt);
+    const bool cross = has_next && nkb > D;  // the next tile's first steps ride in this tile's last D steps
+    // (pinned: a known-zero accumulator would let the compiler schedule the
+    // first step, which it peels, apart from the others, at a register cost)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        acc[j][i] = zero;
+        pin(acc[j][i]);
+      }
+    wait_vm<0>();
+    bare_barrier();
+    const int raw = has_next && tid < kQBM ? raw_of(nxt) : 0;
+    // steady steps: step kb + D of this tile is issued; step kb + 1 must have
+    // landed at the end (later ones may still fly); every LDS read of the step
+    // has returned before its MFMA used it
+    int kb = 0;
+    for (; kb < nkb - D; ++kb) {
+      issue(kb + D, (g0 + kb + D) % S);
+      compute((g0 + kb) % S);
+      if (D == 2 && (kb + 2 < nkb || cross)) wait_vm<L::kDmaPerStep>();
+      else wait_vm<0>();
+      wait_lgkm0();
+      bare_barrier();
+    }
+    // publish the next tile's rows; its first steps ride in this tile's last
+    // D steps
+    if (has_next) {
+      if (tid < kQBM) put_rows(nxt, raw, buf ^ 1);
+      wait_lgkm0();
+      bare_barrier();
+      if (cross) setup(nxt, buf ^ 1);
+    }
+    for (; kb < nkb; ++kb) {
+      if (cross) issue(kb + D - nkb, (g0 + kb + D) % S);
+      compute((g0 + kb) % S);
+      if (kb + 1 < nkb) {
+        if (D == 2 && cross) wait_vm<L::kDmaPerStep>();
+        else wait_vm<0>();
+      }
+      wait_lgkm0();
+      bare_barrier();
+    }
+    epilogue(cur, buf);
+    if (!has_next) break;
+    ahead = cross;
+    cur = nxt;
+    buf ^= 1;
+    g0 += nkb;
+    v += static_cast<int>(gridDim.x);
+    if (!ahead) setup(cur, buf);
   }
 }
 
@@ -921,6 +1012,19 @@ static hipError_t launch_gemm_t(const PrefillGemmArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// CUs of the current device, rounded down to a multiple of the XCD count
+static int q_cu_count() {
+  static int cached = 0;
+  if (cached == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                  hipSuccess || n < kXcds)
+      n = 256;
+    cached = n / kXcds * kXcds;
+  }
+  return cached;
+}
+
 template <int FMT, int GU>
 static hipError_t launch_qgemm_t(PrefillGemmArgs a, hipStream_t stream) {
   static bool attr = false;
@@ -931,7 +1035,12 @@ static hipError_t launch_qgemm_t(PrefillGemmArgs a, hipStream_t stream) {
     attr = true;
   }
   a.ntiles = GU ? a.inter / (kQRows / 2) : (a.N + kQRows - 1) / kQRows;
-  const int wgs = (a.max_blocks + a.shared_blocks) * a.ntiles;
+  // persistent: one workgroup per CU (the LDS ring admits one), each walking
+  // tiles b, b + grid, ...; the grid is a multiple of the XCD count, so a
+  // workgroup's tiles all map to its own XCD's range
+  const long long tiles = static_cast<long long>(a.max_blocks + a.shared_blocks) * a.ntiles;
+  const int wgs = static_cast<int>(std::min<long long>(tiles, q_cu_count()));
+  if (wgs <= 0) return hipSuccess;
   hipLaunchKernelGGL((prefill_qgemm_kernel<FMT, GU>), dim3(wgs), dim3(kQThreads), QLds<FMT>::kTotal, stream, a);
   return hipGetLastError();
 }
