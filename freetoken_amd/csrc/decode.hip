@@ -856,9 +856,11 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, const BankVi
 
 constexpr int kRedFloats4 = kDecWaves * 8 * kWave;  // NMAT * chunks_per_pass <= 8
 
-// Grid: x = row blocks of (4/KS) * RT * 16 rows, y = routed segments
-// (max_seg, the tail beyond n_seg exits) followed by the shared expert's token
-// pieces of seg_cap tokens.
+// Grid: x = row blocks of (4/KS) * RT * 16 rows, y = the shared expert's token
+// pieces of seg_cap tokens, then the routed segments (max_seg, the tail beyond
+// n_seg exits).  The shared pieces come first: their workgroups can be several
+// times heavier than the routed ones (a bf16 shared expert beside MXFP4 routed
+// experts reads 4x the bytes per row) and would otherwise start last and trail.
 template <int FMT_R, int FMT_S, int STAGE, int RT, int KS>
 __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) decode_stage_kernel(DecodeArgs a) {
   constexpr int kNmat = STAGE == 0 ? 2 * RT : RT;
@@ -873,14 +875,16 @@ __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves
   constexpr int kRed = KS > 1 ? kRedFloats4 * 16 : 0;
   constexpr int kSmem = kRing + kAct > kRed ? kRing + kAct : kRed > 16 ? kRed : 16;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kSmem];
-  const int seg = blockIdx.y;
+  const int n_sh = static_cast<int>(gridDim.y) - a.max_seg;  // shared pieces (0 without a shared expert)
+  int seg = blockIdx.y;
   SegView sv;
-  sv.shared = seg >= a.max_seg;
+  sv.shared = seg < n_sh;
   if (sv.shared) {
     sv.expert = 0;
-    sv.start = (seg - a.max_seg) * a.seg_cap;
+    sv.start = seg * a.seg_cap;
     sv.count = min(a.seg_cap, a.M - sv.start);
   } else {
+    seg -= n_sh;
     if (seg >= a.n_seg[0]) return;
     sv.expert = a.seg_expert[seg];
     sv.start = a.seg_start[seg];
