@@ -41,6 +41,17 @@ class FtmoeBank(ctypes.Structure):
 
 _bp = ctypes.POINTER(FtmoeBank)
 
+
+class FtmoeFetchBank(ctypes.Structure):
+    _fields_ = [
+        ("host_rows", ctypes.c_void_p),
+        ("slot_bank", ctypes.c_void_p),
+        ("row_bytes", ctypes.c_size_t),
+    ]
+
+
+_fbp = ctypes.POINTER(FtmoeFetchBank)
+
 SIGNATURES = {
     "ftmoe_last_error": (ctypes.c_char_p, []),
     "ftmoe_version": (_i, []),
@@ -49,6 +60,8 @@ SIGNATURES = {
     "ftmoe_align_sizes": (None, [_i, _i, _i, _ip, _ip]),
     "ftmoe_align": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "ftmoe_slot_map": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp, _vp]),
+    "ftmoe_lru_ensure": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
+    "ftmoe_fetch_experts": (_i, [_fbp, _i, _vp, _vp, _vp, _i, _vp]),
     "ftmoe_act_quant_fp8": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "ftmoe_experts_decode_workspace": (_sz, [_i, _i, _bp, _bp]),
     "ftmoe_experts_decode": (_i, [_vp, _i, _i, _vp, _vp, _bp, _bp, _i, _i, _vp, _vp, _sz, _vp]),

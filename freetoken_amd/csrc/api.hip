@@ -258,6 +258,80 @@ int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_i
                    "slot_map launch");
 }
 
+int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layers, int num_experts,
+                     int32_t* slot_for_id, int32_t* id_of_slot, int64_t* usage, int64_t* step, int cache_size,
+                     int64_t* recency, int max_fetch, int32_t* evict_slots, int32_t* src_indices, int capacity,
+                     int32_t* num_indices, int32_t* num_missing, int64_t* stats, ftmoe_stream_t stream) {
+  if ((!expert_ids && numel) || !slot_for_id || !id_of_slot || !usage || !step || !num_indices || !num_missing ||
+      ((!evict_slots || !src_indices) && capacity))
+    return fail(FTMOE_ERR_INVALID, "lru_ensure: NULL pointer");
+  if (numel < 0 || num_experts <= 0 || num_experts > 8192 || cache_size <= 0 || cache_size > 8192 ||
+      num_layers <= 0 || layer_id < 0 || layer_id >= num_layers || capacity < 0)
+    return fail(FTMOE_ERR_UNSUPPORTED, "lru_ensure: numel=%d E=%d S=%d layer=%d/%d capacity=%d", numel, num_experts,
+                cache_size, layer_id, num_layers, capacity);
+  ftmoe::LruArgs a{};
+  a.ids = expert_ids;
+  a.numel = numel;
+  a.layer = layer_id;
+  a.num_layers = num_layers;
+  a.num_experts = num_experts;
+  a.cache_size = cache_size;
+  a.slot_for_id = slot_for_id;
+  a.id_of_slot = id_of_slot;
+  a.usage = usage;
+  a.step = step;
+  a.recency = recency;
+  a.sort_len = 0;
+  if (recency) {
+    const int most = std::max(1, std::min(numel, num_experts));
+    a.sort_len = 1;
+    while (a.sort_len < most) a.sort_len <<= 1;
+  }
+  a.max_fetch = max_fetch;
+  a.capacity = capacity;
+  a.evict_slots = evict_slots;
+  a.src_indices = src_indices;
+  a.num_indices = num_indices;
+  a.num_missing = num_missing;
+  a.stats = reinterpret_cast<long long*>(stats);
+  if (ftmoe::lru_lds_bytes(num_experts, cache_size, a.sort_len) > 160 * 1024 - 4096)
+    return fail(FTMOE_ERR_UNSUPPORTED, "lru_ensure: E=%d S=%d exceed the LDS of one workgroup", num_experts,
+                cache_size);
+  return check_hip(ftmoe::launch_lru_ensure(a, stream), "lru_ensure launch");
+}
+
+int ftmoe_fetch_experts(const ftmoe_fetch_bank* banks, int nbanks, const int32_t* evict_slots,
+                        const int32_t* src_indices, const int32_t* num_indices, int max_entries,
+                        ftmoe_stream_t stream) {
+  if (!banks || !num_indices || ((!evict_slots || !src_indices) && max_entries))
+    return fail(FTMOE_ERR_INVALID, "fetch_experts: NULL pointer");
+  if (nbanks <= 0 || nbanks > ftmoe::kMaxFetchBanks || max_entries < 0)
+    return fail(FTMOE_ERR_UNSUPPORTED, "fetch_experts: nbanks=%d max_entries=%d", nbanks, max_entries);
+  ftmoe::FetchArgs a{};
+  int chunks = 0;
+  for (int b = 0; b < nbanks; ++b) {
+    const ftmoe_fetch_bank& k = banks[b];
+    if (!k.host_rows || !k.slot_bank) return fail(FTMOE_ERR_INVALID, "fetch_experts: bank %d NULL", b);
+    if (k.row_bytes == 0 || k.row_bytes % 16 || reinterpret_cast<uintptr_t>(k.host_rows) % 16 ||
+        reinterpret_cast<uintptr_t>(k.slot_bank) % 16)
+      return fail(FTMOE_ERR_UNSUPPORTED, "fetch_experts: bank %d rows must be 16-byte multiples at 16-byte addresses",
+                  b);
+    a.src[b] = static_cast<const uint8_t*>(k.host_rows);
+    a.dst[b] = static_cast<uint8_t*>(k.slot_bank);
+    a.row_bytes[b] = k.row_bytes;
+    a.chunk_start[b] = chunks;
+    chunks += ftmoe::fetch_chunks(k.row_bytes);
+  }
+  a.chunks_per_entry = chunks;
+  a.nbanks = nbanks;
+  a.evict_slots = evict_slots;
+  a.src_indices = src_indices;
+  a.num_indices = num_indices;
+  a.max_entries = max_entries;
+  if (max_entries == 0) return FTMOE_OK;
+  return check_hip(ftmoe::launch_fetch_experts(a, max_entries, stream), "fetch_experts launch");
+}
+
 int ftmoe_act_quant_fp8(const void* x, int rows, int K, int mode, void* q, void* scales, ftmoe_stream_t stream) {
   if ((!x || !q || !scales) && rows) return fail(FTMOE_ERR_INVALID, "act_quant_fp8: NULL pointer");
   if (rows < 0 || K <= 0 || K % 128 || (mode != 0 && mode != 1))

@@ -114,6 +114,45 @@ inline int prefill_block_size(int fmt) { return fmt == FMT_BF16 ? 128 : 256; }
 hipError_t launch_act_quant(int mode, const uint16_t* x, int rows, int K, uint8_t* q, void* scales,
                             hipStream_t stream);
 hipError_t launch_prefill_gemm(int fmt, int gate_up, const PrefillGemmArgs& a, hipStream_t stream);
+
+// Expert-cache admission (cache.hip): one call's ids -> slots with LRU
+// admission of the missing experts.
+struct LruArgs {
+  int32_t* ids;           // [numel] expert ids in, slot ids out (-1: unfetched miss or id outside [0, E))
+  int numel;
+  int layer, num_layers, num_experts, cache_size;
+  int32_t* slot_for_id;   // [num_layers * num_experts]
+  int32_t* id_of_slot;    // [cache_size] flat id layer * E + expert, -1 empty
+  int64_t* usage;         // [cache_size] step of last use
+  int64_t* step;          // [1]
+  int64_t* recency;       // nullable [num_experts] of this layer: order misses by recency
+  int sort_len;           // power of two >= the largest miss count (recency order), else 0
+  int max_fetch;          // < 0: every miss
+  int capacity;           // entries of evict_slots / src_indices
+  int32_t* evict_slots;   // [capacity]
+  int32_t* src_indices;   // [capacity] layer-local expert rows
+  int32_t* num_indices;   // [1] entries admitted
+  int32_t* num_missing;   // [1] distinct missing experts before the cap
+  long long* stats;       // nullable [4] accumulated: active, missing, calls, missed routes
+};
+hipError_t launch_lru_ensure(const LruArgs& a, hipStream_t stream);
+size_t lru_lds_bytes(int num_experts, int cache_size, int sort_len);
+
+constexpr int kMaxFetchBanks = 8;
+struct FetchArgs {
+  const uint8_t* src[kMaxFetchBanks];   // this layer's host rows (pinned, device-mapped), per bank
+  uint8_t* dst[kMaxFetchBanks];         // slot banks
+  uint64_t row_bytes[kMaxFetchBanks];   // bytes of one expert in each bank (multiple of 16)
+  int chunk_start[kMaxFetchBanks];      // first 64 KiB chunk of each bank within an entry
+  int chunks_per_entry;
+  int nbanks;
+  int max_entries;                      // bound on *num_indices (the size of the two lists)
+  const int32_t* evict_slots;
+  const int32_t* src_indices;
+  const int32_t* num_indices;
+};
+hipError_t launch_fetch_experts(const FetchArgs& a, int max_entries, hipStream_t stream);
+int fetch_chunks(uint64_t row_bytes);
 hipError_t launch_combine(const uint16_t* ic3, const int32_t* ids, int num_rows, const uint16_t* sh_out, int M,
                           int k, int H, uint16_t* y, hipStream_t stream);
 

@@ -180,7 +180,15 @@ class OffloadMoELayer(MoELayer):
     def _decode_routed(self, hidden_states, topk_weights, topk_ids) -> torch.Tensor:
         cache = self.offload_cache
         assert cache is not None
-        # ensure_experts (expert ids -> slot ids, in place) fused into the decode call
+        if cache.sources:
+            # on-demand load (layers/moe.py:288-320): admit the missing experts,
+            # gather them over PCIe, then compute on the slots
+            cache.ensure_experts(self.layer_id, topk_ids)
+            cache.copy_missing()
+            return ops.experts_decode(hidden_states, topk_weights, topk_ids, self._views_bank(cache.bank_views()),
+                                      shared=self.shared_expert, activation=self.activation)
+        # ensure_experts without admission (expert ids -> slot ids, in place)
+        # fused into the decode call; misses are skipped and counted
         table, stats = cache.slot_lookup(self.layer_id)
         return ops.experts_decode(hidden_states, topk_weights, topk_ids, self._views_bank(cache.bank_views()),
                                   shared=self.shared_expert, activation=self.activation, slot_for_id=table,

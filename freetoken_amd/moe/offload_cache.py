@@ -5,10 +5,14 @@
 ``id_of_slot`` [S] holds the flat id ``layer * E + expert`` of each slot
 (``:155-175``).  The slot banks are one ``[S, ...]`` tensor per bank
 (``bank_views``, ``:555-561``).  ``ensure_experts`` rewrites routed expert
-ids to slot ids in place (``:800-810``); experts that are not resident are
-reported as misses (slot -1, skipped by the expert kernels) instead of being
-fetched -- the PCIe miss path and its LRU admission are not part of this
-build.  Miss statistics accumulate on the device, graph-safe, in the
+ids to slot ids in place (``:800-810``).  With host sources registered
+(``set_bank_sources``, pinned per-layer ``[E, ...]`` tensors, ``:419-470``) it
+also admits the missing experts into least-recently-used slots
+(``lru_ensure``, ``moe/offload_kernels.py:19-40``) and ``copy_missing``
+gathers their rows over PCIe (``:968-1010``); without sources, misses are
+reported (slot -1, skipped by the expert kernels).  ``ensure_experts_hybrid``
+is the capped admission (``offload_kernels.py:43-60``).  Everything runs on
+the device without host synchronisation; miss statistics accumulate in the
 reference's layout (``:205-229,861-934``).
 """
 
@@ -38,6 +42,18 @@ class ExpertSlotCache:
         self.collect_stats = True
         self.lru_stats = torch.zeros((num_layers, N_STATS), dtype=torch.int64, device=self.device)
         self.banks: "OrderedDict[str, torch.Tensor]" = OrderedDict()
+        # admission state (moe/offload_cache.py:155-200)
+        dev = self.device
+        self.usage = torch.zeros((cache_size,), dtype=torch.int64, device=dev)
+        self.step = torch.zeros((1,), dtype=torch.int64, device=dev)
+        self.expert_recency = torch.zeros((num_layers, num_experts), dtype=torch.int64, device=dev)
+        cap = min(num_experts, cache_size)
+        self.evict_slots = torch.zeros((cap,), dtype=torch.int32, device=dev)
+        self.src_indices = torch.zeros((cap,), dtype=torch.int32, device=dev)
+        self.num_indices = torch.zeros((1,), dtype=torch.int32, device=dev)
+        self.num_missing_full = torch.zeros((1,), dtype=torch.int32, device=dev)
+        self.sources: "OrderedDict[str, list[torch.Tensor]]" = OrderedDict()
+        self._pending_src_layer: int | None = None
 
     # -------------------------------------------------------------- setup (host)
     def set_bank_caches(self, **banks: torch.Tensor) -> None:
@@ -46,6 +62,28 @@ class ExpertSlotCache:
         for name, t in banks.items():
             assert t.shape[0] == self.cache_size, (name, t.shape)
             self.banks[name] = t
+
+    def set_bank_sources(self, sources: dict) -> None:
+        """Registers the host copy of every bank: ``name -> [per-layer tensor]``
+        with each tensor ``[num_experts, ...]`` in pinned host memory and the
+        same row shape as the slot bank of that name (``:419-470``)."""
+        assert set(sources) == set(self.banks), (sorted(sources), sorted(self.banks))
+        for name, layers in sources.items():
+            assert len(layers) == self.num_layers, (name, len(layers))
+            for t in layers:
+                assert t.device.type == "cpu" and t.is_pinned() and t.is_contiguous(), name
+                assert t.shape[0] == self.num_experts and t.shape[1:] == self.banks[name].shape[1:], (name, t.shape)
+        self.sources = OrderedDict((name, list(sources[name])) for name in self.banks)
+
+    def reset(self) -> None:
+        """Empties the cache: no expert resident, usage and step cleared."""
+        self.slot_for_id.fill_(-1)
+        self.id_of_slot.fill_(-1)
+        self.usage.zero_()
+        self.step.zero_()
+        self.expert_recency.zero_()
+        self.num_indices.zero_()
+        self._pending_src_layer = None
 
     def assign(self, layer_id: int, experts, slots) -> None:
         """Marks ``experts`` of ``layer_id`` resident in ``slots`` (the caller
@@ -68,10 +106,42 @@ class ExpertSlotCache:
     # -------------------------------------------------------------- hot path
     def ensure_experts(self, layer_id: int, expert_ids: torch.Tensor,
                        miss_mask: torch.Tensor | None = None) -> torch.Tensor:
-        """Rewrites ``expert_ids`` (int32, any shape) to slot ids in place."""
+        """Rewrites ``expert_ids`` (int32, any shape) to slot ids in place.
+        With host sources, the missing experts are first admitted (lowest id
+        first, into the least recently used slots) and staged for
+        ``copy_missing``; without, they map to -1 (``miss_mask`` marks them)."""
         stats = self.lru_stats[layer_id] if self.collect_stats else None
-        ops.slot_map(expert_ids, self.slot_for_id[layer_id], out=expert_ids, miss_mask=miss_mask, stats=stats)
+        if not self.sources:
+            ops.slot_map(expert_ids, self.slot_for_id[layer_id], out=expert_ids, miss_mask=miss_mask, stats=stats)
+            return expert_ids
+        assert miss_mask is None, "every expert is admitted when host sources are registered"
+        return self._admit(layer_id, expert_ids, -1, None, stats)
+
+    def ensure_experts_hybrid(self, layer_id: int, expert_ids: torch.Tensor, max_fetch: int,
+                              by_recency: bool = True) -> torch.Tensor:
+        """Capped admission (``offload_kernels.py:43-60``): at most ``max_fetch``
+        of the missing experts (most recently seen first with ``by_recency``,
+        else lowest id first) are admitted; the others map to -1."""
+        assert self.sources, "set_bank_sources must register the host banks first"
+        stats = self.lru_stats[layer_id] if self.collect_stats else None
+        rec = self.expert_recency[layer_id] if by_recency else None
+        return self._admit(layer_id, expert_ids, max_fetch, rec, stats)
+
+    def _admit(self, layer_id, expert_ids, max_fetch, recency, stats):
+        ops.lru_ensure(expert_ids, layer_id, self.slot_for_id, self.id_of_slot, self.usage, self.step,
+                       self.evict_slots, self.src_indices, self.num_indices, self.num_missing_full,
+                       recency=recency, max_fetch=max_fetch, stats=stats)
+        self._pending_src_layer = layer_id
         return expert_ids
+
+    def copy_missing(self) -> None:
+        """Copies the experts staged by the last admission from their host rows
+        into their slots (``:968-1010``); the count stays on the device."""
+        assert self.sources, "set_bank_sources must register the host banks first"
+        layer_id = self._pending_src_layer
+        assert layer_id is not None, "no staged misses (ensure_experts first)"
+        ops.fetch_experts([layers[layer_id] for layers in self.sources.values()], list(self.banks.values()),
+                          self.evict_slots, self.src_indices, self.num_indices)
 
     def slot_lookup(self, layer_id: int) -> tuple[torch.Tensor, torch.Tensor | None]:
         """(slot table, stats counters or None) of a layer, for decode calls that

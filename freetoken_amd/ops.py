@@ -121,6 +121,65 @@ def slot_map(topk_ids: torch.Tensor, slot_for_id: torch.Tensor, out: torch.Tenso
     return out
 
 
+def lru_ensure(expert_ids: torch.Tensor, layer_id: int, slot_for_id: torch.Tensor, id_of_slot: torch.Tensor,
+               usage: torch.Tensor, step: torch.Tensor, evict_slots: torch.Tensor, src_indices: torch.Tensor,
+               num_indices: torch.Tensor, num_missing: torch.Tensor, recency: torch.Tensor | None = None,
+               max_fetch: int = -1, stats: torch.Tensor | None = None) -> torch.Tensor:
+    """LRU admission of a call's experts into the slot cache; ``expert_ids``
+    (int32) are rewritten to slots in place (see ftmoe_lru_ensure).
+    ``slot_for_id`` [L, E] int32, ``id_of_slot`` [S] int32, ``usage`` [S] and
+    ``step`` [1] int64; ``recency`` (int64 [E] of this layer) selects the
+    most-recent-first miss order."""
+    i32 = (expert_ids, slot_for_id, id_of_slot, evict_slots, src_indices, num_indices, num_missing)
+    if any(t.dtype != torch.int32 for t in i32):
+        raise ValueError("ids, tables, evict/src lists and counts must be int32")
+    if usage.dtype != torch.int64 or step.dtype != torch.int64 or (recency is not None and recency.dtype != torch.int64):
+        raise ValueError("usage, step and recency must be int64")
+    if stats is not None and stats.dtype != torch.int64:
+        raise ValueError("stats must be int64[4]")
+    _require_gpu(*i32, usage, step, recency, stats)
+    if not expert_ids.is_contiguous():
+        raise ValueError("expert_ids must be contiguous")
+    num_layers, num_experts = slot_for_id.shape
+    if recency is not None and recency.numel() != num_experts:
+        raise ValueError("recency must hold one entry per expert of the layer")
+    check(
+        lib().ftmoe_lru_ensure(_ptr(expert_ids), expert_ids.numel(), layer_id, num_layers, num_experts,
+                               _ptr(slot_for_id), _ptr(id_of_slot), _ptr(usage), _ptr(step), id_of_slot.numel(),
+                               _ptr(recency), max_fetch, _ptr(evict_slots), _ptr(src_indices),
+                               min(evict_slots.numel(), src_indices.numel()), _ptr(num_indices), _ptr(num_missing),
+                               _ptr(stats), _stream(expert_ids.device)),
+        "lru_ensure",
+    )
+    return expert_ids
+
+
+def fetch_experts(host_rows, slot_banks, evict_slots: torch.Tensor, src_indices: torch.Tensor,
+                  num_indices: torch.Tensor, max_entries: int | None = None) -> None:
+    """Copies the admitted experts' rows from pinned host tensors (one per
+    bank, ``[E, ...]`` of one layer) into the slot banks (``[S, ...]`` on the
+    device), for the first ``num_indices`` entries (see ftmoe_fetch_experts)."""
+    if len(host_rows) != len(slot_banks) or not host_rows:
+        raise ValueError("one host tensor per slot bank")
+    _require_gpu(evict_slots, src_indices, num_indices, *slot_banks)
+    banks = (_lib.FtmoeFetchBank * len(host_rows))()
+    for b, (h, d) in enumerate(zip(host_rows, slot_banks)):
+        if h.device.type != "cpu" or not h.is_pinned() or not h.is_contiguous():
+            raise ValueError("host rows must be contiguous pinned CPU tensors")
+        if not d.is_contiguous():
+            raise ValueError("slot banks must be contiguous")
+        row = h[0].numel() * h.element_size()
+        if row != d[0].numel() * d.element_size():
+            raise ValueError(f"bank {b}: host row {row} B != slot row {d[0].numel() * d.element_size()} B")
+        banks[b] = _lib.FtmoeFetchBank(h.data_ptr(), d.data_ptr(), row)
+    n = min(evict_slots.numel(), src_indices.numel()) if max_entries is None else max_entries
+    check(
+        lib().ftmoe_fetch_experts(banks, len(host_rows), _ptr(evict_slots), _ptr(src_indices), _ptr(num_indices), n,
+                                  _stream(evict_slots.device)),
+        "fetch_experts",
+    )
+
+
 def act_quant_fp8(x: torch.Tensor, mode: int = 0):
     """Per-token per-128 FP8 quantisation of bf16 rows: mode 0 -> float32 scales
     (amax/448), mode 1 -> uint8 e8m0 power-of-two scale codes."""

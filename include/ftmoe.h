@@ -113,6 +113,50 @@ int ftmoe_align(const int32_t* topk_ids, int numel, int num_experts, int block_s
 int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_id, int num_experts,
                    int32_t* slot_ids, uint8_t* miss_mask, int64_t* stats, ftmoe_stream_t stream);
 
+/* Expert-cache admission (the miss path of OffloadMoeCache.ensure_experts):
+ * replaces lru_ensure / ensure_experts (moe/offload_kernels.py:19-40) and the
+ * capped admission of ensure_experts_hybrid with the "lowest_id" or
+ * "recency" order (offload_kernels.py:43-60), following their CPU mirror
+ * (offload_kernels.py:128-188).  One call:
+ *   step += 1; the distinct ids of expert_ids are seen; resident seen experts
+ *   get usage[slot] = step; missing seen experts are ordered by ascending id,
+ *   or, with recency (nullable, int64 [num_experts] of this layer), by most
+ *   recent first then ascending id; the first min(misses, max_fetch (< 0: no
+ *   cap), capacity) of them take, one after the other, the slot with the
+ *   smallest (usage, slot) -- its previous owner, of any layer, is unmapped
+ *   -- and are listed in evict_slots / src_indices (layer-local rows);
+ *   recency of every seen expert = step; expert_ids are rewritten in place to
+ *   slots (-1 for unfetched misses and ids outside [0, num_experts)).
+ *   slot_for_id int32 [num_layers * num_experts] (row layer_id is this layer),
+ *   id_of_slot int32 [cache_size] (flat ids, -1 empty), usage int64
+ *   [cache_size], step int64 [1]; num_indices / num_missing int32 [1] receive
+ *   the admitted and the missing counts; stats (nullable) int64 [4] is
+ *   accumulated as in ftmoe_slot_map, counted before admission.
+ * num_experts, cache_size <= 8192. */
+int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layers, int num_experts,
+                     int32_t* slot_for_id, int32_t* id_of_slot, int64_t* usage, int64_t* step, int cache_size,
+                     int64_t* recency, int max_fetch, int32_t* evict_slots, int32_t* src_indices, int capacity,
+                     int32_t* num_indices, int32_t* num_missing, int64_t* stats, ftmoe_stream_t stream);
+
+/* One bank of the gather below: this layer's expert rows in pinned host
+ * memory ([num_experts, row_bytes]) and the slot bank ([cache_size,
+ * row_bytes]) on the device. */
+typedef struct ftmoe_fetch_bank {
+  const void* host_rows;
+  void* slot_bank;
+  size_t row_bytes; /* multiple of 16; pointers 16-byte aligned */
+} ftmoe_fetch_bank;
+
+/* Copies, for i < *num_indices (a device value, at most max_entries), row
+ * src_indices[i] of every bank's host rows into row evict_slots[i] of its slot
+ * bank; replaces copy_missing / fast_index_copy_multi (moe/offload_cache.py:
+ * 968-1010, kernel/csrc/jit/fast_index_copy.cuh:486-562).  The host memory is
+ * read in place by the GPU (pinned memory from hipHostMalloc); no host
+ * synchronisation, graph-capturable.  nbanks <= 8. */
+int ftmoe_fetch_experts(const ftmoe_fetch_bank* banks, int nbanks, const int32_t* evict_slots,
+                        const int32_t* src_indices, const int32_t* num_indices, int max_entries,
+                        ftmoe_stream_t stream);
+
 /* Per-token per-128-group FP8 activation quantisation; replaces
  * per_token_group_quant_fp8 (kernel/triton/fp8_block_linear.py:38-82, mode 0:
  * float32 scale amax/448) and the DSV4 act_quant with power-of-two scales

@@ -1,17 +1,30 @@
-"""Expert-cache slot indirection (lookup + miss report, no admission).
+"""Expert-cache slot indirection: lookup + miss report, and LRU admission.
 
 ``OffloadMoeCache.slot_for_id`` is an int32 [L, E] table with -1 for a
 non-resident expert (``moe/offload_cache.py:155-175``); decode rewrites each
 routed expert id to its slot (``ensure_experts``, ``:800-810``; CPU mirror of
-the rewrite at ``moe/offload_kernels.py:185-188``).  This build keeps the
-lookup and reports misses instead of fetching them (fetching is the next
-step of the miss path).  Miss statistics follow the reference's counters
+the rewrite at ``moe/offload_kernels.py:185-188``).  ``slot_map`` is the
+lookup alone (misses reported, not fetched); ``lru_ensure`` adds the
+admission of the misses.  Miss statistics follow the reference's counters
 (``moe/offload_cache.py:861-934``): distinct active experts, distinct missing
 experts and calls, plus the number of routes that missed.
 
-Pins (tests/test_oracle_slots.py): closed-form table lookups on hand-built
-tables (identity, permutation, partial residency, all-miss) and the
-invariant slot_for_id[id_of_slot[s]] == s.
+Pins of ``slot_map`` (tests/test_oracle_experts.py): closed-form table lookups
+on hand-built tables (identity, permutation, partial residency, all-miss) and
+the invariant slot_for_id[id_of_slot[s]] == s.
+
+``lru_ensure`` restates the admission of the miss path from the reference's
+CPU mirror of its admission kernel (``moe/offload_kernels.py:128-188``,
+``_ensure_experts_hybrid_cpu``, which the reference holds bit-identical to its
+GPU kernel; fixed cap, ``frac_q16 == 0``), with the miss order "lowest_id"
+(``by_recency=False``) or "recency" (``:9-16``).  The uncapped lowest-id form
+stands for flashlib's ``lru_ensure`` (``:19-40``), whose own order is not
+available (third-party, absent): parity with flashlib is unpinned; the form
+is pinned by the reference's invariants (tests/moe/test_offload.py:379-404:
+unique victim slots, src rows = the missing ids in order; :522-602: the slot
+tables stay inverse of each other across layers) and by a brute-force
+properties checked in tests/test_oracle_slots.py (LRU victims, residency,
+caps, recency order).
 """
 
 from __future__ import annotations
@@ -35,3 +48,80 @@ def slot_map(topk_ids, slot_for_id):
     stats[STAT_CALLS] = 1
     stats[STAT_MISSED_ROUTES] = int(miss.sum())
     return slots, miss.astype(np.uint8), stats
+
+
+class CacheState:
+    """Mutable admission state of one slot cache (``moe/offload_cache.py:155-175``):
+    ``slot_for_id`` [L, E], ``id_of_slot`` [S] (flat ``layer * E + expert``),
+    ``usage`` [S] (step of last use), ``step``, ``recency`` [L, E]."""
+
+    def __init__(self, num_layers: int, num_experts: int, cache_size: int):
+        self.L, self.E, self.S = num_layers, num_experts, cache_size
+        self.slot_for_id = np.full((num_layers, num_experts), -1, dtype=np.int32)
+        self.id_of_slot = np.full(cache_size, -1, dtype=np.int32)
+        self.usage = np.zeros(cache_size, dtype=np.int64)
+        self.step = 0
+        self.recency = np.zeros((num_layers, num_experts), dtype=np.int64)
+
+    def copy(self) -> "CacheState":
+        c = CacheState(self.L, self.E, self.S)
+        c.slot_for_id = self.slot_for_id.copy()
+        c.id_of_slot = self.id_of_slot.copy()
+        c.usage = self.usage.copy()
+        c.step = self.step
+        c.recency = self.recency.copy()
+        return c
+
+
+def lru_ensure(state: CacheState, layer: int, expert_ids, max_fetch: int = -1, by_recency: bool = False,
+               capacity: int | None = None):
+    """One admission call (``moe/offload_kernels.py:128-188``); mutates ``state``.
+
+    Returns (slot ids [same shape], evict_slots, src_indices, num_missing, stats).
+    Ids outside [0, E) are not seen and map to -1."""
+    ids = np.asarray(expert_ids, dtype=np.int32)
+    flat = ids.reshape(-1)
+    E = state.E
+    seen = []
+    for e in flat.tolist():  # first appearance order (:135-138)
+        if 0 <= e < E and e not in seen:
+            seen.append(e)
+    state.step += 1
+    step = state.step
+    for e in seen:  # touch the resident ones (:143-146)
+        s = int(state.slot_for_id[layer, e])
+        if s != -1:
+            state.usage[s] = step
+    missing = [e for e in seen if int(state.slot_for_id[layer, e]) == -1]
+    if by_recency:
+        rec = state.recency[layer]
+        missing.sort(key=lambda e: (-int(rec[e]), e))
+    else:
+        missing.sort()
+    n = len(missing) if max_fetch < 0 else min(len(missing), max_fetch)
+    if capacity is not None:
+        n = min(n, capacity)
+    evict, src = [], []
+    miss_set = set(missing)
+    for idx in range(n):  # one victim after the other (:163-174)
+        expert = missing[idx]
+        victim = min(range(state.S), key=lambda s: (int(state.usage[s]), s))
+        old = int(state.id_of_slot[victim])
+        if old >= 0:
+            state.slot_for_id.reshape(-1)[old] = -1
+        state.id_of_slot[victim] = layer * E + expert
+        state.slot_for_id[layer, expert] = victim
+        state.usage[victim] = step
+        evict.append(victim)
+        src.append(expert)
+    if by_recency:  # (:176-178)
+        for e in seen:
+            state.recency[layer, e] = step
+    out = np.array([int(state.slot_for_id[layer, e]) if 0 <= e < E else -1 for e in flat.tolist()],
+                   dtype=np.int32).reshape(ids.shape)
+    stats = np.zeros(4, dtype=np.int64)
+    stats[STAT_ACTIVE] = len(seen)
+    stats[STAT_MISS] = len(missing)
+    stats[STAT_CALLS] = 1
+    stats[STAT_MISSED_ROUTES] = sum(1 for e in flat.tolist() if e in miss_set)
+    return out, np.array(evict, dtype=np.int32), np.array(src, dtype=np.int32), len(missing), stats

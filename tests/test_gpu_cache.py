@@ -1,0 +1,158 @@
+"""The expert-cache miss path on the GPU: LRU admission (ftmoe_lru_ensure)
+bit-exact against the oracle's restatement of the reference's CPU mirror
+(moe/offload_kernels.py:128-188) over multi-step, multi-layer sequences; the
+PCIe gather (ftmoe_fetch_experts) byte-exact; and an offload layer that admits
+and fetches its misses computing what the all-resident layer computes
+(layers/moe.py:288-320)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import slots as S
+from oracle import synth
+from freetoken_amd import ops
+from freetoken_amd.core import moe_phase
+from freetoken_amd.layers.moe import OffloadMoELayer
+from freetoken_amd.moe.offload_cache import ExpertSlotCache
+
+from _helpers import bf16_dev, to_device_bank, to_np
+from conftest import COS_TOL, MAX_REL_TOL, cosine, max_rel
+
+
+class _DevCache:
+    """Device copy of an oracle CacheState plus the admission outputs."""
+
+    def __init__(self, st: S.CacheState, dev, capacity: int):
+        self.slot_for_id = torch.from_numpy(st.slot_for_id.copy()).to(dev)
+        self.id_of_slot = torch.from_numpy(st.id_of_slot.copy()).to(dev)
+        self.usage = torch.from_numpy(st.usage.copy()).to(dev)
+        self.step = torch.tensor([st.step], dtype=torch.int64, device=dev)
+        self.recency = torch.from_numpy(st.recency.copy()).to(dev)
+        self.evict = torch.full((capacity,), -7, dtype=torch.int32, device=dev)
+        self.src = torch.full((capacity,), -7, dtype=torch.int32, device=dev)
+        self.n = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.nmiss = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.stats = torch.zeros(4, dtype=torch.int64, device=dev)
+
+    def ensure(self, layer, ids, max_fetch, by_recency):
+        t = torch.from_numpy(np.ascontiguousarray(ids, dtype=np.int32)).to(self.slot_for_id.device)
+        ops.lru_ensure(t, layer, self.slot_for_id, self.id_of_slot, self.usage, self.step, self.evict, self.src,
+                       self.n, self.nmiss, recency=self.recency[layer] if by_recency else None,
+                       max_fetch=max_fetch, stats=self.stats)
+        return t
+
+    def check(self, st: S.CacheState, by_recency: bool):
+        np.testing.assert_array_equal(to_np(self.slot_for_id), st.slot_for_id)
+        np.testing.assert_array_equal(to_np(self.id_of_slot), st.id_of_slot)
+        np.testing.assert_array_equal(to_np(self.usage), st.usage)
+        assert int(self.step.item()) == st.step
+        if by_recency:
+            np.testing.assert_array_equal(to_np(self.recency), st.recency)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("L,E,Sz,max_k,max_fetch,by_recency", [
+    (1, 16, 4, 6, -1, False),      # more misses than slots: the sequential rule
+    (3, 64, 24, 12, -1, False),
+    (2, 256, 64, 64, -1, False),   # C4-like table, decode batch 8
+    (2, 128, 40, 40, 5, True),     # capped, most recent first
+    (4, 160, 160, 64, 3, False),   # capped, lowest id first
+    (1, 1024, 300, 512, -1, True), # a prefill-sized call
+])
+def test_lru_ensure_matches_oracle(dev, L, E, Sz, max_k, max_fetch, by_recency):
+    rng = np.random.default_rng(E + Sz + max_k)
+    st = S.CacheState(L, E, Sz)
+    cap = E  # every miss of a call fits the lists
+    dc = _DevCache(st, dev, cap)
+    acc = np.zeros(4, dtype=np.int64)
+    for call in range(25):
+        layer = int(rng.integers(L))
+        n = int(rng.integers(1, max_k + 1))
+        # skewed ids so that hits, misses and evictions all occur
+        ids = np.minimum((rng.pareto(1.2, size=n) * E / 8).astype(np.int64), E - 1).astype(np.int32)
+        if call % 7 == 3:
+            ids[0] = -1  # an id outside [0, E) is skipped
+        out_ref, evict, src, nmiss, stats = S.lru_ensure(st, layer, ids, max_fetch=max_fetch, by_recency=by_recency,
+                                                         capacity=cap)
+        acc += stats
+        out = dc.ensure(layer, ids, max_fetch, by_recency)
+        np.testing.assert_array_equal(to_np(out), out_ref, err_msg=f"call {call}")
+        k = int(dc.n.item())
+        assert k == evict.size and int(dc.nmiss.item()) == nmiss, (call, k, evict.size)
+        np.testing.assert_array_equal(to_np(dc.evict)[:k], evict)
+        np.testing.assert_array_equal(to_np(dc.src)[:k], src)
+        dc.check(st, by_recency)
+    np.testing.assert_array_equal(to_np(dc.stats), acc)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [0, 1, 5])
+def test_fetch_experts_copies_rows(dev, n):
+    rng = np.random.default_rng(11 + n)
+    E, Sz = 12, 8
+    shapes = [(E, 96, 64), (E, 3, 16), (E, 40000)]  # rows of 6 KiB, 48 B and 40 KB (a partial chunk)
+    host = [torch.from_numpy(rng.integers(0, 256, size=s, dtype=np.uint8)).pin_memory() for s in shapes]
+    slots = [torch.full((Sz,) + s[1:], 0xEE, dtype=torch.uint8, device=dev) for s in shapes]
+    evict = torch.tensor(list(rng.permutation(Sz)[:6]), dtype=torch.int32, device=dev)
+    src = torch.tensor(list(rng.permutation(E)[:6]), dtype=torch.int32, device=dev)
+    num = torch.tensor([n], dtype=torch.int32, device=dev)
+    ops.fetch_experts(host, slots, evict, src, num)
+    torch.cuda.synchronize()
+    ev, sr = evict.tolist(), src.tolist()
+    for h, d in zip(host, slots):
+        got = d.cpu()
+        for s in range(Sz):
+            if s in ev[:n]:
+                assert torch.equal(got[s], h[sr[ev.index(s)]]), s
+            else:
+                assert (got[s] == 0xEE).all(), s
+
+
+def _pinned_bank_sources(bank):
+    names = ("gate_up", "gate_up_scale", "down", "down_scale")
+    arrays = (bank.gate_up, bank.gate_up_scale, bank.down, bank.down_scale)
+    return names, [torch.from_numpy(np.ascontiguousarray(a)).pin_memory() for a in arrays]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4"])
+def test_offload_layer_admits_and_fetches_misses(dev, fmt):
+    """Two layers share 6 slots over 16 experts; every decode call admits its
+    misses, gathers them over PCIe and must equal the all-resident layer."""
+    rng = np.random.default_rng(61)
+    L, E, Sz, H, I, k, M = 2, 16, 6, 512, 256, 2, 3
+    banks = [synth.make_bank(fmt, E, H, I, rng) for _ in range(L)]
+    cache = ExpertSlotCache(L, E, Sz, {"fp8": "fp8_block", "mxfp4": "ds_fp4"}[fmt], device=dev)
+    # slot banks with the decode dtypes (contents arrive by the gather)
+    eb = to_device_bank(banks[0], dev, rows=np.arange(Sz))
+    cache.set_bank_caches(gate_up=eb.gate_up, gate_up_scale=eb.gate_up_scale, down=eb.down, down_scale=eb.down_scale)
+    for t in cache.banks.values():
+        t.view(torch.uint8).fill_(0)
+    names = ("gate_up", "gate_up_scale", "down", "down_scale")
+    per_layer = [_pinned_bank_sources(b)[1] for b in banks]
+    cache.set_bank_sources({n: [per_layer[l][j] for l in range(L)] for j, n in enumerate(names)})
+    cache.reset()
+    layers = [OffloadMoELayer(l, E, k, H, I, device=dev) for l in range(L)]
+    for lay in layers:
+        lay.offload_cache = cache
+    for call in range(6):
+        l = call % L
+        x = synth.activations(rng, M, H)
+        logits = synth.normal(rng, (M, E))
+        w_ref, ids_ref = oracle.routing.softmax_topk(logits, k, True)
+        y_ref = oracle.experts.moe_layer("decode", x, w_ref, ids_ref, banks[l], None)
+        ids = torch.from_numpy(ids_ref.copy()).to(dev)
+        with moe_phase("decode", backend="offload"):
+            y = layers[l].routed_forward(bf16_dev(x, dev), torch.from_numpy(w_ref).to(dev), ids)
+        slots_now = to_np(ids)
+        assert (slots_now >= 0).all() and (slots_now < Sz).all()
+        sft = to_np(cache.slot_for_id)
+        np.testing.assert_array_equal(slots_now, sft[l][ids_ref])
+        g = to_np(y)
+        assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, (fmt, call, max_rel(g, y_ref))
+    st = cache.decode_miss_stats()
+    assert st["layer_calls"] == 6 and st["missing_per_layer"] > 0

@@ -44,6 +44,18 @@ def test_validation_errors_without_launch():
     bank = _lib.FtmoeBank(_lib.FMT_FP8_B128, 8, 1000, 256, 16, None, 16, None)
     rc = L.ftmoe_experts_decode(w, 1, 8, w, w, ctypes.byref(bank), None, 0, 0, w, w, 1 << 20, None)
     assert rc == _lib.FTMOE_ERR_UNSUPPORTED  # hidden not a multiple of 128
+    # miss path: admission tables beyond one workgroup's LDS, unaligned gather rows
+    rc = L.ftmoe_lru_ensure(w, 8, 0, 1, 256, w, w, w, w, 9000, None, -1, w, w, 8, w, w, None, None)
+    assert rc == _lib.FTMOE_ERR_UNSUPPORTED and b"S=9000" in L.ftmoe_last_error()
+    rc = L.ftmoe_lru_ensure(w, 8, 2, 2, 256, w, w, w, w, 64, None, -1, w, w, 8, w, w, None, None)
+    assert rc == _lib.FTMOE_ERR_UNSUPPORTED  # layer outside [0, num_layers)
+    rc = L.ftmoe_lru_ensure(w, 8, 0, 1, 256, None, w, w, w, 64, None, -1, w, w, 8, w, w, None, None)
+    assert rc == _lib.FTMOE_ERR_INVALID
+    fb = (_lib.FtmoeFetchBank * 1)(_lib.FtmoeFetchBank(16, 16, 24))
+    rc = L.ftmoe_fetch_experts(fb, 1, w, w, w, 4, None)
+    assert rc == _lib.FTMOE_ERR_UNSUPPORTED and b"16-byte" in L.ftmoe_last_error()
+    rc = L.ftmoe_fetch_experts(fb, 9, w, w, w, 4, None)
+    assert rc == _lib.FTMOE_ERR_UNSUPPORTED
 
 
 def test_align_sizes_formula():

@@ -1,0 +1,118 @@
+"""Pins of the LRU admission of oracle/slots.py (restating the reference's CPU
+mirror of its admission kernel, moe/offload_kernels.py:128-188).
+
+The reference's own invariants (tests/moe/test_offload.py:379-404 and
+:522-602) are restated on the oracle's tables, and the admission is checked
+against properties that do not retype its loop: the victims of a call are the
+least recently used slots in (usage, slot) order, resident experts keep their
+slots, caps and the recency order behave as documented."""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import slots as S
+
+
+def _inverse_ok(st: S.CacheState) -> bool:
+    flat = st.slot_for_id.reshape(-1)
+    for s, f in enumerate(st.id_of_slot.tolist()):
+        if f >= 0 and flat[f] != s:
+            return False
+    for f, s in enumerate(flat.tolist()):
+        if s >= 0 and st.id_of_slot[s] != f:
+            return False
+    return True
+
+
+def test_large_miss_batch_unique_slots():
+    # tests/moe/test_offload.py:379-404
+    st = S.CacheState(40, 256, 1664)
+    ids = np.arange(256, dtype=np.int32).reshape(32, 8)
+    out, evict, src, nmiss, _ = S.lru_ensure(st, 0, ids)
+    assert nmiss == 256 and evict.size == 256
+    assert out.min() >= 0 and out.max() < 1664
+    assert np.unique(evict).size == 256 and evict.min() >= 0 and evict.max() < 1664
+    assert src.tolist() == list(range(256))
+    # a fresh cache hands out slots in index order (all usages 0)
+    assert evict.tolist() == list(range(256))
+    assert (out.reshape(-1) == np.arange(256)).all()
+
+
+def test_tables_stay_inverse_across_layers():
+    # tests/moe/test_offload.py:522-602 (layer 1 fills the cache, layer 0 then evicts two of its slots)
+    L, E = 2, 8
+    st = S.CacheState(L, E, 8)
+    S.lru_ensure(st, 0, [3, 5])
+    assert _inverse_ok(st)
+    S.lru_ensure(st, 1, list(range(E)))
+    assert _inverse_ok(st)
+    out, evict, src, nmiss, _ = S.lru_ensure(st, 0, [3, 5])
+    assert _inverse_ok(st) and evict.size == nmiss
+    out3, _, _, _, _ = S.lru_ensure(st, 1, [1, 2])
+    assert _inverse_ok(st)
+    for e, s in zip([1, 2], out3.tolist()):
+        assert st.id_of_slot[s] == 1 * E + e
+
+
+def test_victims_are_least_recently_used():
+    rng = np.random.default_rng(5)
+    L, E, Sz = 3, 32, 12
+    st = S.CacheState(L, E, Sz)
+    for call in range(60):
+        layer = int(rng.integers(L))
+        ids = rng.integers(0, E, size=int(rng.integers(1, 9)))
+        before = st.copy()
+        out, evict, src, nmiss, stats = S.lru_ensure(st, layer, ids)
+        seen = sorted(set(ids.tolist()))
+        resident = [e for e in seen if before.slot_for_id[layer, e] >= 0]
+        missing = [e for e in seen if before.slot_for_id[layer, e] < 0]
+        assert src.tolist() == missing and nmiss == len(missing)
+        # untouched slots ranked by (usage, slot); the misses take the first ones
+        touched = {int(before.slot_for_id[layer, e]) for e in resident}
+        free = sorted((int(before.usage[s]), s) for s in range(Sz) if s not in touched)
+        if len(missing) <= len(free):
+            assert evict.tolist() == [s for _, s in free[: len(missing)]]
+        # resident experts keep their slots, every seen expert ends resident
+        for e in resident:
+            assert st.slot_for_id[layer, e] == before.slot_for_id[layer, e]
+        if len(seen) <= Sz:
+            assert (out >= 0).all()
+            for e, s in zip(ids.tolist(), out.tolist()):
+                assert st.id_of_slot[s] == layer * E + e
+        assert _inverse_ok(st)
+        assert stats.tolist() == [len(seen), len(missing), 1, sum(1 for e in ids.tolist() if e in missing)]
+        assert st.step == call + 1
+        assert all(st.usage[s] == st.step for s in out.tolist() if s >= 0)
+
+
+def test_cap_and_recency_order():
+    E = 16
+    st = S.CacheState(1, E, 8)
+    S.lru_ensure(st, 0, [9], by_recency=True)  # step 1: expert 9 seen (resident)
+    S.lru_ensure(st, 0, [4], by_recency=True)  # step 2: expert 4 seen
+    st.slot_for_id[:] = -1                     # drop everything: all three below miss
+    st.id_of_slot[:] = -1
+    out, evict, src, nmiss, _ = S.lru_ensure(st, 0, [1, 9, 4], max_fetch=2, by_recency=True)
+    # most recently seen first (4 at step 2, 9 at step 1), then 1 (never seen); capped at 2
+    assert nmiss == 3 and src.tolist() == [4, 9]
+    assert out.tolist()[0] == -1 and out.tolist()[1] >= 0 and out.tolist()[2] >= 0
+    st2 = S.CacheState(1, E, 8)
+    out, evict, src, nmiss, _ = S.lru_ensure(st2, 0, [7, 3, 5], max_fetch=2)
+    assert src.tolist() == [3, 5] and out.tolist() == [-1, 0, 1]
+
+
+def test_out_of_range_ids_are_not_seen():
+    st = S.CacheState(1, 8, 4)
+    out, evict, src, nmiss, stats = S.lru_ensure(st, 0, [-1, 8, 2])
+    assert out.tolist() == [-1, -1, 0] and src.tolist() == [2] and stats.tolist() == [1, 1, 1, 1]
+
+
+def test_more_misses_than_slots_follows_the_sequential_rule():
+    # every slot is taken in (usage, slot) order; the later misses then reuse
+    # slot 0 (all usages equal), each evicting the previous one
+    st = S.CacheState(1, 8, 2)
+    out, evict, src, nmiss, _ = S.lru_ensure(st, 0, [0, 1, 2, 3])
+    assert evict.tolist() == [0, 1, 0, 0] and src.tolist() == [0, 1, 2, 3]
+    assert out.tolist() == [-1, 1, -1, 0]
+    assert _inverse_ok(st)
