@@ -297,6 +297,53 @@ def run_prefill(fmt: str, steps: int, warmup: int, gen, dev, M: int = 8192):
 # ----------------------------------------------------------------------------- CPU baseline
 
 
+PCIE_PEAK_GBS = 64.0  # PCIe Gen5 x16, one direction
+
+
+def run_miss_fetch(gen, dev, n_fetch: int = 8, steps: int = 10):
+    """Miss path at C4 shape: each step routes n_fetch experts none of which is
+    resident (two disjoint expert sets alternate over n_fetch slots), so the
+    admission evicts and the gather moves n_fetch whole experts from pinned host
+    banks over PCIe.  Reports the gather's GB/s against the link and the
+    admission kernel's time."""
+    c = C4
+    H, I = c["H"], c["I"]
+    E, S = 2 * n_fetch, n_fetch
+    rows = {"gate_up": (2 * I, H), "gate_up_scale": (2 * I // 128 * (H // 128) * 4,), "down": (H, I),
+            "down_scale": (H // 128 * (I // 128) * 4,)}
+    host, slots = [], []
+    for shape in rows.values():
+        h = torch.empty((E,) + shape, dtype=torch.uint8, pin_memory=True)
+        h.view(-1)[:: 4097] = 1
+        host.append(h)
+        slots.append(torch.empty((S,) + shape, dtype=torch.uint8, device=dev))
+    expert_bytes = sum(int(h[0].numel()) for h in host)
+    slot_for_id = torch.full((1, E), -1, dtype=torch.int32, device=dev)
+    id_of_slot = torch.full((S,), -1, dtype=torch.int32, device=dev)
+    usage = torch.zeros((S,), dtype=torch.int64, device=dev)
+    step = torch.zeros((1,), dtype=torch.int64, device=dev)
+    evict = torch.zeros((E,), dtype=torch.int32, device=dev)
+    src = torch.zeros((E,), dtype=torch.int32, device=dev)
+    num = torch.zeros((1,), dtype=torch.int32, device=dev)
+    nmiss = torch.zeros((1,), dtype=torch.int32, device=dev)
+    sets = [torch.arange(g * n_fetch, (g + 1) * n_fetch, dtype=torch.int32, device=dev) for g in range(2)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps + 1)]
+    for i in range(steps + 1):  # call 0 warms up
+        ids = sets[i % 2].clone()
+        ev[i][0].record()
+        ops.lru_ensure(ids, 0, slot_for_id, id_of_slot, usage, step, evict, src, num, nmiss)
+        ev[i][1].record()
+        ops.fetch_experts(host, slots, evict, src, num, max_entries=n_fetch)
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    adm = statistics.median(ev[i][0].elapsed_time(ev[i][1]) for i in range(1, steps + 1))
+    fet = statistics.median(ev[i][1].elapsed_time(ev[i][2]) for i in range(1, steps + 1))
+    assert int(num.item()) == n_fetch and int(nmiss.item()) == n_fetch
+    gbs = n_fetch * expert_bytes / (fet * 1e-3) / 1e9
+    return dict(experts_per_step=n_fetch, expert_bytes=expert_bytes, admission_us=adm * 1e3, fetch_ms=fet,
+                fetch_gbs=gbs, pcie_frac=gbs / PCIE_PEAK_GBS)
+
+
 def cpu_baseline(layer: DecodeLayer, M: int, budget_s: float, gen, dev):
     """C++ restatement of the reference CPU executor on this host: the same C4
     routing (resident slots), bf16-dequantised banks (the reference's CPU route
@@ -380,6 +427,7 @@ def main() -> int:
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--miss-only", action="store_true", help="time the miss path (admission + PCIe gather) alone")
     ap.add_argument("--prefill-only", choices=("fp8_block", "mxfp4"), default=None,
                     help="profiling aid: run only the C5 prefill of this format and print its result")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -402,6 +450,11 @@ def main() -> int:
         b.copy_(a)
         torch.cuda.synchronize()
         del a, b
+
+    if args.miss_only:
+        res = run_miss_fetch(gen, dev)
+        print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}), flush=True)
+        return 0
 
     if args.prefill_only:
         res = run_prefill(args.prefill_only, args.steps, args.warmup, gen, dev)
@@ -442,6 +495,8 @@ def main() -> int:
         for fmt in ("fp8_block", "mxfp4"):
             log(f"[bench] sweep C5 prefill {fmt}")
             sweep[f"c5_prefill_8192_{fmt}"] = run_prefill(fmt, 5, 1, gen, dev)
+        log("[bench] sweep C4 miss path (admission + PCIe gather of 8 experts per step)")
+        sweep["c4_miss_fetch_8_experts"] = run_miss_fetch(gen, dev)
 
     def rnd(d):
         return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}
