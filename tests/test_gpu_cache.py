@@ -156,3 +156,53 @@ def test_offload_layer_admits_and_fetches_misses(dev, fmt):
         assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, (fmt, call, max_rel(g, y_ref))
     st = cache.decode_miss_stats()
     assert st["layer_calls"] == 6 and st["missing_per_layer"] > 0
+
+
+@pytest.mark.gpu
+def test_miss_path_replays_in_a_graph(dev):
+    """Admission, gather and experts captured once (the decode graph of the
+    reference, engine/graph.py:127-187) and replayed with a new routing each
+    time: every replay admits that call's misses and matches the oracle."""
+    rng = np.random.default_rng(67)
+    E, Sz, H, I, k, M = 16, 4, 512, 256, 2, 2
+    bank = synth.make_bank("fp8", E, H, I, rng)
+    cache = ExpertSlotCache(1, E, Sz, "fp8_block", device=dev)
+    eb = to_device_bank(bank, dev, rows=np.arange(Sz))
+    cache.set_bank_caches(gate_up=eb.gate_up, gate_up_scale=eb.gate_up_scale, down=eb.down, down_scale=eb.down_scale)
+    names, host = _pinned_bank_sources(bank)
+    cache.set_bank_sources({n: [h] for n, h in zip(names, host)})
+    cache.reset()
+    layer = OffloadMoELayer(0, E, k, H, I, device=dev)
+    layer.offload_cache = cache
+    x_buf = torch.zeros((M, H), dtype=torch.bfloat16, device=dev)
+    w_buf = torch.zeros((M, k), dtype=torch.float32, device=dev)
+    ids_buf = torch.zeros((M, k), dtype=torch.int32, device=dev)
+
+    def call():
+        ids = ids_buf.clone()
+        with moe_phase("decode", backend="offload"):
+            return layer.routed_forward(x_buf, w_buf, ids)
+
+    ids_buf.copy_(torch.tensor([[0, 1], [2, 3]], dtype=torch.int32))  # warm-up call (eager) sizes the workspace
+    call()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            y = call()
+    torch.cuda.synchronize()
+    for rep in range(5):
+        x = synth.activations(rng, M, H)
+        logits = synth.normal(rng, (M, E))
+        w_ref, ids_ref = oracle.routing.softmax_topk(logits, k, True)
+        x_buf.copy_(bf16_dev(x, dev))
+        w_buf.copy_(torch.from_numpy(w_ref))
+        ids_buf.copy_(torch.from_numpy(ids_ref))
+        graph.replay()
+        torch.cuda.synchronize()
+        y_ref = oracle.experts.moe_layer("decode", x, w_ref, ids_ref, bank, None)
+        g = to_np(y)
+        assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, (rep, max_rel(g, y_ref))
+        sft = to_np(cache.slot_for_id)[0]
+        assert (sft[np.unique(ids_ref)] >= 0).all(), rep
