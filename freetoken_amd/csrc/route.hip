@@ -2,20 +2,16 @@
 //
 // One wave per token.  Expert e lives in lane (e % 64), register slot e / 64;
 // PER = ceil(E / 64) slots per lane is a template parameter.  Selection is k
-// rounds of a wave-wide maximum over 64-bit keys (order_key(value) << 32 | ~index):
-// the larger value wins and on equal values the lower expert index wins -- the
-// lowest-index tie rule of the reference's gpt-oss router
-// (kernel/triton/mxfp4_moe.py:288-331).  Each lane keeps the best not-yet-taken
-// key of its own slots, so a round costs one wave reduction plus a local update.
+// rounds of: a wave-wide float maximum over the entries still available, then
+// one ballot per slot for the entries holding it; the lowest expert index
+// among them wins (the lowest-index tie rule of the reference's gpt-oss router,
+// kernel/triton/mxfp4_moe.py:288-331; -0.0 equals +0.0).  The ballots and the
+// winner are wave-uniform, so a round is one reduction plus scalar work.
 #include "kernels.h"
 
 namespace ftmoe {
 
 constexpr int kRouteWaves = 4;
-
-__device__ __forceinline__ uint64_t pack_key(float v, int e) {
-  return (static_cast<uint64_t>(order_key(v)) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(e));
-}
 
 template <typename T>
 __device__ __forceinline__ float load_logit(const T* p);
@@ -24,22 +20,36 @@ __device__ __forceinline__ float load_logit<float>(const float* p) { return *p; 
 template <>
 __device__ __forceinline__ float load_logit<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
 
-// k rounds of selection over keys[PER] (0 = empty); returns the winner index of
-// round r in lane r (lanes >= k: -1).
+// Largest available value of v[PER] in the wave, the lowest index holding it
+// (slot-major: index = 64 * slot + lane); -1 when nothing is available.
 template <int PER>
-__device__ __forceinline__ int select_topk(uint64_t (&keys)[PER], int k) {
+__device__ __forceinline__ int wave_argmax(const float (&v)[PER], const bool (&live)[PER]) {
+  float best = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (live[j]) best = fmaxf(best, v[j]);
+  best = wave_max_f32(best);
+  int win = -1;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint64_t b = __ballot(live[j] && v[j] == best);
+    if (win < 0 && b != 0) win = j * kWave + __ffsll(static_cast<long long>(b)) - 1;
+  }
+  return win;
+}
+
+// k rounds of selection; returns the winner index of round r in lane r (lanes
+// >= k, and rounds with nothing available: -1).
+template <int PER>
+__device__ __forceinline__ int select_topk(const float (&v)[PER], bool (&live)[PER], int k) {
   const int lane = lane_id();
   int mine = -1;
   for (int r = 0; r < k; ++r) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) best = max_u64(best, keys[j]);
-    best = wave_max_u64(best);
-    const int win = static_cast<int>(~static_cast<uint32_t>(best));
-    if ((win & (kWave - 1)) == lane) {
+    const int win = wave_argmax<PER>(v, live);
+    if (win >= 0 && (win & (kWave - 1)) == lane) {
 #pragma unroll
       for (int j = 0; j < PER; ++j)
-        if (j == win / kWave) keys[j] = 0;
+        if (j == win / kWave) live[j] = false;
     }
     if (lane == r) mine = win;
   }
@@ -59,14 +69,14 @@ __global__ void __launch_bounds__(kRouteWaves * kWave) softmax_topk_kernel(const
   if (tok >= M) return;
   const T* row = logits + static_cast<size_t>(tok) * E;
   float v[PER];
-  uint64_t keys[PER];
+  bool live[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int e = lane + j * kWave;
     v[j] = (e < E) ? load_logit<T>(row + e) : -INFINITY;
-    keys[j] = (e < E) ? pack_key(v[j], e) : 0;
+    live[j] = e < E;
   }
-  const int my_idx = select_topk<PER>(keys, k);
+  const int my_idx = select_topk<PER>(v, live, k);
   const float my_val = (lane < k) ? load_logit<T>(row + my_idx) : -INFINITY;
   const float vmax = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_val), 0));  // rank 0
   float denom;
@@ -146,26 +156,30 @@ __global__ void __launch_bounds__(kRouteWaves * kWave) grouped_sigmoid_kernel(
   const bool lane_groups = (E % kWave) == 0 && per <= kWave && (per & (per - 1)) == 0;
   if (n_group > 1 && lane_groups) {
     // group of (lane, slot j) = j * (64 / per) + lane / per
+    // group of (lane, slot j) = j * (64 / per) + lane / per: ascending in
+    // (slot, lane), so the lowest (slot, lane) holding the maximum is the
+    // lowest group index
     const int gpl = kWave / per;
-    uint64_t gk[PER];
+    float gs[PER];
+    bool glive[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       float a1 = c[j], a2 = -INFINITY;
       block_top2(a1, a2, per);
-      const int grp = j * gpl + lane / per;
-      gk[j] = (lane % per == 0 && lane + j * kWave < E) ? pack_key(a1 + a2, grp) : 0;
+      gs[j] = a1 + a2;
+      glive[j] = lane % per == 0 && lane + j * kWave < E;
     }
     gmask = 0;
     for (int r = 0; r < topk_group; ++r) {
-      uint64_t best = 0;
+      const int win = wave_argmax<PER>(gs, glive);
+      if (win < 0) break;
+      const int wl = win & (kWave - 1), wj = win / kWave;
+      if (wl == lane) {
 #pragma unroll
-      for (int j = 0; j < PER; ++j) best = max_u64(best, gk[j]);
-      best = wave_max_u64(best);
-      const int win = static_cast<int>(~static_cast<uint32_t>(best));
-#pragma unroll
-      for (int j = 0; j < PER; ++j)
-        if (gk[j] == best) gk[j] = 0;
-      gmask |= 1ull << win;
+        for (int j = 0; j < PER; ++j)
+          if (j == wj) glive[j] = false;
+      }
+      gmask |= 1ull << (wj * gpl + wl / per);
     }
   } else if (n_group > 1) {
 #pragma unroll
@@ -186,23 +200,26 @@ __global__ void __launch_bounds__(kRouteWaves * kWave) grouped_sigmoid_kernel(
       }
       gscore = a1 + a2;
     }
-    uint64_t gkey = (lane < n_group) ? pack_key(gscore, lane) : 0;
+    float gv[1] = {gscore};
+    bool glive[1] = {lane < n_group};
     gmask = 0;
     for (int r = 0; r < topk_group; ++r) {
-      const uint64_t best = wave_max_u64(gkey);
-      const int win = static_cast<int>(~static_cast<uint32_t>(best));
-      if (lane == win) gkey = 0;
+      const int win = wave_argmax<1>(gv, glive);
+      if (win < 0) break;
+      if (lane == win) glive[0] = false;
       gmask |= 1ull << win;
     }
   }
-  uint64_t keys[PER];
+  float sel[PER];
+  bool live[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int e = lane + j * kWave;
     const bool kept = (gmask >> ((e < E ? e : 0) / per)) & 1ull;
-    keys[j] = (e < E) ? pack_key(kept ? c[j] : -INFINITY, e) : 0;
+    sel[j] = kept ? c[j] : -INFINITY;
+    live[j] = e < E;
   }
-  const int my_idx = select_topk<PER>(keys, k);
+  const int my_idx = select_topk<PER>(sel, live, k);
   float w = 0.0f;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
