@@ -140,6 +140,11 @@ class DecodeLayer:
             top = torch.sort(torch.argsort(freq, descending=True, stable=True)[: cfg["slots"]]).values
             self.table[top] = torch.arange(cfg["slots"], dtype=torch.int32, device=dev)
         self.stats = torch.zeros(4, dtype=torch.int64, device=dev)
+        if cfg["router"] == "softmax":
+            self.router = ops.Router("softmax", cfg["k"], True)
+        else:
+            self.router = ops.Router("grouped_sigmoid", cfg["k"], True, self.bias, cfg["n_group"], cfg["topk_group"],
+                                     cfg["scale"])
 
     def route(self, logits):
         c = self.cfg
@@ -148,10 +153,11 @@ class DecodeLayer:
         return ops.route_grouped_sigmoid(logits, self.bias, c["n_group"], c["topk_group"], c["k"], True, c["scale"])
 
     def step(self, logits, x, out):
-        """Router, then the offload layer's decode: expert ids -> slot ids
-        (ensure_experts) and the experts in one call."""
-        w, ids = self.route(logits)
-        ops.experts_decode(x, w, ids, self.bank, shared=self.shared, out=out, slot_for_id=self.table, stats=self.stats)
+        """Router, expert ids -> slot ids (ensure_experts) and the experts of the
+        offload layer's decode in one call (the router and the permutation
+        share a launch for up to 16 tokens and 64 routes)."""
+        _, _, ids = ops.experts_decode_routed(x, logits, self.router, self.bank, shared=self.shared, out=out,
+                                              slot_for_id=self.table, stats=self.stats)
         return ids
 
     def step_bytes(self, ids: torch.Tensor, M: int) -> tuple[int, int, int]:

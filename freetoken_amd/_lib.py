@@ -42,6 +42,23 @@ class FtmoeBank(ctypes.Structure):
 _bp = ctypes.POINTER(FtmoeBank)
 
 
+ROUTER_SOFTMAX_TOPK, ROUTER_GROUPED_SIGMOID = 0, 1
+
+
+class FtmoeRouter(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int),
+        ("logits", ctypes.c_void_p),
+        ("logits_dtype", ctypes.c_int),
+        ("num_experts", ctypes.c_int),
+        ("renormalize", ctypes.c_int),
+        ("bias", ctypes.c_void_p),
+        ("n_group", ctypes.c_int),
+        ("topk_group", ctypes.c_int),
+        ("routed_scaling_factor", ctypes.c_float),
+    ]
+
+
 class FtmoeFetchBank(ctypes.Structure):
     _fields_ = [
         ("host_rows", ctypes.c_void_p),
@@ -67,6 +84,8 @@ SIGNATURES = {
     "ftmoe_experts_decode": (_i, [_vp, _i, _i, _vp, _vp, _bp, _bp, _i, _i, _vp, _vp, _sz, _vp]),
     "ftmoe_experts_decode_cached": (_i, [_vp, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _bp, _bp, _i, _i, _vp, _vp, _sz,
                                          _vp]),
+    "ftmoe_experts_decode_routed": (_i, [_vp, _i, _i, ctypes.POINTER(FtmoeRouter), _vp, _vp, _vp, _i, _vp, _vp, _vp,
+                                         _bp, _bp, _i, _i, _vp, _vp, _sz, _vp]),
     "ftmoe_experts_prefill_workspace": (_sz, [_i, _i, _bp, _bp]),
     "ftmoe_experts_prefill": (_i, [_vp, _i, _i, _vp, _vp, _bp, _bp, _i, _vp, _vp, _sz, _vp]),
     "ftmoe_stage_timing_begin": (_i, []),

@@ -358,10 +358,12 @@ struct SlotLookup {
   int64_t* stats;
 };
 
+// route (nullable): the router call that produces topk_w / topk_ids first
+// (fused with the permutation when both fit one launch).
 int experts_decode_impl(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
                         const SlotLookup* slots, const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
                         int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
-                        ftmoe_stream_t stream) {
+                        ftmoe_stream_t stream, const ftmoe::RouteArgs* route = nullptr) {
   int rc = check_bank(bank, "routed", false);
   if (rc) return rc;
   if (shared) {
@@ -421,7 +423,8 @@ int experts_decode_impl(const void* x, int M, int top_k, const float* topk_w, co
   // ids the later kernels see: slot ids when the lookup ran here
   const int32_t* route_ids = slots ? slots->slot_ids : topk_ids;
   g_timer.start_call(stream);
-  rc = check_hip(ftmoe::launch_align(al, stream), "experts_decode align");
+  rc = route ? check_hip(ftmoe::launch_route_align(*route, al, stream), "experts_decode route + align")
+             : check_hip(ftmoe::launch_align(al, stream), "experts_decode align");
   if (rc) return rc;
   g_timer.mark();
 
@@ -489,6 +492,55 @@ int ftmoe_experts_decode_cached(const void* x, int M, int top_k, const float* to
   const SlotLookup sl{slot_for_id, num_experts, slot_ids, miss_mask, stats};
   return experts_decode_impl(x, M, top_k, topk_w, topk_ids, &sl, bank, shared, activation,
                              apply_router_weight_on_input, y, workspace, workspace_bytes, stream);
+}
+
+int ftmoe_experts_decode_routed(const void* x, int M, int top_k, const ftmoe_router* router, float* topk_w,
+                                int32_t* topk_ids, const int32_t* slot_for_id, int num_experts, int32_t* slot_ids,
+                                uint8_t* miss_mask, int64_t* stats, const ftmoe_bank* bank, const ftmoe_bank* shared,
+                                int activation, int apply_router_weight_on_input, void* y, void* workspace,
+                                size_t workspace_bytes, ftmoe_stream_t stream) {
+  if (!router || !router->logits || !topk_w || !topk_ids)
+    return fail(FTMOE_ERR_INVALID, "experts_decode_routed: NULL router, logits or router outputs");
+  const int E = router->num_experts, k = top_k;
+  ftmoe::RouteArgs r{};
+  r.logits = router->logits;
+  r.M = M;
+  r.E = E;
+  r.k = k;
+  r.renorm = router->renormalize;
+  r.out_w = topk_w;
+  r.out_ids = topk_ids;
+  if (router->kind == FTMOE_ROUTER_SOFTMAX_TOPK) {
+    if (router->logits_dtype != FTMOE_DTYPE_F32 && router->logits_dtype != FTMOE_DTYPE_BF16)
+      return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode_routed: logits dtype %d", router->logits_dtype);
+    if (E <= 0 || E > 1024 || k <= 0 || k > E || k > 64)
+      return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode_routed: E=%d k=%d (need E<=1024, 0<k<=min(E,64))", E, k);
+    r.grouped = 0;
+    r.logits_bf16 = router->logits_dtype == FTMOE_DTYPE_BF16;
+  } else if (router->kind == FTMOE_ROUTER_GROUPED_SIGMOID) {
+    const int ng = router->n_group, tg = router->topk_group;
+    if (router->logits_dtype != FTMOE_DTYPE_F32)
+      return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode_routed: grouped routing takes float32 logits");
+    if (E <= 0 || E > 1024 || ng <= 0 || ng > 64 || E % ng || tg <= 0 || tg > ng || k <= 0 || k > 64 ||
+        k > E / ng * tg || (ng > 1 && E / ng < 2))
+      return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode_routed: E=%d n_group=%d topk_group=%d k=%d", E, ng, tg, k);
+    r.grouped = 1;
+    r.bias = router->bias;
+    r.n_group = ng;
+    r.topk_group = tg;
+    r.scale = router->routed_scaling_factor;
+  } else {
+    return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode_routed: router kind %d", router->kind);
+  }
+  if (!slot_for_id)
+    return experts_decode_impl(x, M, top_k, topk_w, topk_ids, nullptr, bank, shared, activation,
+                               apply_router_weight_on_input, y, workspace, workspace_bytes, stream, &r);
+  if (!slot_ids) return fail(FTMOE_ERR_INVALID, "experts_decode_routed: NULL slot ids");
+  if (num_experts <= 0 || num_experts > 16384)
+    return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode_routed: num_experts=%d", num_experts);
+  const SlotLookup sl{slot_for_id, num_experts, slot_ids, miss_mask, stats};
+  return experts_decode_impl(x, M, top_k, topk_w, topk_ids, &sl, bank, shared, activation,
+                             apply_router_weight_on_input, y, workspace, workspace_bytes, stream, &r);
 }
 
 size_t ftmoe_experts_prefill_workspace(int M, int top_k, const ftmoe_bank* bank, const ftmoe_bank* shared) {

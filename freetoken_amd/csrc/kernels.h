@@ -71,6 +71,23 @@ hipError_t launch_grouped_sigmoid(const float* logits, const float* bias, int M,
                                   int topk_group, int k, int renorm, float scale, float* w, int32_t* ids,
                                   hipStream_t stream);
 hipError_t launch_align(const AlignArgs& a, hipStream_t stream);
+
+// A router call (softmax top-k or grouped sigmoid top-k) feeding the decode
+// permutation.
+struct RouteArgs {
+  int grouped;            // 0: softmax top-k, 1: grouped sigmoid
+  const void* logits;     // [M, E] float32 (or bf16 for softmax)
+  int logits_bf16;
+  int M, E, k, renorm;
+  const float* bias;      // grouped: nullable [E]
+  int n_group, topk_group;
+  float scale;            // grouped: routed scaling factor
+  float* out_w;           // [M, k]
+  int32_t* out_ids;       // [M, k]
+};
+// Router then permutation: one kernel when the permutation fits one wave
+// (a.ids must be r.out_ids), else the router and launch_align.
+hipError_t launch_route_align(const RouteArgs& r, const AlignArgs& a, hipStream_t stream);
 // Multi-workgroup align for large route counts without slot lookup, stats or
 // segments; gcount: align_gcount_ints(numel, num_experts) ints of workspace.
 size_t align_gcount_ints(int numel, int num_experts);

@@ -7,6 +7,7 @@
 // among them wins (the lowest-index tie rule of the reference's gpt-oss router,
 // kernel/triton/mxfp4_moe.py:288-331; -0.0 equals +0.0).  The ballots and the
 // winner are wave-uniform, so a round is one reduction plus scalar work.
+#include "align_wave.h"
 #include "kernels.h"
 
 namespace ftmoe {
@@ -60,14 +61,9 @@ __device__ __forceinline__ int select_topk(const float (&v)[PER], bool (&live)[P
 // renormalize the weights are the softmax over the k selected logits, else the
 // softmax over all experts evaluated at the selected ones.
 template <typename T, int PER>
-__global__ void __launch_bounds__(kRouteWaves * kWave) softmax_topk_kernel(const T* __restrict__ logits, int M,
-                                                                            int E, int k, int renorm,
-                                                                            float* __restrict__ out_w,
-                                                                            int32_t* __restrict__ out_ids) {
+__device__ __forceinline__ int softmax_token(const T* __restrict__ row, int E, int k, int renorm,
+                                             float* __restrict__ w_out, int32_t* __restrict__ ids_out) {
   const int lane = lane_id();
-  const int tok = blockIdx.x * kRouteWaves + threadIdx.x / kWave;
-  if (tok >= M) return;
-  const T* row = logits + static_cast<size_t>(tok) * E;
   float v[PER];
   bool live[PER];
 #pragma unroll
@@ -90,9 +86,21 @@ __global__ void __launch_bounds__(kRouteWaves * kWave) softmax_topk_kernel(const
     denom = wave_sum_f32(s);
   }
   if (lane < k) {
-    out_w[static_cast<size_t>(tok) * k + lane] = expf(my_val - vmax) / denom;
-    out_ids[static_cast<size_t>(tok) * k + lane] = my_idx;
+    w_out[lane] = expf(my_val - vmax) / denom;
+    ids_out[lane] = my_idx;
   }
+  return my_idx;
+}
+
+template <typename T, int PER>
+__global__ void __launch_bounds__(kRouteWaves * kWave) softmax_topk_kernel(const T* __restrict__ logits, int M,
+                                                                            int E, int k, int renorm,
+                                                                            float* __restrict__ out_w,
+                                                                            int32_t* __restrict__ out_ids) {
+  const int tok = blockIdx.x * kRouteWaves + threadIdx.x / kWave;
+  if (tok >= M) return;
+  softmax_token<T, PER>(logits + static_cast<size_t>(tok) * E, E, k, renorm, out_w + static_cast<size_t>(tok) * k,
+                        out_ids + static_cast<size_t>(tok) * k);
 }
 
 // Multiset top-2 of two disjoint sets given as (largest, second largest).
@@ -130,15 +138,10 @@ __device__ __forceinline__ void block_top2(float& a1, float& a2, int per) {
 //   group g.  The weights s[id] come from the lanes holding them (shuffles),
 //   not from a second read of the logits.
 template <int PER>
-__global__ void __launch_bounds__(kRouteWaves * kWave) grouped_sigmoid_kernel(
-    const float* __restrict__ logits, const float* __restrict__ bias, int M, int E, int n_group, int topk_group,
-    int k, int renorm, float scale, float* __restrict__ out_w, int32_t* __restrict__ out_ids) {
-  __shared__ float s_c[kRouteWaves][PER * kWave];
+__device__ __forceinline__ int grouped_token(const float* __restrict__ row, const float* __restrict__ bias, int E,
+                                             int n_group, int topk_group, int k, int renorm, float scale,
+                                             float* s_c, float* __restrict__ w_out, int32_t* __restrict__ ids_out) {
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
-  const int tok = blockIdx.x * kRouteWaves + wave;
-  if (tok >= M) return;
-  const float* row = logits + static_cast<size_t>(tok) * E;
   const int per = E / n_group;
   float sg[PER], c[PER];
 #pragma unroll
@@ -183,14 +186,14 @@ __global__ void __launch_bounds__(kRouteWaves * kWave) grouped_sigmoid_kernel(
     }
   } else if (n_group > 1) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) s_c[wave][lane + j * kWave] = c[j];
+    for (int j = 0; j < PER; ++j) s_c[lane + j * kWave] = c[j];
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     float gscore = -INFINITY;
     if (lane < n_group) {
       float a1 = -INFINITY, a2 = -INFINITY;  // top-2 with duplicates kept
       for (int i = 0; i < per; ++i) {
-        const float x = s_c[wave][lane * per + i];
+        const float x = s_c[lane * per + i];
         if (x > a1) {
           a2 = a1;
           a1 = x;
@@ -233,9 +236,22 @@ __global__ void __launch_bounds__(kRouteWaves * kWave) grouped_sigmoid_kernel(
   }
   w = w * scale;
   if (lane < k) {
-    out_w[static_cast<size_t>(tok) * k + lane] = w;
-    out_ids[static_cast<size_t>(tok) * k + lane] = my_idx;
+    w_out[lane] = w;
+    ids_out[lane] = my_idx;
   }
+  return my_idx;
+}
+
+template <int PER>
+__global__ void __launch_bounds__(kRouteWaves * kWave) grouped_sigmoid_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int M, int E, int n_group, int topk_group,
+    int k, int renorm, float scale, float* __restrict__ out_w, int32_t* __restrict__ out_ids) {
+  __shared__ float s_c[kRouteWaves][PER * kWave];
+  const int wave = threadIdx.x / kWave;
+  const int tok = blockIdx.x * kRouteWaves + wave;
+  if (tok >= M) return;
+  grouped_token<PER>(logits + static_cast<size_t>(tok) * E, bias, E, n_group, topk_group, k, renorm, scale, s_c[wave],
+                     out_w + static_cast<size_t>(tok) * k, out_ids + static_cast<size_t>(tok) * k);
 }
 
 template <int PER>
@@ -277,6 +293,74 @@ hipError_t launch_grouped_sigmoid(const float* logits, const float* bias, int M,
   else if (per <= 4) launch_grouped_per<4>(logits, bias, M, E, n_group, topk_group, k, renorm, scale, w, ids, stream);
   else if (per <= 8) launch_grouped_per<8>(logits, bias, M, E, n_group, topk_group, k, renorm, scale, w, ids, stream);
   else launch_grouped_per<16>(logits, bias, M, E, n_group, topk_group, k, renorm, scale, w, ids, stream);
+  return hipGetLastError();
+}
+
+
+// ----------------------------------------------------------------------------
+// Router + permutation in one launch for decode-sized calls (at most 16 tokens,
+// at most 64 routes): wave t routes token t, writing the router outputs and
+// the ids into LDS; after one barrier wave 0 runs the one-wave align on them.
+// Saves the permutation's launch and the ids' round trip through memory.
+// ----------------------------------------------------------------------------
+constexpr int kFrontWaves = 16;
+
+template <int GROUPED, typename T, int PER>
+__global__ void __launch_bounds__(kFrontWaves * kWave) route_align_kernel(RouteArgs r, AlignArgs a) {
+  __shared__ int s_ids[kWave];
+  __shared__ float s_c[GROUPED ? kFrontWaves * PER * kWave : 1];
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int tok = wave;
+  if (tok < r.M) {
+    int id;
+    if constexpr (GROUPED) {
+      id = grouped_token<PER>(static_cast<const float*>(r.logits) + static_cast<size_t>(tok) * r.E, r.bias, r.E,
+                              r.n_group, r.topk_group, r.k, r.renorm, r.scale, s_c + wave * PER * kWave,
+                              r.out_w + static_cast<size_t>(tok) * r.k, r.out_ids + static_cast<size_t>(tok) * r.k);
+    } else {
+      id = softmax_token<T, PER>(static_cast<const T*>(r.logits) + static_cast<size_t>(tok) * r.E, r.E, r.k, r.renorm,
+                                 r.out_w + static_cast<size_t>(tok) * r.k, r.out_ids + static_cast<size_t>(tok) * r.k);
+    }
+    if (lane < r.k) s_ids[tok * r.k + lane] = id;
+  }
+  __syncthreads();
+  if (wave == 0) align_wave(a, s_ids);
+}
+
+template <int GROUPED, typename T, int PER>
+static void launch_front(const RouteArgs& r, const AlignArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((route_align_kernel<GROUPED, T, PER>), dim3(1), dim3(kFrontWaves * kWave), 0, stream, r, a);
+}
+
+hipError_t launch_route_align(const RouteArgs& r, const AlignArgs& a, hipStream_t stream) {
+  const int per = (r.E + kWave - 1) / kWave;
+  const bool fused = align_fits_wave(a) && r.M <= kFrontWaves && r.M * r.k <= kWave && (r.grouped ? per <= 4 : true);
+  if (!fused) {
+    const hipError_t err =
+        r.grouped ? launch_grouped_sigmoid(static_cast<const float*>(r.logits), r.bias, r.M, r.E, r.n_group,
+                                           r.topk_group, r.k, r.renorm, r.scale, r.out_w, r.out_ids, stream)
+                  : launch_softmax_topk(r.logits, r.logits_bf16, r.M, r.E, r.k, r.renorm, r.out_w, r.out_ids, stream);
+    if (err != hipSuccess) return err;
+    return launch_align(a, stream);
+  }
+  if (r.grouped) {
+    if (per <= 1) launch_front<1, float, 1>(r, a, stream);
+    else if (per <= 2) launch_front<1, float, 2>(r, a, stream);
+    else launch_front<1, float, 4>(r, a, stream);
+  } else if (r.logits_bf16) {
+    if (per <= 1) launch_front<0, uint16_t, 1>(r, a, stream);
+    else if (per <= 2) launch_front<0, uint16_t, 2>(r, a, stream);
+    else if (per <= 4) launch_front<0, uint16_t, 4>(r, a, stream);
+    else if (per <= 8) launch_front<0, uint16_t, 8>(r, a, stream);
+    else launch_front<0, uint16_t, 16>(r, a, stream);
+  } else {
+    if (per <= 1) launch_front<0, float, 1>(r, a, stream);
+    else if (per <= 2) launch_front<0, float, 2>(r, a, stream);
+    else if (per <= 4) launch_front<0, float, 4>(r, a, stream);
+    else if (per <= 8) launch_front<0, float, 8>(r, a, stream);
+    else launch_front<0, float, 16>(r, a, stream);
+  }
   return hipGetLastError();
 }
 

@@ -133,6 +133,15 @@ class MoELayer:
                 activation=self.activation, apply_router_weight_on_input=self.apply_router_weight_on_input,
             )
             return self._maybe_all_reduce(out)
+        if not _is_prefill(hidden_states.shape[0] * self.top_k) and router_logits is not None:
+            # decode: router and experts in one call (router + permutation in one
+            # launch for small batches)
+            assert not self.apply_router_weight_on_input or self.weight_format == "bf16"
+            y, _, _ = ops.experts_decode_routed(hidden_states, router_logits,
+                                                ops.Router("softmax", self.top_k, self.renormalize), self.bank(),
+                                                shared=self.shared_expert, activation=self.activation,
+                                                apply_router_weight_on_input=self.apply_router_weight_on_input)
+            return self._maybe_all_reduce(y)
         topk_weights, topk_ids = fused_topk(hidden_states, router_logits, self.top_k, self.renormalize)
         return self._maybe_all_reduce(self._resident_gemm(hidden_states, topk_weights, topk_ids))
 

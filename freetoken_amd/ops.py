@@ -323,6 +323,81 @@ def experts_decode(x: torch.Tensor, topk_w: torch.Tensor, topk_ids: torch.Tensor
     return y
 
 
+@dataclass
+class Router:
+    """A router for ``experts_decode_routed``: ``"softmax"`` (``fused_topk``) or
+    ``"grouped_sigmoid"`` (DeepSeek-V3 ``_route``: bias, groups, scaling)."""
+
+    kind: str
+    top_k: int
+    renormalize: bool = True
+    bias: torch.Tensor | None = None
+    n_group: int = 1
+    topk_group: int = 1
+    scale: float = 1.0
+
+
+def experts_decode_routed(x: torch.Tensor, logits: torch.Tensor, router: Router, bank: ExpertBank,
+                          shared: ExpertBank | None = None, activation: str = "silu",
+                          apply_router_weight_on_input: bool = False, out: torch.Tensor | None = None,
+                          slot_for_id: torch.Tensor | None = None, miss_mask: torch.Tensor | None = None,
+                          stats: torch.Tensor | None = None, topk_w: torch.Tensor | None = None,
+                          topk_ids: torch.Tensor | None = None):
+    """Router logits -> decode output in one call (router + ``experts_decode``);
+    returns (y, topk_w, topk_ids), the ids rewritten to slots when ``slot_for_id``
+    is given.  For up to 16 tokens and 64 routes the router and the permutation
+    share one launch."""
+    if x.dtype != torch.bfloat16:
+        raise ValueError("hidden_states must be bfloat16")
+    if activation not in _lib.ACT:
+        raise ValueError(f"Unsupported activation: {activation}")
+    if router.kind == "softmax":
+        kind = _lib.ROUTER_SOFTMAX_TOPK
+        if logits.dtype == torch.bfloat16:
+            dt = _lib.DTYPE_BF16
+        else:
+            logits, dt = logits.float(), _lib.DTYPE_F32
+    elif router.kind == "grouped_sigmoid":
+        kind, logits, dt = _lib.ROUTER_GROUPED_SIGMOID, logits.float(), _lib.DTYPE_F32
+    else:
+        raise ValueError(f"Unsupported router: {router.kind}")
+    bias = router.bias.float().contiguous() if router.bias is not None else None
+    logits = logits.contiguous()
+    _require_gpu(x, logits, bias)
+    m, e = logits.shape
+    if x.shape[0] != m:
+        raise ValueError("Number of tokens mismatch")
+    k = router.top_k
+    w = topk_w if topk_w is not None else torch.empty((m, k), dtype=torch.float32, device=x.device)
+    ids = topk_ids if topk_ids is not None else torch.empty((m, k), dtype=torch.int32, device=x.device)
+    _require_gpu(w, ids)
+    r = _lib.FtmoeRouter(kind, logits.data_ptr(), dt, e, int(router.renormalize), _ptr(bias), router.n_group,
+                         router.topk_group, float(router.scale))
+    b = bank.cstruct()
+    sb = shared.cstruct() if shared is not None else None
+    bp = ctypes.byref(b)
+    sp = ctypes.byref(sb) if sb is not None else None
+    nbytes = lib().ftmoe_experts_decode_workspace(m, k, bp, sp)
+    ws = _WS.get(x.device, nbytes)
+    y = out if out is not None else torch.empty_like(x)
+    if slot_for_id is not None:
+        if slot_for_id.dtype != torch.int32:
+            raise ValueError("slot_for_id must be int32")
+        if stats is not None and stats.dtype != torch.int64:
+            raise ValueError("stats must be int64[4]")
+        _require_gpu(slot_for_id, miss_mask, stats)
+    check(
+        lib().ftmoe_experts_decode_routed(_ptr(x), m, k, ctypes.byref(r), _ptr(w), _ptr(ids), _ptr(slot_for_id),
+                                          slot_for_id.numel() if slot_for_id is not None else 0,
+                                          _ptr(ids) if slot_for_id is not None else None, _ptr(miss_mask),
+                                          _ptr(stats), bp, sp, _lib.ACT[activation],
+                                          int(apply_router_weight_on_input), _ptr(y), _ptr(ws), ws.numel(),
+                                          _stream(x.device)),
+        "experts_decode_routed",
+    )
+    return y, w, ids
+
+
 def experts_prefill(x: torch.Tensor, topk_w: torch.Tensor, topk_ids: torch.Tensor, bank: ExpertBank,
                     shared: ExpertBank | None = None, activation: str = "silu",
                     out: torch.Tensor | None = None) -> torch.Tensor:

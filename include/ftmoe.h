@@ -195,6 +195,33 @@ int ftmoe_experts_decode_cached(const void* x, int M, int top_k, const float* to
                                 int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
                                 ftmoe_stream_t stream);
 
+/* A router for ftmoe_experts_decode_routed. */
+enum { FTMOE_ROUTER_SOFTMAX_TOPK = 0, FTMOE_ROUTER_GROUPED_SIGMOID = 1 };
+typedef struct ftmoe_router {
+  int kind;                    /* FTMOE_ROUTER_* */
+  const void* logits;          /* [M, num_experts]; float32, or bf16 for the softmax router */
+  int logits_dtype;            /* FTMOE_DTYPE_F32 / FTMOE_DTYPE_BF16 */
+  int num_experts;             /* E of the router (logit columns) */
+  int renormalize;
+  const float* bias;           /* grouped sigmoid: nullable [E] selection bias */
+  int n_group, topk_group;     /* grouped sigmoid */
+  float routed_scaling_factor; /* grouped sigmoid */
+} ftmoe_router;
+
+/* Decode from router logits in one call: the router (as
+ * ftmoe_route_softmax_topk or ftmoe_route_grouped_sigmoid, writing topk_w /
+ * topk_ids) followed by ftmoe_experts_decode, or, with slot_for_id (nullable),
+ * by ftmoe_experts_decode_cached; replaces MoELayer.forward's decode path
+ * (fused_topk + experts, layers/moe.py:166-194, moe/fused.py:16-85) and the
+ * DeepSeek-V3 block's _route + routed_forward (models/glm4_moe/moe.py:53-83).
+ * For decode-sized calls (at most 16 tokens and 64 routes) the router and the
+ * permutation share one launch.  Workspace as ftmoe_experts_decode. */
+int ftmoe_experts_decode_routed(const void* x, int M, int top_k, const ftmoe_router* router, float* topk_w,
+                                int32_t* topk_ids, const int32_t* slot_for_id, int num_experts, int32_t* slot_ids,
+                                uint8_t* miss_mask, int64_t* stats, const ftmoe_bank* bank, const ftmoe_bank* shared,
+                                int activation, int apply_router_weight_on_input, void* y, void* workspace,
+                                size_t workspace_bytes, ftmoe_stream_t stream);
+
 /* Prefill (grouped GEMM) expert computation for a precomputed routing;
  * replaces fused_experts_fp8_block (moe/fused_fp8_block.py:16-29 ->
  * kernel/triton/fp8_blockscale_moe.py:218-256, W8A8 with per-token per-128
