@@ -500,7 +500,7 @@ def main() -> int:
             torch.cuda.empty_cache()
         for fmt in ("fp8_block", "mxfp4"):
             log(f"[bench] sweep C5 prefill {fmt}")
-            sweep[f"c5_prefill_8192_{fmt}"] = run_prefill(fmt, 5, 1, gen, dev)
+            sweep[f"c5_prefill_8192_{fmt}"] = run_prefill(fmt, 10, 3, gen, dev)
         log("[bench] sweep C4 miss path (admission + PCIe gather of 8 experts per step)")
         sweep["c4_miss_fetch_8_experts"] = run_miss_fetch(gen, dev)
 
