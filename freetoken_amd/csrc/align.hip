@@ -8,13 +8,15 @@
 //   sentinel numel.  The reference ranks routes inside an expert with atomics;
 //   here the order is the canonical stable one: ascending flat route index.
 //
-// One workgroup of 16 waves does everything.  The routes are cut into 16
-// contiguous chunks, one per wave.  Pass 1 counts per (wave, expert) with LDS
-// atomics (order-free).  A scan over waves turns the counts into per-wave
-// bases, a scan over experts gives the padded region starts.  Pass 2 walks each
-// chunk in 64-route batches in order; a 64-key bitonic sort of
-// (expert << 6 | lane) inside the wave yields, for every route, its rank among
-// the equal-expert routes of the batch, so the final position is
+// Decode-sized calls (at most 64 routes, block size 1) take one wave
+// (align_wave.h).  Otherwise one workgroup of 16 waves does everything
+// (align_kernel; the multi-workgroup variant below for prefill).  The routes
+// are cut into 16 contiguous chunks, one per wave.  Pass 1 counts per (wave,
+// expert) with LDS atomics (order-free).  A scan over waves turns the counts
+// into per-wave bases, a scan over experts gives the padded region starts.
+// Pass 2 walks each chunk in 64-route batches in order; a 64-key bitonic sort
+// of (expert << 6 | lane) inside the wave yields, for every route, its rank
+// among the equal-expert routes of the batch, so the final position is
 // region_start[e] + wave_base[w][e] + rank -- no atomics, fully deterministic.
 #include "align_wave.h"
 #include "kernels.h"

@@ -35,14 +35,6 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
-// Monotone map float32 -> uint32 (IEEE order on non-NaN values); -0.0 is
-// folded onto +0.0 first so equal values get equal keys.
-__device__ __forceinline__ uint32_t order_key(float v) {
-  uint32_t u = __float_as_uint(v);
-  if (u == 0x80000000u) u = 0u;
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
 // Deterministic float32 exp/sigmoid.  Bit-identical to oracle/numerics.py
 // (exp_det / sigmoid_det): Cody-Waite reduction with ln2 split into a 16-bit
 // head (exact products) and a tail, degree-6 Taylor polynomial in Horner form,
