@@ -77,7 +77,8 @@ SIGNATURES = {
     "ftmoe_align_sizes": (None, [_i, _i, _i, _ip, _ip]),
     "ftmoe_align": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "ftmoe_slot_map": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp, _vp]),
-    "ftmoe_lru_ensure": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
+    "ftmoe_lru_ensure": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp,
+                              _vp]),
     "ftmoe_fetch_experts": (_i, [_fbp, _i, _vp, _vp, _vp, _i, _vp]),
     "ftmoe_act_quant_fp8": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "ftmoe_experts_decode_workspace": (_sz, [_i, _i, _bp, _bp]),
@@ -88,6 +89,12 @@ SIGNATURES = {
                                          _bp, _bp, _i, _i, _vp, _vp, _sz, _vp]),
     "ftmoe_experts_prefill_workspace": (_sz, [_i, _i, _bp, _bp]),
     "ftmoe_experts_prefill": (_i, [_vp, _i, _i, _vp, _vp, _bp, _bp, _i, _vp, _vp, _sz, _vp]),
+    "ftmoe_cpu_executor_create": (_vp, [_i]),
+    "ftmoe_cpu_executor_destroy": (None, [_vp]),
+    "ftmoe_cpu_executor_isa": (ctypes.c_char_p, [_vp]),
+    "ftmoe_cpu_experts": (_i, [_vp, _bp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "ftmoe_cpu_experts_submit": (_i, [_vp, _bp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, ctypes.POINTER(_vp)]),
+    "ftmoe_cpu_experts_wait": (_i, [_vp, _vp, _vp]),
     "ftmoe_stage_timing_begin": (_i, []),
     "ftmoe_stage_timing_end": (_i, [ctypes.POINTER(ctypes.c_double), _i, _ip, _ip]),
 }

@@ -185,6 +185,10 @@ PrefillLayout prefill_layout(void* ws, int M, int k, const ftmoe_bank* bank, con
 
 }  // namespace
 
+namespace ftmoe {
+int report_error(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace ftmoe
+
 extern "C" {
 
 const char* ftmoe_last_error(void) { return g_last_error.c_str(); }
@@ -260,15 +264,17 @@ int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_i
 
 int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layers, int num_experts,
                      int32_t* slot_for_id, int32_t* id_of_slot, int64_t* usage, int64_t* step, int cache_size,
-                     int64_t* recency, int max_fetch, int32_t* evict_slots, int32_t* src_indices, int capacity,
-                     int32_t* num_indices, int32_t* num_missing, int64_t* stats, ftmoe_stream_t stream) {
+                     int64_t* recency, int max_fetch, int fetch_frac_q16, int32_t* evict_slots,
+                     int32_t* src_indices, int capacity, int32_t* num_indices, int32_t* num_missing,
+                     int32_t* cpu_ids, int64_t* stats, ftmoe_stream_t stream) {
   if ((!expert_ids && numel) || !slot_for_id || !id_of_slot || !usage || !step || !num_indices || !num_missing ||
       ((!evict_slots || !src_indices) && capacity))
     return fail(FTMOE_ERR_INVALID, "lru_ensure: NULL pointer");
   if (numel < 0 || num_experts <= 0 || num_experts > 8192 || cache_size <= 0 || cache_size > 8192 ||
-      num_layers <= 0 || layer_id < 0 || layer_id >= num_layers || capacity < 0)
-    return fail(FTMOE_ERR_UNSUPPORTED, "lru_ensure: numel=%d E=%d S=%d layer=%d/%d capacity=%d", numel, num_experts,
-                cache_size, layer_id, num_layers, capacity);
+      num_layers <= 0 || layer_id < 0 || layer_id >= num_layers || capacity < 0 || fetch_frac_q16 < 0 ||
+      fetch_frac_q16 > (1 << 16))
+    return fail(FTMOE_ERR_UNSUPPORTED, "lru_ensure: numel=%d E=%d S=%d layer=%d/%d capacity=%d frac_q16=%d", numel,
+                num_experts, cache_size, layer_id, num_layers, capacity, fetch_frac_q16);
   ftmoe::LruArgs a{};
   a.ids = expert_ids;
   a.numel = numel;
@@ -288,6 +294,8 @@ int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layer
     while (a.sort_len < most) a.sort_len <<= 1;
   }
   a.max_fetch = max_fetch;
+  a.fetch_frac_q16 = fetch_frac_q16;
+  a.cpu_ids = cpu_ids;
   a.capacity = capacity;
   a.evict_slots = evict_slots;
   a.src_indices = src_indices;

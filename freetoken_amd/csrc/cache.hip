@@ -10,12 +10,18 @@
 //   step += 1; the distinct ids of the call are "seen"; every resident seen
 //   expert's slot gets usage = step; the missing seen experts are ordered by
 //   ascending id, or with a recency table by (most recently seen first, then
-//   ascending id); the first min(misses, max_fetch) of them take, one after
+//   ascending id); the first min(misses, cap) of them take, one after
 //   the other, the slot with the smallest (usage, slot) -- the previous owner
 //   (any layer) loses its mapping, the slot gets usage = step -- and are listed
 //   in (evict_slots, src_indices); the recency of every seen expert becomes
 //   step; finally every id is rewritten to its slot (-1 for unfetched misses
 //   and for ids outside [0, num_experts)).
+// The cap is max_fetch (< 0: none), or with a fetch fraction f (Q16, > 0) the
+// integer n in {floor(m f), floor(m f) + 1} with the smaller max(n (1 - f),
+// (m - n) f) -- PCIe fetch and CPU overflow balanced, lower n on a tie
+// (offload_kernels.py:160-164).  cpu_ids, when given, receives per route the
+// expert id of an unfetched miss and -1 elsewhere: the routes the CPU computes
+// in the hybrid decode (layers/moe.py:350-352).
 #include "kernels.h"
 
 namespace ftmoe {
@@ -134,6 +140,12 @@ __global__ void __launch_bounds__(kLruThreads) lru_ensure_kernel(LruArgs a) {
     __syncthreads();
   }
   int nfetch = a.max_fetch < 0 ? m : min(m, a.max_fetch);
+  if (a.fetch_frac_q16 > 0) {
+    const long long f = a.fetch_frac_q16, q = 1ll << 16;
+    const long long lo = (static_cast<long long>(m) * f) >> 16;
+    const long long c0 = max(lo * (q - f), (m - lo) * f), c1 = max((lo + 1) * (q - f), (m - lo - 1) * f);
+    nfetch = min(m, static_cast<int>(c0 <= c1 ? lo : lo + 1));
+  }
   nfetch = min(nfetch, a.capacity);
   if (tid == 0) {
     a.num_missing[0] = m;
@@ -171,7 +183,9 @@ __global__ void __launch_bounds__(kLruThreads) lru_ensure_kernel(LruArgs a) {
     const int e = a.ids[i];
     const bool valid = e >= 0 && e < E;
     if (valid && seen[e] == 2) ++missed;
-    a.ids[i] = valid ? a.slot_for_id[base + e] : -1;
+    const int s = valid ? a.slot_for_id[base + e] : -1;
+    a.ids[i] = s;
+    if (a.cpu_ids) a.cpu_ids[i] = valid && s < 0 ? e : -1;
   }
   if (tid == 0) a.step[0] = step;
   if (a.stats) {

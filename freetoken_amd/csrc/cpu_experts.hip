@@ -1,0 +1,451 @@
+// Host-side expert executor of the hybrid decode: the routes whose experts are
+// neither resident nor fetched this call are computed on the CPU from the
+// pinned host banks while the GPU computes the others (reference: the hybrid
+// backend, layers/moe.py:325-372, with its CPU pool, moe/cpu_executor.py).
+//
+// Math per route (the decode rounding points of the GPU path): g = W_gate x,
+// u = W_up x in fp32 (FP8: per 128-deep K block partial times the block scale;
+// MXFP4: e2m1 * 2^(e8m0 - 127)), rounded to bf16; act = bf16(silu(g) * u);
+// d = W_down act the same way, times the router weight, rounded to bf16; the
+// token's output is bf16 of the fp32 sum of its CPU routes in route order.
+//
+// Work: pass 1 over (route, 32 rows of I), pass 2 over (token, 32 rows of H),
+// grabbed from an atomic counter by a persistent pool; a driver thread runs
+// the passes of one job after the other.  The stream sees the job through two
+// host-function nodes: "submit" hands the job to the driver and returns at
+// once, "wait" blocks the stream until the job is done -- so the CPU work
+// overlaps whatever the stream runs between them (the GPU's share of the
+// layer), and both nodes replay in a captured graph.
+#include <hip/hip_runtime.h>
+#include <immintrin.h>
+#include <sched.h>
+
+#include <atomic>
+#include <cmath>
+#include <condition_variable>
+#include <cstdint>
+#include <cstring>
+#include <deque>
+#include <functional>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include "ftmoe.h"
+#include "kernels.h"
+
+namespace ftmoe_cpu {
+
+using bf16 = uint16_t;
+
+inline float b2f(bf16 v) {
+  const uint32_t u = static_cast<uint32_t>(v) << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+inline bf16 f2b(float f) {  // round to nearest even
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<bf16>(u >> 16);
+}
+
+inline float rb(float f) { return b2f(f2b(f)); }
+
+// e4m3 (bias 7, no infinities, S.1111.111 NaN) and e2m1 value tables
+struct Tables {
+  float e4m3[256];
+  float e2m1[16];
+  Tables() {
+    for (int c = 0; c < 256; ++c) {
+      const int s = c >> 7, e = (c >> 3) & 15, m = c & 7;
+      float v = e == 0 ? std::ldexp(static_cast<float>(m), -9) : std::ldexp(1.0f + m / 8.0f, e - 7);
+      if (e == 15 && m == 7) v = NAN;
+      e4m3[c] = s ? -v : v;
+    }
+    const float p[8] = {0.f, .5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+    for (int c = 0; c < 16; ++c) e2m1[c] = c & 8 ? -p[c & 7] : p[c & 7];
+  }
+};
+const Tables kT;
+
+// ---------------------------------------------------------------- row dots
+// dot of weight row n (K values) with x (fp32, K), in the format's
+// accumulation order: bf16 one pass; FP8 per 128-block partial * scale;
+// MXFP4 per 32-block with its power-of-two scale.
+struct Mat {
+  int format;
+  int K;
+  const uint8_t* w;  // [N, K * bytes per value]
+  const void* s;     // FP8 float [N/128, K/128]; MXFP4 uint8 [N, K/32]
+};
+
+float dot_scalar(const Mat& m, int n, const float* x) {
+  if (m.format == FTMOE_FMT_BF16) {
+    const bf16* w = reinterpret_cast<const bf16*>(m.w) + static_cast<size_t>(n) * m.K;
+    float acc = 0.f;
+    for (int k = 0; k < m.K; ++k) acc += b2f(w[k]) * x[k];
+    return acc;
+  }
+  if (m.format == FTMOE_FMT_FP8_B128) {
+    const uint8_t* w = m.w + static_cast<size_t>(n) * m.K;
+    const float* s = static_cast<const float*>(m.s) + static_cast<size_t>(n / 128) * (m.K / 128);
+    float acc = 0.f;
+    for (int kb = 0; kb < m.K / 128; ++kb) {
+      float part = 0.f;
+      for (int k = 0; k < 128; ++k) part += kT.e4m3[w[kb * 128 + k]] * x[kb * 128 + k];
+      acc += part * s[kb];
+    }
+    return acc;
+  }
+  const uint8_t* w = m.w + static_cast<size_t>(n) * (m.K / 2);
+  const uint8_t* s = static_cast<const uint8_t*>(m.s) + static_cast<size_t>(n) * (m.K / 32);
+  float acc = 0.f;
+  for (int kb = 0; kb < m.K / 32; ++kb) {
+    float part = 0.f;
+    for (int k = 0; k < 32; k += 2) {
+      const uint8_t b = w[kb * 16 + k / 2];
+      part += kT.e2m1[b & 15] * x[kb * 32 + k] + kT.e2m1[b >> 4] * x[kb * 32 + k + 1];
+    }
+    acc += part * std::ldexp(1.0f, static_cast<int>(s[kb]) - 127);
+  }
+  return acc;
+}
+
+__attribute__((target("avx512f"))) float dot_avx512(const Mat& m, int n, const float* x) {
+  if (m.format == FTMOE_FMT_BF16) {
+    const bf16* w = reinterpret_cast<const bf16*>(m.w) + static_cast<size_t>(n) * m.K;
+    __m512 acc = _mm512_setzero_ps();
+    for (int k = 0; k < m.K; k += 16) {
+      const __m512i wi = _mm512_slli_epi32(_mm512_cvtepu16_epi32(_mm256_loadu_si256(reinterpret_cast<const __m256i*>(w + k))), 16);
+      acc = _mm512_fmadd_ps(_mm512_castsi512_ps(wi), _mm512_loadu_ps(x + k), acc);
+    }
+    return _mm512_reduce_add_ps(acc);
+  }
+  if (m.format == FTMOE_FMT_FP8_B128) {
+    const uint8_t* w = m.w + static_cast<size_t>(n) * m.K;
+    const float* s = static_cast<const float*>(m.s) + static_cast<size_t>(n / 128) * (m.K / 128);
+    __m512 acc = _mm512_setzero_ps();
+    for (int kb = 0; kb < m.K / 128; ++kb) {
+      __m512 part = _mm512_setzero_ps();
+      for (int k = 0; k < 128; k += 16) {
+        const __m512i idx = _mm512_cvtepu8_epi32(_mm_loadu_si128(reinterpret_cast<const __m128i*>(w + kb * 128 + k)));
+        part = _mm512_fmadd_ps(_mm512_i32gather_ps(idx, kT.e4m3, 4), _mm512_loadu_ps(x + kb * 128 + k), part);
+      }
+      acc = _mm512_fmadd_ps(part, _mm512_set1_ps(s[kb]), acc);
+    }
+    return _mm512_reduce_add_ps(acc);
+  }
+  const uint8_t* w = m.w + static_cast<size_t>(n) * (m.K / 2);
+  const uint8_t* s = static_cast<const uint8_t*>(m.s) + static_cast<size_t>(n) * (m.K / 32);
+  const __m512 lut = _mm512_loadu_ps(kT.e2m1);
+  __m512 acc = _mm512_setzero_ps();
+  for (int kb = 0; kb < m.K / 32; ++kb) {
+    // 16 bytes = 32 values; even k in the low nibble
+    const __m512i b = _mm512_cvtepu8_epi32(_mm_loadu_si128(reinterpret_cast<const __m128i*>(w + kb * 16)));
+    const __m512 lo = _mm512_permutexvar_ps(_mm512_and_si512(b, _mm512_set1_epi32(15)), lut);
+    const __m512 hi = _mm512_permutexvar_ps(_mm512_srli_epi32(b, 4), lut);
+    // x pairs: x[2j] with lo[j], x[2j+1] with hi[j]
+    const __m512i ev = _mm512_setr_epi32(0, 2, 4, 6, 8, 10, 12, 14, 16, 18, 20, 22, 24, 26, 28, 30);
+    const __m512i od = _mm512_add_epi32(ev, _mm512_set1_epi32(1));
+    const __m512 x0 = _mm512_loadu_ps(x + kb * 32), x1 = _mm512_loadu_ps(x + kb * 32 + 16);
+    const __m512 xe = _mm512_permutex2var_ps(x0, ev, x1), xo = _mm512_permutex2var_ps(x0, od, x1);
+    const __m512 part = _mm512_fmadd_ps(hi, xo, _mm512_mul_ps(lo, xe));
+    acc = _mm512_fmadd_ps(part, _mm512_set1_ps(std::ldexp(1.0f, static_cast<int>(s[kb]) - 127)), acc);
+  }
+  return _mm512_reduce_add_ps(acc);
+}
+
+using dot_fn = float (*)(const Mat&, int, const float*);
+
+float silu(float g) { return g / (1.0f + std::exp(-g)); }
+float gelu(float g) { return 0.5f * g * (1.0f + std::erf(g * 0.70710678118654752f)); }
+float gelu_tanh(float g) {
+  return 0.5f * g * (1.0f + std::tanh(0.7978845608028654f * (g + 0.044715f * g * g * g)));
+}
+
+class Executor;
+
+struct Job {
+  Executor* ex;
+  ftmoe_bank bank;  // host pointers
+  const bf16* x;    // [M, H]
+  const float* w;   // [M, k]
+  const int32_t* ids;  // [M, k] bank rows; < 0 or >= num_rows skipped
+  int M, k, activation;
+  bf16* y;          // [M, H]
+  bool permanent = false;
+  bool done = true;
+};
+
+class Executor {
+ public:
+  explicit Executor(int threads) : nthreads_(threads < 1 ? 1 : threads) {
+    dot_ = __builtin_cpu_supports("avx512f") ? dot_avx512 : dot_scalar;
+    for (int t = 0; t < nthreads_; ++t) workers_.emplace_back([this] { worker(); });
+    driver_ = std::thread([this] { drive(); });
+  }
+  ~Executor() {
+    {
+      std::lock_guard<std::mutex> g(m_);
+      stop_ = true;
+    }
+    cv_job_.notify_all();
+    cv_work_.notify_all();
+    driver_.join();
+    for (auto& t : workers_) t.join();
+    for (Job* j : jobs_) delete j;
+  }
+  const char* isa() const { return dot_ == dot_avx512 ? "avx512f" : "scalar"; }
+
+  Job* new_job(bool permanent) {
+    std::lock_guard<std::mutex> g(m_);
+    Job* j = nullptr;
+    if (!permanent && !free_.empty()) {
+      j = free_.back();
+      free_.pop_back();
+    } else {
+      j = new Job();
+      jobs_.push_back(j);
+    }
+    j->ex = this;
+    j->permanent = permanent;
+    return j;
+  }
+  // host node: queue the job for the driver
+  void start(Job* j) {
+    {
+      std::lock_guard<std::mutex> g(m_);
+      j->done = false;
+      queue_.push_back(j);
+    }
+    cv_job_.notify_all();
+  }
+  // host node: block until the job is done; recycle it unless a graph holds it
+  void finish(Job* j) {
+    std::unique_lock<std::mutex> g(m_);
+    cv_done_.wait(g, [j] { return j->done; });
+    if (!j->permanent) free_.push_back(j);
+  }
+  // synchronous run (tests, callers without a stream)
+  void run(Job* j) {
+    start(j);
+    std::unique_lock<std::mutex> g(m_);
+    cv_done_.wait(g, [j] { return j->done; });
+  }
+
+ private:
+  void parallel(int units, const std::function<void(int)>& fn) {
+    {
+      std::lock_guard<std::mutex> g(m_);
+      fn_ = &fn;
+      units_ = units;
+      next_.store(0);
+      left_ = nthreads_;
+      ++gen_;
+    }
+    cv_work_.notify_all();
+    std::unique_lock<std::mutex> g(m_);
+    cv_pass_.wait(g, [this] { return left_ == 0; });
+    fn_ = nullptr;
+  }
+  void worker() {
+    uint64_t seen = 0;
+    for (;;) {
+      const std::function<void(int)>* fn;
+      int units;
+      {
+        std::unique_lock<std::mutex> g(m_);
+        cv_work_.wait(g, [&] { return stop_ || gen_ != seen; });
+        if (stop_) return;
+        seen = gen_;
+        fn = fn_;
+        units = units_;
+      }
+      for (int u = next_.fetch_add(1); u < units; u = next_.fetch_add(1)) (*fn)(u);
+      std::lock_guard<std::mutex> g(m_);
+      if (--left_ == 0) cv_pass_.notify_all();
+    }
+  }
+  void drive() {
+    for (;;) {
+      Job* j;
+      {
+        std::unique_lock<std::mutex> g(m_);
+        cv_job_.wait(g, [this] { return stop_ || !queue_.empty(); });
+        if (stop_) return;
+        j = queue_.front();
+        queue_.pop_front();
+      }
+      compute(*j);
+      {
+        std::lock_guard<std::mutex> g(m_);
+        j->done = true;
+      }
+      cv_done_.notify_all();
+    }
+  }
+  void compute(const Job& j) {
+    const int H = j.bank.hidden, I = j.bank.inter, R = j.M * j.k;
+    const Mat gu{j.bank.format, H, static_cast<const uint8_t*>(j.bank.gate_up), j.bank.gate_up_scale};
+    const Mat dn{j.bank.format, I, static_cast<const uint8_t*>(j.bank.down), j.bank.down_scale};
+    const size_t gu_rows = static_cast<size_t>(2) * I, dn_rows = H;
+    const auto rowmat = [&](const Mat& m, size_t rows, int e) {
+      Mat r = m;
+      const size_t vb = m.format == FTMOE_FMT_BF16 ? 2 : 1;  // bytes per value (MXFP4: per pair)
+      const size_t row_bytes = m.format == FTMOE_FMT_MXFP4 ? m.K / 2 : m.K * vb;
+      r.w = m.w + static_cast<size_t>(e) * rows * row_bytes;
+      if (m.format == FTMOE_FMT_FP8_B128)
+        r.s = static_cast<const float*>(m.s) + static_cast<size_t>(e) * (rows / 128) * (m.K / 128);
+      else if (m.format == FTMOE_FMT_MXFP4)
+        r.s = static_cast<const uint8_t*>(m.s) + static_cast<size_t>(e) * rows * (m.K / 32);
+      return r;
+    };
+    xf_.assign(static_cast<size_t>(j.M) * H, 0.f);
+    for (size_t i = 0; i < xf_.size(); ++i) xf_[i] = b2f(j.x[i]);
+    act_.assign(static_cast<size_t>(R) * I, 0.f);
+    const auto valid = [&](int r) { return j.ids[r] >= 0 && j.ids[r] < j.bank.num_rows; };
+    constexpr int kTile = 32;
+    // pass 1: gate/up rows of (route, 32 rows of I)
+    const int tiles1 = I / kTile;
+    parallel(R * tiles1, [&](int u) {
+      const int r = u / tiles1, i0 = (u % tiles1) * kTile;
+      if (!valid(r)) return;
+      const Mat m = rowmat(gu, gu_rows, j.ids[r]);
+      const float* x = xf_.data() + static_cast<size_t>(r / j.k) * H;
+      for (int i = i0; i < i0 + kTile; ++i) {
+        const float g = rb(dot_(m, i, x)), v = rb(dot_(m, I + i, x));
+        const float a = j.activation == FTMOE_ACT_SILU ? silu(g) : j.activation == FTMOE_ACT_GELU ? gelu(g)
+                                                                                                : gelu_tanh(g);
+        act_[static_cast<size_t>(r) * I + i] = rb(a * v);
+      }
+    });
+    // pass 2: down rows of (token, 32 rows of H), routes summed in order
+    const int tiles2 = H / kTile;
+    parallel(j.M * tiles2, [&](int u) {
+      const int t = u / tiles2, h0 = (u % tiles2) * kTile;
+      for (int h = h0; h < h0 + kTile; ++h) {
+        float s = 0.f;
+        for (int q = 0; q < j.k; ++q) {
+          const int r = t * j.k + q;
+          if (!valid(r)) continue;
+          const Mat m = rowmat(dn, dn_rows, j.ids[r]);
+          s += rb(dot_(m, h, act_.data() + static_cast<size_t>(r) * I) * j.w[r]);
+        }
+        j.y[static_cast<size_t>(t) * H + h] = f2b(s);
+      }
+    });
+  }
+
+  int nthreads_;
+  dot_fn dot_;
+  std::vector<std::thread> workers_;
+  std::thread driver_;
+  std::mutex m_;
+  std::condition_variable cv_job_, cv_done_, cv_work_, cv_pass_;
+  std::deque<Job*> queue_;
+  std::vector<Job*> jobs_, free_;
+  const std::function<void(int)>* fn_ = nullptr;
+  int units_ = 0, left_ = 0;
+  uint64_t gen_ = 0;
+  std::atomic<int> next_{0};
+  bool stop_ = false;
+  std::vector<float> xf_, act_;
+};
+
+void host_start(void* p) {
+  Job* j = static_cast<Job*>(p);
+  j->ex->start(j);
+}
+void host_finish(void* p) {
+  Job* j = static_cast<Job*>(p);
+  j->ex->finish(j);
+}
+
+int check_job(const ftmoe_bank* b, const void* x, const float* w, const int32_t* ids, int M, int k, int act,
+              const void* y) {
+  if (!b || !x || !w || !ids || !y || !b->gate_up || !b->down)
+    return ftmoe::report_error(FTMOE_ERR_INVALID, "cpu_experts: NULL pointer");
+  if (b->format < FTMOE_FMT_BF16 || b->format > FTMOE_FMT_MXFP4 || b->hidden <= 0 || b->inter <= 0 ||
+      b->hidden % 128 || b->inter % 128 || b->num_rows <= 0 ||
+      (b->format != FTMOE_FMT_BF16 && (!b->gate_up_scale || !b->down_scale)))
+    return ftmoe::report_error(FTMOE_ERR_UNSUPPORTED, "cpu_experts: bank format/shape");
+  if (M <= 0 || k <= 0 || act < FTMOE_ACT_SILU || act > FTMOE_ACT_GELU_TANH)
+    return ftmoe::report_error(FTMOE_ERR_UNSUPPORTED, "cpu_experts: M/k/activation");
+  return FTMOE_OK;
+}
+
+void fill(Job* j, const ftmoe_bank* b, const void* x, const float* w, const int32_t* ids, int M, int k, int act,
+          void* y) {
+  j->bank = *b;
+  j->x = static_cast<const bf16*>(x);
+  j->w = w;
+  j->ids = ids;
+  j->M = M;
+  j->k = k;
+  j->activation = act;
+  j->y = static_cast<bf16*>(y);
+}
+
+}  // namespace ftmoe_cpu
+
+extern "C" {
+
+ftmoe_cpu_executor* ftmoe_cpu_executor_create(int threads) {
+  if (threads <= 0) {  // the CPUs this process may run on, not the machine's count
+    cpu_set_t set;
+    threads = sched_getaffinity(0, sizeof(set), &set) == 0 ? CPU_COUNT(&set)
+                                                             : static_cast<int>(std::thread::hardware_concurrency());
+  }
+  return reinterpret_cast<ftmoe_cpu_executor*>(new ftmoe_cpu::Executor(threads));
+}
+
+void ftmoe_cpu_executor_destroy(ftmoe_cpu_executor* ex) { delete reinterpret_cast<ftmoe_cpu::Executor*>(ex); }
+
+const char* ftmoe_cpu_executor_isa(ftmoe_cpu_executor* ex) {
+  return ex ? reinterpret_cast<ftmoe_cpu::Executor*>(ex)->isa() : "";
+}
+
+int ftmoe_cpu_experts(ftmoe_cpu_executor* ex, const ftmoe_bank* bank, const void* x, const float* w,
+                      const int32_t* ids, int M, int k, int activation, void* y) {
+  if (!ex) return ftmoe::report_error(FTMOE_ERR_INVALID, "cpu_experts: NULL executor");
+  const int rc = ftmoe_cpu::check_job(bank, x, w, ids, M, k, activation, y);
+  if (rc) return rc;
+  auto* e = reinterpret_cast<ftmoe_cpu::Executor*>(ex);
+  ftmoe_cpu::Job* j = e->new_job(false);
+  ftmoe_cpu::fill(j, bank, x, w, ids, M, k, activation, y);
+  e->run(j);
+  e->finish(j);
+  return FTMOE_OK;
+}
+
+int ftmoe_cpu_experts_submit(ftmoe_cpu_executor* ex, const ftmoe_bank* bank, const void* x, const float* w,
+                             const int32_t* ids, int M, int k, int activation, void* y, ftmoe_stream_t stream,
+                             void** job) {
+  if (!ex || !job) return ftmoe::report_error(FTMOE_ERR_INVALID, "cpu_experts_submit: NULL executor or job");
+  const int rc = ftmoe_cpu::check_job(bank, x, w, ids, M, k, activation, y);
+  if (rc) return rc;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (stream && hipStreamIsCapturing(stream, &cs) != hipSuccess)
+    return ftmoe::report_error(FTMOE_ERR_HIP, "cpu_experts_submit: stream query failed");
+  auto* e = reinterpret_cast<ftmoe_cpu::Executor*>(ex);
+  // a job captured into a graph is replayed with the same record: never recycled
+  ftmoe_cpu::Job* j = e->new_job(cs != hipStreamCaptureStatusNone);
+  ftmoe_cpu::fill(j, bank, x, w, ids, M, k, activation, y);
+  if (hipLaunchHostFunc(stream, ftmoe_cpu::host_start, j) != hipSuccess)
+    return ftmoe::report_error(FTMOE_ERR_HIP, "cpu_experts_submit: hipLaunchHostFunc failed");
+  *job = j;
+  return FTMOE_OK;
+}
+
+int ftmoe_cpu_experts_wait(ftmoe_cpu_executor* ex, void* job, ftmoe_stream_t stream) {
+  if (!ex || !job) return ftmoe::report_error(FTMOE_ERR_INVALID, "cpu_experts_wait: NULL executor or job");
+  if (hipLaunchHostFunc(stream, ftmoe_cpu::host_finish, job) != hipSuccess)
+    return ftmoe::report_error(FTMOE_ERR_HIP, "cpu_experts_wait: hipLaunchHostFunc failed");
+  return FTMOE_OK;
+}
+
+}  // extern "C"

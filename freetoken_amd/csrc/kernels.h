@@ -145,11 +145,13 @@ struct LruArgs {
   int64_t* recency;       // nullable [num_experts] of this layer: order misses by recency
   int sort_len;           // power of two >= the largest miss count (recency order), else 0
   int max_fetch;          // < 0: every miss
+  int fetch_frac_q16;     // > 0: fetch the bandwidth-matched share of the misses instead of max_fetch
   int capacity;           // entries of evict_slots / src_indices
   int32_t* evict_slots;   // [capacity]
   int32_t* src_indices;   // [capacity] layer-local expert rows
   int32_t* num_indices;   // [1] entries admitted
   int32_t* num_missing;   // [1] distinct missing experts before the cap
+  int32_t* cpu_ids;       // nullable [numel]: the expert id of an unfetched miss, else -1
   long long* stats;       // nullable [4] accumulated: active, missing, calls, missed routes
 };
 hipError_t launch_lru_ensure(const LruArgs& a, hipStream_t stream);
@@ -170,6 +172,9 @@ struct FetchArgs {
 };
 hipError_t launch_fetch_experts(const FetchArgs& a, int max_entries, hipStream_t stream);
 int fetch_chunks(uint64_t row_bytes);
+
+// Records the message of a failed C-ABI call (ftmoe_last_error) and returns code.
+int report_error(int code, const char* msg);
 hipError_t launch_combine(const uint16_t* ic3, const int32_t* ids, int num_rows, const uint16_t* sh_out, int M,
                           int k, int H, uint16_t* y, hipStream_t stream);
 

@@ -22,6 +22,7 @@ from .. import ops
 from ..core import get_global_ctx, has_global_ctx
 from ..moe import is_offload_moe_backend
 from ..moe.fused import GROUPED_MIN_ROUTES, fused_experts_impl, fused_topk
+from ..moe.offload_cache import bank_from_views
 
 if TYPE_CHECKING:
     from ..moe.offload_cache import ExpertSlotCache
@@ -166,13 +167,7 @@ class OffloadMoELayer(MoELayer):
         self.offload_cache: ExpertSlotCache | None = None
 
     def _views_bank(self, views) -> ops.ExpertBank:
-        fmt = self.offload_cache.quant_format
-        if fmt == "bf16":
-            gate_up, down = views
-            return ops.ExpertBank("bf16", gate_up, down)
-        gate_up, gate_up_scale, down, down_scale = views
-        return ops.ExpertBank("fp8_block" if fmt == "fp8_block" else "mxfp4", gate_up, down, gate_up_scale,
-                              down_scale)
+        return bank_from_views(self.offload_cache.quant_format, views)
 
     def forward(self, hidden_states: torch.Tensor, router_logits: torch.Tensor | None = None):
         topk_weights, topk_ids = fused_topk(hidden_states, router_logits, self.top_k, self.renormalize)
@@ -189,6 +184,10 @@ class OffloadMoELayer(MoELayer):
     def _decode_routed(self, hidden_states, topk_weights, topk_ids) -> torch.Tensor:
         cache = self.offload_cache
         assert cache is not None
+        if cache.is_cpu_layer(self.layer_id):
+            return self._decode_cpu(cache, hidden_states, topk_weights, topk_ids)
+        if cache.decode_target == "hybrid":
+            return self._decode_hybrid(cache, hidden_states, topk_weights, topk_ids)
         if cache.sources:
             # on-demand load (layers/moe.py:288-320): admit the missing experts,
             # gather them over PCIe, then compute on the slots
@@ -202,6 +201,36 @@ class OffloadMoELayer(MoELayer):
         return ops.experts_decode(hidden_states, topk_weights, topk_ids, self._views_bank(cache.bank_views()),
                                   shared=self.shared_expert, activation=self.activation, slot_for_id=table,
                                   stats=stats)
+
+    def _decode_hybrid(self, cache, hidden_states, topk_weights, topk_ids) -> torch.Tensor:
+        """Hybrid decode (reference ``:325-372``): the admission fetches at most
+        the cache's cap of this step's misses and lists the others, by expert
+        id, for the CPU; the CPU job starts before the PCIe gather and the GPU
+        experts, and the two partials are added at the end.  Each route is
+        computed once: the GPU skips the -1 slots, the CPU the -1 ids."""
+        dec = cache.cpu_executor
+        assert dec is not None, "hybrid decode needs cache.set_cpu_executor"
+        cpu_ids = torch.empty_like(topk_ids)
+        cache.ensure_experts_hybrid(self.layer_id, topk_ids, cpu_ids=cpu_ids)
+        pending = dec.decode_submit(self.layer_id, hidden_states, topk_weights, cpu_ids)
+        cache.copy_missing()
+        gpu = ops.experts_decode(hidden_states, topk_weights, topk_ids, self._views_bank(cache.bank_views()),
+                                 shared=self.shared_expert, activation=self.activation)
+        return gpu + dec.decode_sync(pending)
+
+    def _decode_cpu(self, cache, hidden_states, topk_weights, topk_ids) -> torch.Tensor:
+        """A layer decoded on the CPU executor from its host banks (reference
+        ``:307-310``); the slot cache is not touched.  A shared expert runs on
+        the GPU meanwhile."""
+        dec = cache.cpu_executor
+        assert dec is not None, "CPU layers need cache.set_cpu_executor"
+        pending = dec.decode_submit(self.layer_id, hidden_states, topk_weights, topk_ids)
+        if self.shared_expert is None:
+            return dec.decode_sync(pending)
+        shared = ops.experts_decode(hidden_states, topk_weights, torch.full_like(topk_ids, -1),
+                                    self._views_bank(cache.bank_views()), shared=self.shared_expert,
+                                    activation=self.activation)
+        return shared + dec.decode_sync(pending)
 
     def _prefill_routed(self, hidden_states, topk_weights, topk_ids) -> torch.Tensor:
         cache = self.offload_cache

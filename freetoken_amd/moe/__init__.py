@@ -2,8 +2,9 @@
 
 ``"fused"`` (and its alias ``"mi355x"``) is the resident-expert backend backed
 by the gfx950 kernels; ``"offload"`` marks the expert-cache path whose work is
-done by ``OffloadMoELayer`` (``moe/offload.py`` of the reference).  The CPU and
-hybrid executors of the reference are not part of this build.
+done by ``OffloadMoELayer`` (``moe/offload.py`` of the reference); ``"cpu"``
+and ``"hybrid"`` are the offload family's decode placements whose CPU share
+runs on the host executor (``moe/cpu_offload.py`` of the reference).
 """
 
 from __future__ import annotations
@@ -40,7 +41,7 @@ class Registry:
 
 SUPPORTED_MOE_BACKENDS = Registry("MoE Backend")
 
-OFFLOAD_MOE_BACKENDS = frozenset({"offload"})
+OFFLOAD_MOE_BACKENDS = frozenset({"offload", "cpu", "hybrid"})
 
 
 def is_offload_moe_backend(backend: str) -> bool:
@@ -66,6 +67,20 @@ def create_offload_moe_backend():
     from .offload import OffloadMoeBackend
 
     return OffloadMoeBackend()
+
+
+@SUPPORTED_MOE_BACKENDS.register("cpu")
+def create_cpu_moe_backend():
+    from .offload import CpuOffloadMoeBackend
+
+    return CpuOffloadMoeBackend()
+
+
+@SUPPORTED_MOE_BACKENDS.register("hybrid")
+def create_hybrid_moe_backend():
+    from .offload import HybridMoeBackend
+
+    return HybridMoeBackend()
 
 
 def create_moe_backend(backend: str) -> BaseMoeBackend:

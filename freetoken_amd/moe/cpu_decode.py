@@ -1,0 +1,80 @@
+"""CPU share of the MoE decode (reference ``moe/cpu_executor.py:523-600``).
+
+``CpuMoeDecoder`` owns the host executor (``ftmoe_cpu_experts_*``), one set
+of pinned IO buffers per decode batch size and the host banks of every layer
+(the cache's pinned sources, read in place).  ``decode_submit`` copies the
+step's activations and routing to the pinned buffers and enqueues the CPU job
+on the current stream; ``decode_sync`` makes the stream wait for it and
+copies the result back.  Everything is stream-ordered, so GPU work enqueued
+between the two runs while the CPU computes, and the whole sequence replays
+in a captured graph (the first call of a batch size must be eager: it
+allocates that size's pinned buffers).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import ops
+from .offload_cache import ExpertSlotCache, bank_from_views
+
+
+class CpuMoeDecoder:
+    def __init__(self, cache: ExpertSlotCache, top_k: int, threads: int = 0, activation: str = "silu"):
+        assert cache.sources, "the CPU share reads the cache's host sources: set_bank_sources first"
+        self.cache = cache
+        self.top_k = top_k
+        self.activation = activation
+        self.executor = ops.CpuExecutor(threads)
+        self._io: dict[int, dict[str, torch.Tensor]] = {}
+        self._banks: dict[int, ops.ExpertBank] = {}
+
+    def host_bank(self, layer_id: int) -> ops.ExpertBank:
+        bank = self._banks.get(layer_id)
+        if bank is None:
+            bank = bank_from_views(self.cache.quant_format, self.cache.host_bank_tensors(layer_id))
+            self._banks[layer_id] = bank
+        return bank
+
+    def _io_for(self, bs: int, hidden: int) -> dict[str, torch.Tensor]:
+        io = self._io.get(bs)
+        if io is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(f"no pinned IO buffers for decode batch {bs}: run one eager call before capture")
+            k = self.top_k
+            io = {
+                "x": torch.empty((bs, hidden), dtype=torch.bfloat16, pin_memory=True),
+                "ids": torch.empty((bs, k), dtype=torch.int32, pin_memory=True),
+                "w": torch.empty((bs, k), dtype=torch.float32, pin_memory=True),
+                "y": torch.empty((bs, hidden), dtype=torch.bfloat16, pin_memory=True),
+            }
+            self._io[bs] = io
+        return io
+
+    def decode_submit(self, layer_id: int, hidden_states: torch.Tensor, topk_weights: torch.Tensor,
+                      topk_ids: torch.Tensor) -> tuple:
+        """Ships the step to pinned memory and starts the CPU job; routes with
+        id -1 are skipped by the CPU.  Returns the handle for ``decode_sync``."""
+        bs, hidden = hidden_states.shape
+        if topk_ids.shape != (bs, self.top_k):
+            raise ValueError(f"topk_ids {tuple(topk_ids.shape)} != ({bs}, {self.top_k})")
+        io = self._io_for(bs, hidden)
+        io["x"].copy_(hidden_states, non_blocking=True)
+        io["ids"].copy_(topk_ids, non_blocking=True)
+        io["w"].copy_(topk_weights, non_blocking=True)
+        job = self.executor.submit(self.host_bank(layer_id), io["x"], io["w"], io["ids"], io["y"],
+                                   activation=self.activation, device=hidden_states.device)
+        out = torch.empty_like(hidden_states)
+        return io, job, out
+
+    def decode_sync(self, pending: tuple) -> torch.Tensor:
+        io, job, out = pending
+        self.executor.wait(job, device=out.device)
+        out.copy_(io["y"], non_blocking=True)
+        return out
+
+    def decode(self, layer_id: int, hidden_states, topk_weights, topk_ids) -> torch.Tensor:
+        return self.decode_sync(self.decode_submit(layer_id, hidden_states, topk_weights, topk_ids))
+
+    def close(self) -> None:
+        self.executor.close()

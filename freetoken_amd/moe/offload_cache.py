@@ -11,9 +11,11 @@ also admits the missing experts into least-recently-used slots
 (``lru_ensure``, ``moe/offload_kernels.py:19-40``) and ``copy_missing``
 gathers their rows over PCIe (``:968-1010``); without sources, misses are
 reported (slot -1, skipped by the expert kernels).  ``ensure_experts_hybrid``
-is the capped admission (``offload_kernels.py:43-60``).  Everything runs on
-the device without host synchronisation; miss statistics accumulate in the
-reference's layout (``:205-229,861-934``).
+is the capped admission (``offload_kernels.py:43-60``) of the hybrid decode,
+whose unfetched misses a CPU executor computes (``decode_target``
+"hybrid"; "cpu" layers decode on the CPU entirely, ``:117-150,513-526``).
+Everything runs on the device without host synchronisation; miss statistics
+accumulate in the reference's layout (``:205-229,861-934``).
 """
 
 from __future__ import annotations
@@ -28,10 +30,32 @@ STAT_ACTIVE, STAT_MISS, STAT_CALLS, STAT_MISSED_ROUTES = range(4)
 N_STATS = 4
 
 
+def bank_from_views(quant_format: str, views) -> ops.ExpertBank:
+    """An ``ExpertBank`` over bank tensors in registration order: (gate_up,
+    down) for bf16, (gate_up, gate_up_scale, down, down_scale) otherwise."""
+    if quant_format == "bf16":
+        gate_up, down = views
+        return ops.ExpertBank("bf16", gate_up, down)
+    gate_up, gate_up_scale, down, down_scale = views
+    return ops.ExpertBank("fp8_block" if quant_format == "fp8_block" else "mxfp4", gate_up, down, gate_up_scale,
+                          down_scale)
+
+
 class ExpertSlotCache:
     def __init__(self, num_layers: int, num_experts: int, cache_size: int, quant_format: str,
-                 device: torch.device | str = "cuda"):
+                 device: torch.device | str = "cuda", decode_target: str = "gpu", hybrid_max_fetch: int = 1,
+                 hybrid_fetch_fraction: float = 0.0):
         assert quant_format in ("bf16", "fp8_block", "ds_fp4"), quant_format
+        assert decode_target in ("gpu", "cpu", "hybrid"), decode_target
+        # decode placement (moe/offload_cache.py:117-136): "gpu" fetches every
+        # miss; "hybrid" fetches at most hybrid_max_fetch (or the
+        # hybrid_fetch_fraction share) of a step's misses and the CPU executor
+        # computes the rest; cpu_layer_ids decode on the CPU entirely
+        self.decode_target = decode_target
+        self.hybrid_max_fetch = hybrid_max_fetch
+        self.hybrid_fetch_fraction = hybrid_fetch_fraction
+        self.cpu_executor = None
+        self.cpu_layer_ids: frozenset = frozenset()
         self.num_layers = num_layers
         self.num_experts = num_experts
         self.cache_size = cache_size
@@ -75,6 +99,20 @@ class ExpertSlotCache:
                 assert t.shape[0] == self.num_experts and t.shape[1:] == self.banks[name].shape[1:], (name, t.shape)
         self.sources = OrderedDict((name, list(sources[name])) for name in self.banks)
 
+    def set_cpu_executor(self, executor) -> None:
+        """Attaches the CPU share of the decode (a ``CpuMoeDecoder`` reading
+        this cache's host sources; ``:513-522``)."""
+        assert self.decode_target in ("cpu", "hybrid"), "set_cpu_executor requires decode_target cpu or hybrid"
+        self.cpu_executor = executor
+
+    def is_cpu_layer(self, layer_id: int) -> bool:
+        return layer_id in self.cpu_layer_ids
+
+    def host_bank_tensors(self, layer_id: int) -> tuple[torch.Tensor, ...]:
+        """The pinned host rows of one layer, in bank order."""
+        assert self.sources, "set_bank_sources must register the host banks first"
+        return tuple(layers[layer_id] for layers in self.sources.values())
+
     def reset(self) -> None:
         """Empties the cache: no expert resident, usage and step cleared."""
         self.slot_for_id.fill_(-1)
@@ -117,20 +155,27 @@ class ExpertSlotCache:
         assert miss_mask is None, "every expert is admitted when host sources are registered"
         return self._admit(layer_id, expert_ids, -1, None, stats)
 
-    def ensure_experts_hybrid(self, layer_id: int, expert_ids: torch.Tensor, max_fetch: int,
-                              by_recency: bool = True) -> torch.Tensor:
-        """Capped admission (``offload_kernels.py:43-60``): at most ``max_fetch``
-        of the missing experts (most recently seen first with ``by_recency``,
-        else lowest id first) are admitted; the others map to -1."""
+    def ensure_experts_hybrid(self, layer_id: int, expert_ids: torch.Tensor, max_fetch: int | None = None,
+                              by_recency: bool = True, fetch_fraction: float | None = None,
+                              cpu_ids: torch.Tensor | None = None) -> torch.Tensor:
+        """Capped admission (``offload_kernels.py:43-60``, ``offload_cache.py:812-831``):
+        at most ``max_fetch`` (default ``hybrid_max_fetch``; or the
+        ``fetch_fraction`` share, default ``hybrid_fetch_fraction``) of the
+        missing experts, most recently seen first with ``by_recency`` (else
+        lowest id first), are admitted; the others map to -1 and, with
+        ``cpu_ids``, are listed there by expert id for the CPU."""
         assert self.sources, "set_bank_sources must register the host banks first"
         stats = self.lru_stats[layer_id] if self.collect_stats else None
         rec = self.expert_recency[layer_id] if by_recency else None
-        return self._admit(layer_id, expert_ids, max_fetch, rec, stats)
+        max_fetch = self.hybrid_max_fetch if max_fetch is None else max_fetch
+        frac = self.hybrid_fetch_fraction if fetch_fraction is None else fetch_fraction
+        return self._admit(layer_id, expert_ids, max_fetch, rec, stats, frac, cpu_ids)
 
-    def _admit(self, layer_id, expert_ids, max_fetch, recency, stats):
+    def _admit(self, layer_id, expert_ids, max_fetch, recency, stats, fetch_fraction=0.0, cpu_ids=None):
         ops.lru_ensure(expert_ids, layer_id, self.slot_for_id, self.id_of_slot, self.usage, self.step,
                        self.evict_slots, self.src_indices, self.num_indices, self.num_missing_full,
-                       recency=recency, max_fetch=max_fetch, stats=stats)
+                       recency=recency, max_fetch=max_fetch, stats=stats, fetch_fraction=fetch_fraction,
+                       cpu_ids=cpu_ids)
         self._pending_src_layer = layer_id
         return expert_ids
 

@@ -8,6 +8,7 @@ torch tensors.  There is no CPU path: tensors must live on a ROCm device.
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass
 
 import torch
@@ -124,20 +125,29 @@ def slot_map(topk_ids: torch.Tensor, slot_for_id: torch.Tensor, out: torch.Tenso
 def lru_ensure(expert_ids: torch.Tensor, layer_id: int, slot_for_id: torch.Tensor, id_of_slot: torch.Tensor,
                usage: torch.Tensor, step: torch.Tensor, evict_slots: torch.Tensor, src_indices: torch.Tensor,
                num_indices: torch.Tensor, num_missing: torch.Tensor, recency: torch.Tensor | None = None,
-               max_fetch: int = -1, stats: torch.Tensor | None = None) -> torch.Tensor:
+               max_fetch: int = -1, stats: torch.Tensor | None = None, fetch_fraction: float = 0.0,
+               cpu_ids: torch.Tensor | None = None) -> torch.Tensor:
     """LRU admission of a call's experts into the slot cache; ``expert_ids``
     (int32) are rewritten to slots in place (see ftmoe_lru_ensure).
     ``slot_for_id`` [L, E] int32, ``id_of_slot`` [S] int32, ``usage`` [S] and
     ``step`` [1] int64; ``recency`` (int64 [E] of this layer) selects the
-    most-recent-first miss order."""
+    most-recent-first miss order.  ``fetch_fraction`` > 0 replaces the
+    ``max_fetch`` cap with the bandwidth-matched share of the misses, in Q16
+    as the reference rounds it (moe/offload_kernels.py:58); ``cpu_ids``
+    (int32, shaped like ``expert_ids``) receives the unfetched misses' expert
+    ids and -1 elsewhere."""
+    frac_q16 = min(1 << 16, max(0, round(fetch_fraction * (1 << 16))))
     i32 = (expert_ids, slot_for_id, id_of_slot, evict_slots, src_indices, num_indices, num_missing)
+    if cpu_ids is not None and (cpu_ids.dtype != torch.int32 or cpu_ids.shape != expert_ids.shape
+                                or not cpu_ids.is_contiguous()):
+        raise ValueError("cpu_ids must be contiguous int32 shaped like expert_ids")
     if any(t.dtype != torch.int32 for t in i32):
         raise ValueError("ids, tables, evict/src lists and counts must be int32")
     if usage.dtype != torch.int64 or step.dtype != torch.int64 or (recency is not None and recency.dtype != torch.int64):
         raise ValueError("usage, step and recency must be int64")
     if stats is not None and stats.dtype != torch.int64:
         raise ValueError("stats must be int64[4]")
-    _require_gpu(*i32, usage, step, recency, stats)
+    _require_gpu(*i32, usage, step, recency, stats, cpu_ids)
     if not expert_ids.is_contiguous():
         raise ValueError("expert_ids must be contiguous")
     num_layers, num_experts = slot_for_id.shape
@@ -146,9 +156,9 @@ def lru_ensure(expert_ids: torch.Tensor, layer_id: int, slot_for_id: torch.Tenso
     check(
         lib().ftmoe_lru_ensure(_ptr(expert_ids), expert_ids.numel(), layer_id, num_layers, num_experts,
                                _ptr(slot_for_id), _ptr(id_of_slot), _ptr(usage), _ptr(step), id_of_slot.numel(),
-                               _ptr(recency), max_fetch, _ptr(evict_slots), _ptr(src_indices),
+                               _ptr(recency), max_fetch, frac_q16, _ptr(evict_slots), _ptr(src_indices),
                                min(evict_slots.numel(), src_indices.numel()), _ptr(num_indices), _ptr(num_missing),
-                               _ptr(stats), _stream(expert_ids.device)),
+                               _ptr(cpu_ids), _ptr(stats), _stream(expert_ids.device)),
         "lru_ensure",
     )
     return expert_ids
@@ -240,6 +250,17 @@ class ExpertBank:
     @property
     def inter(self) -> int:
         return self.gate_up.shape[1] // 2
+
+    def host_cstruct(self) -> _lib.FtmoeBank:
+        """The bank as ftmoe_bank with host pointers (the CPU executor's banks:
+        contiguous CPU tensors, pinned when the stream-ordered path reads them)."""
+        for t in (self.gate_up, self.down, self.gate_up_scale, self.down_scale):
+            if t is not None and (t.device.type != "cpu" or not t.is_contiguous()):
+                raise ValueError("host banks are contiguous CPU tensors")
+        return _lib.FtmoeBank(
+            _FORMATS[self.fmt], self.num_rows, self.hidden, self.inter,
+            self.gate_up.data_ptr(), _ptr(self.gate_up_scale), self.down.data_ptr(), _ptr(self.down_scale),
+        )
 
     def cstruct(self) -> _lib.FtmoeBank:
         _require_gpu(self.gate_up, self.down, self.gate_up_scale, self.down_scale)
@@ -427,3 +448,69 @@ def experts_prefill(x: torch.Tensor, topk_w: torch.Tensor, topk_ids: torch.Tenso
         "experts_prefill",
     )
     return y
+
+
+# --------------------------------------------------------------------------- CPU executor
+
+
+class CpuExecutor:
+    """Host-side expert executor of the hybrid decode (ftmoe_cpu_executor):
+    ``run`` computes synchronously; ``submit`` / ``wait`` order the job on a
+    stream (host-function nodes) so that GPU work queued between them overlaps
+    it.  Inputs and outputs are host tensors (pinned for the stream path)."""
+
+    def __init__(self, threads: int = 0):
+        if threads <= 0:  # the process's CPU share: OMP_NUM_THREADS when set, else the affinity mask
+            threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+        self.threads = threads
+        self._h = lib().ftmoe_cpu_executor_create(threads)
+        if not self._h:
+            raise RuntimeError("ftmoe_cpu_executor_create failed")
+
+    @property
+    def isa(self) -> str:
+        return lib().ftmoe_cpu_executor_isa(self._h).decode()
+
+    def close(self) -> None:
+        if self._h:
+            lib().ftmoe_cpu_executor_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def _check(x, w, ids, y):
+        for t in (x, w, ids, y):
+            if t.device.type != "cpu" or not t.is_contiguous():
+                raise ValueError("CPU executor tensors are contiguous host tensors")
+        if x.dtype != torch.bfloat16 or y.dtype != torch.bfloat16 or w.dtype != torch.float32 or ids.dtype != torch.int32:
+            raise ValueError("x, y bf16; w float32; ids int32")
+        if w.shape != ids.shape or x.shape[0] != ids.shape[0] or y.shape != x.shape:
+            raise ValueError("shape mismatch")
+
+    def run(self, bank: ExpertBank, x, w, ids, y=None, activation: str = "silu"):
+        y = y if y is not None else torch.empty_like(x)
+        self._check(x, w, ids, y)
+        b = bank.host_cstruct()
+        m, k = ids.shape
+        check(lib().ftmoe_cpu_experts(self._h, ctypes.byref(b), x.data_ptr(), w.data_ptr(), ids.data_ptr(), m, k,
+                                      _lib.ACT[activation], y.data_ptr()), "cpu_experts")
+        return y
+
+    def submit(self, bank: ExpertBank, x, w, ids, y, activation: str = "silu", device=None):
+        """Enqueues the job on the current stream of ``device``; returns a handle for ``wait``."""
+        self._check(x, w, ids, y)
+        b = bank.host_cstruct()
+        m, k = ids.shape
+        job = ctypes.c_void_p()
+        check(lib().ftmoe_cpu_experts_submit(self._h, ctypes.byref(b), x.data_ptr(), w.data_ptr(), ids.data_ptr(),
+                                             m, k, _lib.ACT[activation], y.data_ptr(), _stream(device),
+                                             ctypes.byref(job)), "cpu_experts_submit")
+        return job
+
+    def wait(self, job, device=None) -> None:
+        check(lib().ftmoe_cpu_experts_wait(self._h, job, _stream(device)), "cpu_experts_wait")

@@ -121,12 +121,19 @@ int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_i
  *   step += 1; the distinct ids of expert_ids are seen; resident seen experts
  *   get usage[slot] = step; missing seen experts are ordered by ascending id,
  *   or, with recency (nullable, int64 [num_experts] of this layer), by most
- *   recent first then ascending id; the first min(misses, max_fetch (< 0: no
- *   cap), capacity) of them take, one after the other, the slot with the
+ *   recent first then ascending id; the first min(misses, cap, capacity) of
+ *   them take, one after the other, the slot with the
  *   smallest (usage, slot) -- its previous owner, of any layer, is unmapped
  *   -- and are listed in evict_slots / src_indices (layer-local rows);
  *   recency of every seen expert = step; expert_ids are rewritten in place to
  *   slots (-1 for unfetched misses and ids outside [0, num_experts)).
+ *   cap = max_fetch (< 0: no cap); with fetch_frac_q16 in (0, 65536] (the
+ *   hybrid_fetch_fraction f of offload_cache.py:131-136 in Q16) it is instead
+ *   the n in {floor(m f), floor(m f) + 1} with the smaller max(n (1 - f),
+ *   (m - n) f), lower n on a tie (offload_kernels.py:160-164), m the misses.
+ *   cpu_ids (nullable) int32 [numel] receives, per route, the expert id of
+ *   an unfetched miss and -1 elsewhere: the routes the hybrid decode gives
+ *   the CPU (layers/moe.py:350-352).
  *   slot_for_id int32 [num_layers * num_experts] (row layer_id is this layer),
  *   id_of_slot int32 [cache_size] (flat ids, -1 empty), usage int64
  *   [cache_size], step int64 [1]; num_indices / num_missing int32 [1] receive
@@ -135,8 +142,9 @@ int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_i
  * num_experts, cache_size <= 8192. */
 int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layers, int num_experts,
                      int32_t* slot_for_id, int32_t* id_of_slot, int64_t* usage, int64_t* step, int cache_size,
-                     int64_t* recency, int max_fetch, int32_t* evict_slots, int32_t* src_indices, int capacity,
-                     int32_t* num_indices, int32_t* num_missing, int64_t* stats, ftmoe_stream_t stream);
+                     int64_t* recency, int max_fetch, int fetch_frac_q16, int32_t* evict_slots,
+                     int32_t* src_indices, int capacity, int32_t* num_indices, int32_t* num_missing,
+                     int32_t* cpu_ids, int64_t* stats, ftmoe_stream_t stream);
 
 /* One bank of the gather below: this layer's expert rows in pinned host
  * memory ([num_experts, row_bytes]) and the slot bank ([cache_size,
@@ -235,6 +243,35 @@ size_t ftmoe_experts_prefill_workspace(int M, int top_k, const ftmoe_bank* bank,
 int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
                           const ftmoe_bank* bank, const ftmoe_bank* shared, int activation, void* y,
                           void* workspace, size_t workspace_bytes, ftmoe_stream_t stream);
+
+/* Host-side expert executor of the hybrid decode (CPU pool computing the
+ * routes whose experts are on the host; replaces the CPU MoE executor of the
+ * hybrid backend, moe/cpu_executor.py:538-600 and
+ * kernel/csrc/cpu_moe/cpu_moe_ext.cpp:1574-1668, run beside the GPU as in
+ * layers/moe.py:325-372).  Banks are ftmoe_bank with HOST pointers (bf16,
+ * FP8 128x128, MXFP4 as on the device).  x bf16 [M,H], w float32 [M,k], ids
+ * int32 [M,k] bank rows (< 0 or >= num_rows skipped), y bf16 [M,H] =
+ * bf16(sum over the token's routes, in route order, of bf16(w * expert(x))),
+ * expert rounding as ftmoe_experts_decode; tokens without routes get 0.
+ * threads <= 0: one per hardware thread. */
+typedef struct ftmoe_cpu_executor ftmoe_cpu_executor;
+ftmoe_cpu_executor* ftmoe_cpu_executor_create(int threads);
+void ftmoe_cpu_executor_destroy(ftmoe_cpu_executor* ex);
+const char* ftmoe_cpu_executor_isa(ftmoe_cpu_executor* ex);
+/* Synchronous run on the calling thread's behalf. */
+int ftmoe_cpu_experts(ftmoe_cpu_executor* ex, const ftmoe_bank* host_bank, const void* x, const float* w,
+                      const int32_t* ids, int M, int k, int activation, void* y);
+/* Stream-ordered run: _submit enqueues a host function that starts the job when
+ * the stream reaches it (x, w, ids then must hold the inputs: pinned buffers
+ * filled by earlier copies on the stream) and returns at once; _wait enqueues a
+ * host function that blocks the stream until the job is done.  Work on the
+ * stream between the two overlaps the CPU job.  Graph-capturable (a captured
+ * job keeps its record for the graph's lifetime).  One executor runs its jobs
+ * in submission order. */
+int ftmoe_cpu_experts_submit(ftmoe_cpu_executor* ex, const ftmoe_bank* host_bank, const void* x, const float* w,
+                             const int32_t* ids, int M, int k, int activation, void* y, ftmoe_stream_t stream,
+                             void** job);
+int ftmoe_cpu_experts_wait(ftmoe_cpu_executor* ex, void* job, ftmoe_stream_t stream);
 
 /* Instrumentation (no counterpart in the reference, whose NVTX ranges play this
  * role): between begin and end, every ftmoe_experts_* call made outside graph

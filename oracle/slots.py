@@ -73,9 +73,34 @@ class CacheState:
         return c
 
 
+def fraction_cap(num_missing: int, frac_q16: int) -> int:
+    """Bandwidth-matched fetch count (``moe/offload_kernels.py:160-164``): with
+    m misses and f = frac_q16 / 2^16, the n in {floor(m f), floor(m f) + 1}
+    whose max(n (1 - f), (m - n) f) is smaller, the lower one on a tie, then
+    at most m.  Pinned (tests/test_oracle_slots.py) against the brute-force
+    argmin of that cost over every n in [0, m]."""
+    m, q = num_missing, 1 << 16
+    lo = (m * frac_q16) >> 16
+
+    def cost(f):
+        return max(f * (q - frac_q16), (m - f) * frac_q16)
+
+    return min(m, lo if cost(lo) <= cost(lo + 1) else lo + 1)
+
+
+def hybrid_split(raw_ids, slot_ids, num_experts: int):
+    """Routes the CPU computes in the hybrid decode (``layers/moe.py:350-352``):
+    the raw expert id where admission left no slot (an unfetched miss), -1
+    where the GPU computes the route or the id is outside [0, E)."""
+    raw = np.asarray(raw_ids, dtype=np.int32)
+    valid = (raw >= 0) & (raw < num_experts)
+    return np.where(valid & (np.asarray(slot_ids) < 0), raw, -1).astype(np.int32)
+
+
 def lru_ensure(state: CacheState, layer: int, expert_ids, max_fetch: int = -1, by_recency: bool = False,
-               capacity: int | None = None):
+               capacity: int | None = None, frac_q16: int = 0):
     """One admission call (``moe/offload_kernels.py:128-188``); mutates ``state``.
+    ``frac_q16`` > 0 replaces ``max_fetch`` by ``fraction_cap``.
 
     Returns (slot ids [same shape], evict_slots, src_indices, num_missing, stats).
     Ids outside [0, E) are not seen and map to -1."""
@@ -99,6 +124,8 @@ def lru_ensure(state: CacheState, layer: int, expert_ids, max_fetch: int = -1, b
     else:
         missing.sort()
     n = len(missing) if max_fetch < 0 else min(len(missing), max_fetch)
+    if frac_q16 > 0:
+        n = fraction_cap(len(missing), frac_q16)
     if capacity is not None:
         n = min(n, capacity)
     evict, src = [], []

@@ -1,0 +1,86 @@
+"""The host-side expert executor of the hybrid decode (ftmoe_cpu_experts,
+freetoken_amd/csrc/cpu_experts.hip) against the oracle's decode layer
+(oracle.experts.moe_layer, the reference's rounding points) on host banks of
+every format: the routes the CPU takes in the reference's hybrid backend
+(layers/moe.py:325-372, CPU pool of moe/cpu_executor.py).  No GPU needed:
+the synchronous entry point touches no HIP call."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import synth
+from freetoken_amd import _lib, ops
+
+from _helpers import to_device_bank
+from conftest import COS_TOL, MAX_REL_TOL, cosine, max_rel
+
+
+@pytest.fixture(scope="module")
+def executor():
+    ex = ops.CpuExecutor(threads=4)
+    yield ex
+    ex.close()
+
+
+def _host(a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=dtype))
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "fp8", "mxfp4"])
+@pytest.mark.parametrize("M,k,skip", [(1, 2, False), (3, 4, True), (5, 8, True)])
+def test_cpu_experts_match_oracle(executor, fmt, M, k, skip):
+    rng = np.random.default_rng(M * 10 + k)
+    E, H, I = 8, 256, 384
+    bank = synth.make_bank(fmt, E, H, I, rng)
+    x = synth.activations(rng, M, H)
+    logits = synth.normal(rng, (M, E))
+    w, ids = oracle.routing.softmax_topk(logits, k, True)
+    if skip:  # routes the GPU takes are passed as -1 and contribute nothing
+        ids = ids.copy()
+        ids[rng.random(ids.shape) < 0.4] = -1
+    y_ref = oracle.experts.moe_layer("decode", x, w, ids, bank, None)
+    hb = to_device_bank(bank, "cpu")
+    y = executor.run(hb, _host(x, np.float32).to(torch.bfloat16), _host(w, np.float32), _host(ids, np.int32))
+    g = y.float().numpy()
+    assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, (fmt, max_rel(g, y_ref))
+    if skip:
+        none = (ids < 0).all(axis=1)
+        assert (g[none] == 0).all()  # a token with every route elsewhere gets exact zeros
+
+
+def test_cpu_experts_activation_variants(executor):
+    """gelu and gelu_tanh change only the activation of the gate rows."""
+    rng = np.random.default_rng(3)
+    E, H, I = 4, 128, 128
+    bank = synth.make_bank("bf16", E, H, I, rng)
+    hb = to_device_bank(bank, "cpu")
+    x = synth.activations(rng, 2, H)
+    w, ids = oracle.routing.softmax_topk(synth.normal(rng, (2, E)), 2, True)
+    args = (_host(x, np.float32).to(torch.bfloat16), _host(w, np.float32), _host(ids, np.int32))
+    ys = {a: executor.run(hb, *args, activation=a).float().numpy() for a in ("silu", "gelu", "gelu_tanh")}
+    assert cosine(ys["gelu"], ys["gelu_tanh"]) > 0.999  # the tanh form approximates erf
+    assert not np.array_equal(ys["silu"], ys["gelu"])
+
+
+def test_cpu_experts_validation(executor):
+    rng = np.random.default_rng(5)
+    bank = synth.make_bank("fp8", 4, 256, 128, rng)
+    hb = to_device_bank(bank, "cpu")
+    x = torch.zeros(2, 256, dtype=torch.bfloat16)
+    w = torch.ones(2, 2)
+    with pytest.raises(ValueError):
+        executor.run(hb, x, w, torch.zeros(2, 2, dtype=torch.int64))
+    L = _lib.lib()
+    b = hb.host_cstruct()
+    b.hidden = 200  # not a multiple of 128
+    rc = L.ftmoe_cpu_experts(executor._h, b, x.data_ptr(), w.data_ptr(), w.data_ptr(), 2, 2, 0, x.data_ptr())
+    assert rc == _lib.FTMOE_ERR_UNSUPPORTED
+    assert L.ftmoe_cpu_experts(None, b, None, None, None, 2, 2, 0, None) == _lib.FTMOE_ERR_INVALID
+
+
+def test_executor_reports_isa(executor):
+    assert executor.isa in ("avx512f", "scalar")

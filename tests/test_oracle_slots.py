@@ -116,3 +116,35 @@ def test_more_misses_than_slots_follows_the_sequential_rule():
     assert evict.tolist() == [0, 1, 0, 0] and src.tolist() == [0, 1, 2, 3]
     assert out.tolist() == [-1, 1, -1, 0]
     assert _inverse_ok(st)
+
+
+def test_fraction_cap_known_answers():
+    # tests/moe/test_hybrid_fetch.py:29-41: rounding to the balanced neighbour, not up
+    q = 1 << 16
+    assert S.fraction_cap(3, round(0.415 * q)) == 1
+    assert S.fraction_cap(4, round(0.415 * q)) == 2
+    for frac in (0.1, 0.415, 0.454, 0.7, 1.0):
+        fq = round(frac * q)
+        for m in range(65):
+            n = S.fraction_cap(m, fq)
+            assert 0 <= n <= m and abs(n - frac * m) <= 1.0
+            # brute force: the lowest n in [0, m] minimising the slower overlapped side
+            costs = [max(f * (q - fq), (m - f) * fq) for f in range(m + 1)]
+            assert n == costs.index(min(costs)), (frac, m)
+
+
+def test_fraction_cap_admission_and_split():
+    """The fraction replaces the fixed cap; the CPU split holds exactly the
+    unfetched misses (tests/moe/test_hybrid_fetch.py:89-115 on the oracle)."""
+    rng = np.random.default_rng(2)
+    st = S.CacheState(2, 32, 40)
+    fq = round(0.415 * (1 << 16))
+    for _ in range(64):
+        ids = rng.permutation(32)[:8].astype(np.int32)
+        out, evict, src, nmiss, _ = S.lru_ensure(st, 0, ids, max_fetch=32, by_recency=True, frac_q16=fq)
+        assert evict.size == S.fraction_cap(nmiss, fq)
+        assert (out >= 0).sum() == len(set(ids.tolist())) - (nmiss - evict.size)
+        cpu = S.hybrid_split(ids, out, 32)
+        assert ((cpu >= 0) == (out < 0)).all() and (cpu[cpu >= 0] == ids[cpu >= 0]).all()
+        assert _inverse_ok(st)
+    assert S.hybrid_split([-1, 40, 3], [-1, -1, -1], 32).tolist() == [-1, -1, 3]
