@@ -350,6 +350,85 @@ def run_miss_fetch(gen, dev, n_fetch: int = 8, steps: int = 10):
                 fetch_gbs=gbs, pcie_frac=gbs / PCIE_PEAK_GBS)
 
 
+def run_hybrid(gen, dev, M: int = 1, n_sets: int = 4, slots: int = 8, max_fetch: int = 1, steps: int = 8,
+               warmup: int = 8):
+    """Hybrid decode at C4 shape (FP8 experts, one layer): each step routes the
+    M tokens to one of n_sets disjoint sets of k experts in turn, over a slot
+    cache of ``slots`` experts, so every step has misses; the admission fetches
+    at most max_fetch of them over PCIe and the CPU executor computes the rest
+    while the GPU runs its share.  Besides the step time it times the two
+    shares alone on the same routing (the CPU job; the gather plus the GPU
+    experts), so the overlap is (cpu + gpu) / step."""
+    from freetoken_amd.core import moe_phase
+    from freetoken_amd.layers.moe import OffloadMoELayer
+    from freetoken_amd.moe.cpu_decode import CpuMoeDecoder
+    from freetoken_amd.moe.offload_cache import ExpertSlotCache
+
+    c = C4
+    H, I, k = c["H"], c["I"], c["k"]
+    E = n_sets * k
+    shapes = {"gate_up": (2 * I, H), "gate_up_scale": (2 * I // 128, H // 128), "down": (H, I),
+              "down_scale": (H // 128, I // 128)}
+    host = {}
+    for name, shape in shapes.items():
+        if name.endswith("scale"):
+            d = torch.rand((E,) + shape, generator=gen, device=dev) * 1e-3 + 1e-4
+        else:
+            d = torch.randint(0, 256, (E,) + shape, generator=gen, device=dev, dtype=torch.uint8)
+            d[(d & 0x7F) == 0x7F] = 0  # no NaN codes
+        h = torch.empty(d.shape, dtype=d.dtype, pin_memory=True)
+        h.copy_(d)
+        host[name] = h
+        del d
+    cache = ExpertSlotCache(1, E, slots, "fp8_block", device=dev, decode_target="hybrid", hybrid_max_fetch=max_fetch)
+    cache.set_bank_caches(**{n: torch.zeros((slots,) + h.shape[1:], dtype=h.dtype, device=dev)
+                             for n, h in host.items()})
+    cache.set_bank_sources({n: [h] for n, h in host.items()})
+    cache.reset()
+    dec = CpuMoeDecoder(cache, k)
+    cache.set_cpu_executor(dec)
+    layer = OffloadMoELayer(0, E, k, H, I, device=dev)
+    layer.offload_cache = cache
+    x = torch.randn((M, H), generator=gen, device=dev).to(torch.bfloat16)
+    w = torch.full((M, k), 1.0 / k, device=dev)
+    sets = [torch.arange(s * k, (s + 1) * k, dtype=torch.int32, device=dev).repeat(M, 1) for s in range(n_sets)]
+    eb = expert_bytes("fp8_block", H, I)
+    rec = []
+    with moe_phase("decode", backend="hybrid"):
+        for i in range(warmup + steps):
+            raw = sets[i % n_sets]
+            ids = raw.clone()
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+            torch.cuda.synchronize()
+            ev[0].record()
+            layer.routed_forward(x, w, ids)
+            ev[1].record()
+            torch.cuda.synchronize()
+            cpu_ids = torch.where(ids < 0, raw, torch.full_like(raw, -1))
+            ev[2].record()
+            dec.decode(0, x, w, cpu_ids)
+            ev[3].record()
+            cache.copy_missing()
+            ops.experts_decode(x, w, ids, layer._views_bank(cache.bank_views()))
+            ev[4].record()
+            torch.cuda.synchronize()
+            if i >= warmup:
+                n_cpu = int(torch.unique(cpu_ids[cpu_ids >= 0]).numel())
+                n_fetch = int(cache.num_indices.item())
+                n_gpu = int(torch.unique(ids[ids >= 0]).numel())
+                rec.append((ev[0].elapsed_time(ev[1]), ev[2].elapsed_time(ev[3]), ev[3].elapsed_time(ev[4]),
+                            n_cpu, n_fetch, n_gpu))
+    threads, isa = dec.executor.threads, dec.executor.isa
+    dec.close()
+    med = lambda j: statistics.median(r[j] for r in rec)  # noqa: E731
+    step, cpu_ms, gpu_ms = med(0), med(1), med(2)
+    n_cpu, n_fetch, n_gpu = med(3), med(4), med(5)
+    return dict(batch=M, experts_per_step=k, slots=slots, max_fetch=max_fetch, step_ms=step,
+                cpu_experts=n_cpu, fetched_experts=n_fetch, gpu_experts=n_gpu, cpu_ms=cpu_ms, gpu_ms=gpu_ms,
+                overlap=(cpu_ms + gpu_ms) / step, cpu_gbs=n_cpu * eb / (cpu_ms * 1e-3) / 1e9,
+                cpu_threads=threads, cpu_isa=isa)
+
+
 def cpu_baseline(layer: DecodeLayer, M: int, budget_s: float, gen, dev):
     """C++ restatement of the reference CPU executor on this host: the same C4
     routing (resident slots), bf16-dequantised banks (the reference's CPU route
@@ -434,6 +513,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--miss-only", action="store_true", help="time the miss path (admission + PCIe gather) alone")
+    ap.add_argument("--hybrid-only", action="store_true", help="time the hybrid CPU/GPU decode alone")
     ap.add_argument("--prefill-only", choices=("fp8_block", "mxfp4"), default=None,
                     help="profiling aid: run only the C5 prefill of this format and print its result")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -460,6 +540,12 @@ def main() -> int:
     if args.miss_only:
         res = run_miss_fetch(gen, dev)
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}), flush=True)
+        return 0
+
+    if args.hybrid_only:
+        for M in (1, 4):
+            res = run_hybrid(gen, dev, M=M)
+            print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}), flush=True)
         return 0
 
     if args.prefill_only:
@@ -503,6 +589,8 @@ def main() -> int:
             sweep[f"c5_prefill_8192_{fmt}"] = run_prefill(fmt, 10, 3, gen, dev)
         log("[bench] sweep C4 miss path (admission + PCIe gather of 8 experts per step)")
         sweep["c4_miss_fetch_8_experts"] = run_miss_fetch(gen, dev)
+        log("[bench] sweep C4 hybrid decode (1 expert fetched per step, the other misses on the CPU)")
+        sweep["c4_hybrid_b1"] = run_hybrid(gen, dev, M=1)
 
     def rnd(d):
         return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}

@@ -20,6 +20,7 @@
 #include <immintrin.h>
 #include <sched.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <condition_variable>
@@ -83,83 +84,152 @@ struct Mat {
   const void* s;     // FP8 float [N/128, K/128]; MXFP4 uint8 [N, K/32]
 };
 
-float dot_scalar(const Mat& m, int n, const float* x) {
-  if (m.format == FTMOE_FMT_BF16) {
-    const bf16* w = reinterpret_cast<const bf16*>(m.w) + static_cast<size_t>(n) * m.K;
-    float acc = 0.f;
-    for (int k = 0; k < m.K; ++k) acc += b2f(w[k]) * x[k];
-    return acc;
-  }
-  if (m.format == FTMOE_FMT_FP8_B128) {
-    const uint8_t* w = m.w + static_cast<size_t>(n) * m.K;
-    const float* s = static_cast<const float*>(m.s) + static_cast<size_t>(n / 128) * (m.K / 128);
-    float acc = 0.f;
-    for (int kb = 0; kb < m.K / 128; ++kb) {
-      float part = 0.f;
-      for (int k = 0; k < 128; ++k) part += kT.e4m3[w[kb * 128 + k]] * x[kb * 128 + k];
-      acc += part * s[kb];
-    }
-    return acc;
-  }
-  const uint8_t* w = m.w + static_cast<size_t>(n) * (m.K / 2);
-  const uint8_t* s = static_cast<const uint8_t*>(m.s) + static_cast<size_t>(n) * (m.K / 32);
-  float acc = 0.f;
-  for (int kb = 0; kb < m.K / 32; ++kb) {
-    float part = 0.f;
-    for (int k = 0; k < 32; k += 2) {
-      const uint8_t b = w[kb * 16 + k / 2];
-      part += kT.e2m1[b & 15] * x[kb * 32 + k] + kT.e2m1[b >> 4] * x[kb * 32 + k + 1];
-    }
-    acc += part * std::ldexp(1.0f, static_cast<int>(s[kb]) - 127);
-  }
-  return acc;
-}
+constexpr int kMaxVec = 8;  // activation vectors per pass over a weight row
 
-__attribute__((target("avx512f"))) float dot_avx512(const Mat& m, int n, const float* x) {
-  if (m.format == FTMOE_FMT_BF16) {
-    const bf16* w = reinterpret_cast<const bf16*>(m.w) + static_cast<size_t>(n) * m.K;
-    __m512 acc = _mm512_setzero_ps();
-    for (int k = 0; k < m.K; k += 16) {
-      const __m512i wi = _mm512_slli_epi32(_mm512_cvtepu16_epi32(_mm256_loadu_si256(reinterpret_cast<const __m256i*>(w + k))), 16);
-      acc = _mm512_fmadd_ps(_mm512_castsi512_ps(wi), _mm512_loadu_ps(x + k), acc);
-    }
-    return _mm512_reduce_add_ps(acc);
-  }
-  if (m.format == FTMOE_FMT_FP8_B128) {
-    const uint8_t* w = m.w + static_cast<size_t>(n) * m.K;
-    const float* s = static_cast<const float*>(m.s) + static_cast<size_t>(n / 128) * (m.K / 128);
-    __m512 acc = _mm512_setzero_ps();
-    for (int kb = 0; kb < m.K / 128; ++kb) {
-      __m512 part = _mm512_setzero_ps();
-      for (int k = 0; k < 128; k += 16) {
-        const __m512i idx = _mm512_cvtepu8_epi32(_mm_loadu_si128(reinterpret_cast<const __m128i*>(w + kb * 128 + k)));
-        part = _mm512_fmadd_ps(_mm512_i32gather_ps(idx, kT.e4m3, 4), _mm512_loadu_ps(x + kb * 128 + k), part);
+// dots of weight row n with nx activation vectors xs[] (each K fp32), in the
+// format's accumulation order: bf16 one pass; FP8 per 128-block partial times
+// the block scale; MXFP4 per 32-block times its power-of-two scale.
+void dot_scalar(const Mat& m, int n, const float* const* xs, int nx, float* out) {
+  for (int v = 0; v < nx; ++v) {
+    const float* x = xs[v];
+    float acc = 0.f;
+    if (m.format == FTMOE_FMT_BF16) {
+      const bf16* w = reinterpret_cast<const bf16*>(m.w) + static_cast<size_t>(n) * m.K;
+      for (int k = 0; k < m.K; ++k) acc += b2f(w[k]) * x[k];
+    } else if (m.format == FTMOE_FMT_FP8_B128) {
+      const uint8_t* w = m.w + static_cast<size_t>(n) * m.K;
+      const float* s = static_cast<const float*>(m.s) + static_cast<size_t>(n / 128) * (m.K / 128);
+      for (int kb = 0; kb < m.K / 128; ++kb) {
+        float part = 0.f;
+        for (int k = 0; k < 128; ++k) part += kT.e4m3[w[kb * 128 + k]] * x[kb * 128 + k];
+        acc += part * s[kb];
       }
-      acc = _mm512_fmadd_ps(part, _mm512_set1_ps(s[kb]), acc);
+    } else {
+      const uint8_t* w = m.w + static_cast<size_t>(n) * (m.K / 2);
+      const uint8_t* s = static_cast<const uint8_t*>(m.s) + static_cast<size_t>(n) * (m.K / 32);
+      for (int kb = 0; kb < m.K / 32; ++kb) {
+        float part = 0.f;
+        for (int k = 0; k < 32; k += 2) {
+          const uint8_t b = w[kb * 16 + k / 2];
+          part += kT.e2m1[b & 15] * x[kb * 32 + k] + kT.e2m1[b >> 4] * x[kb * 32 + k + 1];
+        }
+        acc += part * std::ldexp(1.0f, static_cast<int>(s[kb]) - 127);
+      }
     }
-    return _mm512_reduce_add_ps(acc);
+    out[v] = acc;
   }
-  const uint8_t* w = m.w + static_cast<size_t>(n) * (m.K / 2);
-  const uint8_t* s = static_cast<const uint8_t*>(m.s) + static_cast<size_t>(n) * (m.K / 32);
-  const __m512 lut = _mm512_loadu_ps(kT.e2m1);
-  __m512 acc = _mm512_setzero_ps();
-  for (int kb = 0; kb < m.K / 32; ++kb) {
-    // 16 bytes = 32 values; even k in the low nibble
-    const __m512i b = _mm512_cvtepu8_epi32(_mm_loadu_si128(reinterpret_cast<const __m128i*>(w + kb * 16)));
-    const __m512 lo = _mm512_permutexvar_ps(_mm512_and_si512(b, _mm512_set1_epi32(15)), lut);
-    const __m512 hi = _mm512_permutexvar_ps(_mm512_srli_epi32(b, 4), lut);
-    // x pairs: x[2j] with lo[j], x[2j+1] with hi[j]
-    const __m512i ev = _mm512_setr_epi32(0, 2, 4, 6, 8, 10, 12, 14, 16, 18, 20, 22, 24, 26, 28, 30);
-    const __m512i od = _mm512_add_epi32(ev, _mm512_set1_epi32(1));
-    const __m512 x0 = _mm512_loadu_ps(x + kb * 32), x1 = _mm512_loadu_ps(x + kb * 32 + 16);
-    const __m512 xe = _mm512_permutex2var_ps(x0, ev, x1), xo = _mm512_permutex2var_ps(x0, od, x1);
-    const __m512 part = _mm512_fmadd_ps(hi, xo, _mm512_mul_ps(lo, xe));
-    acc = _mm512_fmadd_ps(part, _mm512_set1_ps(std::ldexp(1.0f, static_cast<int>(s[kb]) - 127)), acc);
-  }
-  return _mm512_reduce_add_ps(acc);
 }
 
-using dot_fn = float (*)(const Mat&, int, const float*);
+// AVX-512: each 32 weights are decoded to fp32 once and used for every
+// vector.  FP8 codes widen to 16 bits and become fp16 by a shift (sign to bit
+// 15, exponent and mantissa under fp16's, exact for every finite e4m3 value
+// including subnormals: the fp16 holds value / 2^8), then fp32 by vcvtph2ps;
+// the 2^8 rides on the block scale, so the block partial times (scale * 2^8)
+// is the same product.  MXFP4 looks its values up with one permute and
+// interleaves the low / high nibbles back into k order.
+template <int FMT, int NX>
+__attribute__((target("avx512f,avx512bw"))) void dot_avx512_t(const Mat& m, int n, const float* const* xs,
+                                                               float* out) {
+  // A independent accumulator chains per vector: few vectors would otherwise
+  // wait on the FMA latency
+  constexpr int A = NX <= 4 ? 2 : 1;
+  __m512 acc[A][NX];
+#pragma unroll
+  for (int a = 0; a < A; ++a)
+#pragma unroll
+    for (int v = 0; v < NX; ++v) acc[a][v] = _mm512_setzero_ps();
+  if constexpr (FMT == FTMOE_FMT_BF16) {
+    const bf16* w = reinterpret_cast<const bf16*>(m.w) + static_cast<size_t>(n) * m.K;
+    for (int k = 0; k < m.K; k += 32) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const __m512 wv = _mm512_castsi512_ps(_mm512_slli_epi32(
+            _mm512_cvtepu16_epi32(_mm256_loadu_si256(reinterpret_cast<const __m256i*>(w + k + 16 * c))), 16));
+#pragma unroll
+        for (int v = 0; v < NX; ++v)
+          acc[c % A][v] = _mm512_fmadd_ps(wv, _mm512_loadu_ps(xs[v] + k + 16 * c), acc[c % A][v]);
+      }
+    }
+  } else if constexpr (FMT == FTMOE_FMT_FP8_B128) {
+    const uint8_t* w = m.w + static_cast<size_t>(n) * m.K;
+    const float* s = static_cast<const float*>(m.s) + static_cast<size_t>(n / 128) * (m.K / 128);
+    const __m512i sgn = _mm512_set1_epi16(0x80), mag = _mm512_set1_epi16(0x7F);
+    for (int kb = 0; kb < m.K / 128; ++kb) {
+      __m512 part[A][NX];
+#pragma unroll
+      for (int a = 0; a < A; ++a)
+#pragma unroll
+        for (int v = 0; v < NX; ++v) part[a][v] = _mm512_setzero_ps();
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int k = kb * 128 + 32 * c;
+        const __m512i b = _mm512_cvtepu8_epi16(_mm256_loadu_si256(reinterpret_cast<const __m256i*>(w + k)));
+        const __m512i h = _mm512_or_si512(_mm512_slli_epi16(_mm512_and_si512(b, sgn), 8),
+                                          _mm512_slli_epi16(_mm512_and_si512(b, mag), 7));
+        const __m512 w0 = _mm512_cvtph_ps(_mm512_castsi512_si256(h));
+        const __m512 w1 = _mm512_cvtph_ps(_mm512_extracti64x4_epi64(h, 1));
+#pragma unroll
+        for (int v = 0; v < NX; ++v) {
+          part[0][v] = _mm512_fmadd_ps(w0, _mm512_loadu_ps(xs[v] + k), part[0][v]);
+          part[A - 1][v] = _mm512_fmadd_ps(w1, _mm512_loadu_ps(xs[v] + k + 16), part[A - 1][v]);
+        }
+      }
+      const __m512 sc = _mm512_set1_ps(s[kb] * 256.0f);
+#pragma unroll
+      for (int v = 0; v < NX; ++v) {
+        const __m512 p = A == 2 ? _mm512_add_ps(part[0][v], part[A - 1][v]) : part[0][v];
+        acc[kb % A][v] = _mm512_fmadd_ps(p, sc, acc[kb % A][v]);
+      }
+    }
+  } else {
+    const uint8_t* w = m.w + static_cast<size_t>(n) * (m.K / 2);
+    const uint8_t* s = static_cast<const uint8_t*>(m.s) + static_cast<size_t>(n) * (m.K / 32);
+    const __m512 lut = _mm512_loadu_ps(kT.e2m1);
+    const __m512i il0 = _mm512_setr_epi32(0, 16, 1, 17, 2, 18, 3, 19, 4, 20, 5, 21, 6, 22, 7, 23);
+    const __m512i il1 = _mm512_setr_epi32(8, 24, 9, 25, 10, 26, 11, 27, 12, 28, 13, 29, 14, 30, 15, 31);
+    for (int kb = 0; kb < m.K / 32; ++kb) {
+      // 16 bytes = 32 values; even k in the low nibble
+      const __m512i b = _mm512_cvtepu8_epi32(_mm_loadu_si128(reinterpret_cast<const __m128i*>(w + kb * 16)));
+      const __m512 lo = _mm512_permutexvar_ps(_mm512_and_si512(b, _mm512_set1_epi32(15)), lut);
+      const __m512 hi = _mm512_permutexvar_ps(_mm512_srli_epi32(b, 4), lut);
+      const __m512 w0 = _mm512_permutex2var_ps(lo, il0, hi), w1 = _mm512_permutex2var_ps(lo, il1, hi);
+      const __m512 sc = _mm512_set1_ps(std::ldexp(1.0f, static_cast<int>(s[kb]) - 127));
+#pragma unroll
+      for (int v = 0; v < NX; ++v) {
+        const __m512 p = _mm512_fmadd_ps(w1, _mm512_loadu_ps(xs[v] + kb * 32 + 16),
+                                         _mm512_mul_ps(w0, _mm512_loadu_ps(xs[v] + kb * 32)));
+        acc[kb % A][v] = _mm512_fmadd_ps(p, sc, acc[kb % A][v]);
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < NX; ++v)
+    out[v] = _mm512_reduce_add_ps(A == 2 ? _mm512_add_ps(acc[0][v], acc[A - 1][v]) : acc[0][v]);
+}
+
+template <int FMT>
+void dot_avx512_f(const Mat& m, int n, const float* const* xs, int nx, float* out) {
+  switch (nx) {
+    case 1: return dot_avx512_t<FMT, 1>(m, n, xs, out);
+    case 2: return dot_avx512_t<FMT, 2>(m, n, xs, out);
+    case 3: return dot_avx512_t<FMT, 3>(m, n, xs, out);
+    case 4: return dot_avx512_t<FMT, 4>(m, n, xs, out);
+    case 5: return dot_avx512_t<FMT, 5>(m, n, xs, out);
+    case 6: return dot_avx512_t<FMT, 6>(m, n, xs, out);
+    case 7: return dot_avx512_t<FMT, 7>(m, n, xs, out);
+    default: return dot_avx512_t<FMT, 8>(m, n, xs, out);
+  }
+}
+
+void dot_avx512(const Mat& m, int n, const float* const* xs, int nx, float* out) {
+  if (m.format == FTMOE_FMT_BF16) return dot_avx512_f<FTMOE_FMT_BF16>(m, n, xs, nx, out);
+  if (m.format == FTMOE_FMT_FP8_B128) return dot_avx512_f<FTMOE_FMT_FP8_B128>(m, n, xs, nx, out);
+  dot_avx512_f<FTMOE_FMT_MXFP4>(m, n, xs, nx, out);
+}
+
+static_assert(kMaxVec == 8, "dot_avx512_f dispatches 1..8 vectors");
+
+using dot_fn = void (*)(const Mat&, int, const float* const*, int, float*);
 
 float silu(float g) { return g / (1.0f + std::exp(-g)); }
 float gelu(float g) { return 0.5f * g * (1.0f + std::erf(g * 0.70710678118654752f)); }
@@ -184,7 +254,7 @@ struct Job {
 class Executor {
  public:
   explicit Executor(int threads) : nthreads_(threads < 1 ? 1 : threads) {
-    dot_ = __builtin_cpu_supports("avx512f") ? dot_avx512 : dot_scalar;
+    dot_ = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") ? dot_avx512 : dot_scalar;
     for (int t = 0; t < nthreads_; ++t) workers_.emplace_back([this] { worker(); });
     driver_ = std::thread([this] { drive(); });
   }
@@ -295,8 +365,7 @@ class Executor {
     const size_t gu_rows = static_cast<size_t>(2) * I, dn_rows = H;
     const auto rowmat = [&](const Mat& m, size_t rows, int e) {
       Mat r = m;
-      const size_t vb = m.format == FTMOE_FMT_BF16 ? 2 : 1;  // bytes per value (MXFP4: per pair)
-      const size_t row_bytes = m.format == FTMOE_FMT_MXFP4 ? m.K / 2 : m.K * vb;
+      const size_t row_bytes = m.format == FTMOE_FMT_MXFP4 ? m.K / 2 : m.format == FTMOE_FMT_BF16 ? m.K * 2 : m.K;
       r.w = m.w + static_cast<size_t>(e) * rows * row_bytes;
       if (m.format == FTMOE_FMT_FP8_B128)
         r.s = static_cast<const float*>(m.s) + static_cast<size_t>(e) * (rows / 128) * (m.K / 128);
@@ -304,38 +373,68 @@ class Executor {
         r.s = static_cast<const uint8_t*>(m.s) + static_cast<size_t>(e) * rows * (m.K / 32);
       return r;
     };
-    xf_.assign(static_cast<size_t>(j.M) * H, 0.f);
-    for (size_t i = 0; i < xf_.size(); ++i) xf_[i] = b2f(j.x[i]);
-    act_.assign(static_cast<size_t>(R) * I, 0.f);
     const auto valid = [&](int r) { return j.ids[r] >= 0 && j.ids[r] < j.bank.num_rows; };
+    // routes grouped by expert (ascending expert, then route), split into
+    // groups of at most kMaxVec routes
+    order_.clear();
+    for (int r = 0; r < R; ++r)
+      if (valid(r)) order_.push_back(r);
+    std::stable_sort(order_.begin(), order_.end(), [&](int a, int b) { return j.ids[a] < j.ids[b]; });
+    group_.clear();
+    for (size_t i = 0; i < order_.size(); ++i)
+      if (i == 0 || j.ids[order_[i]] != j.ids[order_[i - 1]] || i - group_.back() == kMaxVec)
+        group_.push_back(static_cast<int>(i));
+    const int G = static_cast<int>(group_.size());
+    group_.push_back(static_cast<int>(order_.size()));
+    xf_.resize(static_cast<size_t>(j.M) * H);
+    for (size_t i = 0; i < xf_.size(); ++i) xf_[i] = b2f(j.x[i]);
+    act_.resize(static_cast<size_t>(R) * I);
+    dout_.resize(static_cast<size_t>(R) * H);
     constexpr int kTile = 32;
-    // pass 1: gate/up rows of (route, 32 rows of I)
+    // pass 1: gate and up rows of (group, 32 rows of I) -> bf16 act
     const int tiles1 = I / kTile;
-    parallel(R * tiles1, [&](int u) {
-      const int r = u / tiles1, i0 = (u % tiles1) * kTile;
-      if (!valid(r)) return;
-      const Mat m = rowmat(gu, gu_rows, j.ids[r]);
-      const float* x = xf_.data() + static_cast<size_t>(r / j.k) * H;
+    parallel(G * tiles1, [&](int u) {
+      const int g = u / tiles1, i0 = (u % tiles1) * kTile;
+      const int* rs = order_.data() + group_[g];
+      const int nv = group_[g + 1] - group_[g];
+      const Mat m = rowmat(gu, gu_rows, j.ids[rs[0]]);
+      const float* xs[kMaxVec];
+      for (int v = 0; v < nv; ++v) xs[v] = xf_.data() + static_cast<size_t>(rs[v] / j.k) * H;
+      float gv[kMaxVec], uv[kMaxVec];
       for (int i = i0; i < i0 + kTile; ++i) {
-        const float g = rb(dot_(m, i, x)), v = rb(dot_(m, I + i, x));
-        const float a = j.activation == FTMOE_ACT_SILU ? silu(g) : j.activation == FTMOE_ACT_GELU ? gelu(g)
-                                                                                                : gelu_tanh(g);
-        act_[static_cast<size_t>(r) * I + i] = rb(a * v);
+        dot_(m, i, xs, nv, gv);
+        dot_(m, I + i, xs, nv, uv);
+        for (int v = 0; v < nv; ++v) {
+          const float g = rb(gv[v]), up = rb(uv[v]);
+          const float a = j.activation == FTMOE_ACT_SILU ? silu(g) : j.activation == FTMOE_ACT_GELU ? gelu(g)
+                                                                                                  : gelu_tanh(g);
+          act_[static_cast<size_t>(rs[v]) * I + i] = rb(a * up);
+        }
       }
     });
-    // pass 2: down rows of (token, 32 rows of H), routes summed in order
+    // pass 2: down rows of (group, 32 rows of H) -> bf16(down * router weight) per route
     const int tiles2 = H / kTile;
-    parallel(j.M * tiles2, [&](int u) {
-      const int t = u / tiles2, h0 = (u % tiles2) * kTile;
+    parallel(G * tiles2, [&](int u) {
+      const int g = u / tiles2, h0 = (u % tiles2) * kTile;
+      const int* rs = order_.data() + group_[g];
+      const int nv = group_[g + 1] - group_[g];
+      const Mat m = rowmat(dn, dn_rows, j.ids[rs[0]]);
+      const float* xs[kMaxVec];
+      for (int v = 0; v < nv; ++v) xs[v] = act_.data() + static_cast<size_t>(rs[v]) * I;
+      float dv[kMaxVec];
       for (int h = h0; h < h0 + kTile; ++h) {
+        dot_(m, h, xs, nv, dv);
+        for (int v = 0; v < nv; ++v) dout_[static_cast<size_t>(rs[v]) * H + h] = rb(dv[v] * j.w[rs[v]]);
+      }
+    });
+    // pass 3: each token's routes summed in route order
+    parallel(j.M, [&](int t) {
+      bf16* y = j.y + static_cast<size_t>(t) * H;
+      for (int h = 0; h < H; ++h) {
         float s = 0.f;
-        for (int q = 0; q < j.k; ++q) {
-          const int r = t * j.k + q;
-          if (!valid(r)) continue;
-          const Mat m = rowmat(dn, dn_rows, j.ids[r]);
-          s += rb(dot_(m, h, act_.data() + static_cast<size_t>(r) * I) * j.w[r]);
-        }
-        j.y[static_cast<size_t>(t) * H + h] = f2b(s);
+        for (int q = 0; q < j.k; ++q)
+          if (valid(t * j.k + q)) s += dout_[static_cast<size_t>(t * j.k + q) * H + h];
+        y[h] = f2b(s);
       }
     });
   }
@@ -353,7 +452,8 @@ class Executor {
   uint64_t gen_ = 0;
   std::atomic<int> next_{0};
   bool stop_ = false;
-  std::vector<float> xf_, act_;
+  std::vector<float> xf_, act_, dout_;
+  std::vector<int> order_, group_;
 };
 
 void host_start(void* p) {

@@ -84,3 +84,19 @@ def test_cpu_experts_validation(executor):
 
 def test_executor_reports_isa(executor):
     assert executor.isa in ("avx512f", "scalar")
+
+
+def test_cpu_experts_hot_experts(executor):
+    """More routes on one expert than one weight pass takes (split groups)."""
+    rng = np.random.default_rng(9)
+    E, H, I, M, k = 4, 256, 256, 11, 2
+    bank = synth.make_bank("fp8", E, H, I, rng)
+    x = synth.activations(rng, M, H)
+    ids = np.tile(np.array([[1, 3]], dtype=np.int32), (M, 1))
+    ids[4] = [3, 1]
+    w = rng.uniform(0.1, 1.0, size=(M, k)).astype(np.float32)
+    y_ref = oracle.experts.moe_layer("decode", x, w, ids, bank, None)
+    y = executor.run(to_device_bank(bank, "cpu"), _host(x, np.float32).to(torch.bfloat16), _host(w, np.float32),
+                     _host(ids, np.int32))
+    g = y.float().numpy()
+    assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, max_rel(g, y_ref)
