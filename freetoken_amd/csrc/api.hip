@@ -308,6 +308,47 @@ int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layer
   return check_hip(ftmoe::launch_lru_ensure(a, stream), "lru_ensure launch");
 }
 
+int ftmoe_materialize_layer(int layer_id, int num_layers, int num_experts, int32_t* slot_for_id, int32_t* id_of_slot,
+                            int64_t* usage, int64_t* step, int cache_size, int32_t* evict_slots,
+                            int32_t* src_indices, int32_t* num_indices, ftmoe_stream_t stream) {
+  if (!slot_for_id || !id_of_slot || !usage || !step || !evict_slots || !src_indices || !num_indices)
+    return fail(FTMOE_ERR_INVALID, "materialize_layer: NULL pointer");
+  if (num_experts <= 0 || cache_size < num_experts || num_layers <= 0 || layer_id < 0 || layer_id >= num_layers ||
+      static_cast<long long>(num_layers) * num_experts > (1ll << 30))
+    return fail(FTMOE_ERR_UNSUPPORTED, "materialize_layer: E=%d S=%d layer=%d/%d (needs S >= E)", num_experts,
+                cache_size, layer_id, num_layers);
+  ftmoe::PlaceArgs a{};
+  a.layer = layer_id;
+  a.num_layers = num_layers;
+  a.num_experts = num_experts;
+  a.cache_size = cache_size;
+  a.slot_for_id = slot_for_id;
+  a.id_of_slot = id_of_slot;
+  a.usage = usage;
+  a.step = step;
+  a.evict_slots = evict_slots;
+  a.src_indices = src_indices;
+  a.num_indices = num_indices;
+  return check_hip(ftmoe::launch_materialize_layer(a, stream), "materialize_layer launch");
+}
+
+int ftmoe_release_slots(int slot_begin, int slot_end, int num_layers, int num_experts, int32_t* slot_for_id,
+                        int32_t* id_of_slot, int64_t* usage, int cache_size, ftmoe_stream_t stream) {
+  if (!slot_for_id || !id_of_slot || !usage) return fail(FTMOE_ERR_INVALID, "release_slots: NULL pointer");
+  if (slot_begin < 0 || slot_end < slot_begin || slot_end > cache_size || num_layers <= 0 || num_experts <= 0)
+    return fail(FTMOE_ERR_UNSUPPORTED, "release_slots: [%d, %d) of %d slots", slot_begin, slot_end, cache_size);
+  ftmoe::PlaceArgs a{};
+  a.num_layers = num_layers;
+  a.num_experts = num_experts;
+  a.cache_size = cache_size;
+  a.slot_for_id = slot_for_id;
+  a.id_of_slot = id_of_slot;
+  a.usage = usage;
+  a.slot_begin = slot_begin;
+  a.slot_end = slot_end;
+  return check_hip(ftmoe::launch_release_slots(a, stream), "release_slots launch");
+}
+
 int ftmoe_fetch_experts(const ftmoe_fetch_bank* banks, int nbanks, const int32_t* evict_slots,
                         const int32_t* src_indices, const int32_t* num_indices, int max_entries,
                         ftmoe_stream_t stream) {

@@ -221,6 +221,70 @@ hipError_t launch_lru_ensure(const LruArgs& a, hipStream_t stream) {
 }
 
 // ----------------------------------------------------------------------------
+// Whole-layer placement for the prefill (reference: _materialize_layer_kernel,
+// moe/offload_kernels.py:250-281): expert e of the layer goes to slot e.  Slots
+// holding this layer's experts are emptied (usage 0: the next victims); the
+// other layers' experts in slots [0, E) lose their mapping; step += 1; slots
+// [0, E) get this layer's experts with usage = step and are listed as the
+// entries (e -> e) of the gather.  Every slot is read before it is written by
+// the same thread, and the slot_for_id rows written (other layers' unmaps,
+// this layer's map) are disjoint, so one pass suffices.
+// ----------------------------------------------------------------------------
+__global__ void __launch_bounds__(kLruThreads) materialize_layer_kernel(PlaceArgs a) {
+  const int E = a.num_experts, tid = threadIdx.x;
+  const int base = a.layer * E;
+  const long long step = a.step[0] + 1;
+  for (int s = tid; s < a.cache_size; s += kLruThreads) {
+    const int old = a.id_of_slot[s];
+    const bool same = old >= base && old < base + E;
+    if (same) {
+      a.id_of_slot[s] = -1;
+      a.usage[s] = 0;
+    } else if (s < E && old >= 0 && old < a.num_layers * E) {
+      a.slot_for_id[old] = -1;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kLruThreads) {
+    a.id_of_slot[e] = base + e;
+    a.slot_for_id[base + e] = e;
+    a.usage[e] = step;
+    a.evict_slots[e] = e;
+    a.src_indices[e] = e;
+  }
+  if (tid == 0) {
+    a.step[0] = step;
+    a.num_indices[0] = E;
+  }
+}
+
+// Release of slots [slot_begin, slot_end) (reference: _invalidate_prefill_buffer,
+// moe/offload_cache.py:592-600): their experts lose their mapping, the slots
+// become empty with usage 0.
+__global__ void __launch_bounds__(kLruThreads) release_slots_kernel(PlaceArgs a) {
+  for (int s = a.slot_begin + static_cast<int>(blockIdx.x * kLruThreads + threadIdx.x); s < a.slot_end;
+       s += static_cast<int>(gridDim.x * kLruThreads)) {
+    const int old = a.id_of_slot[s];
+    if (old >= 0 && old < a.num_layers * a.num_experts) a.slot_for_id[old] = -1;
+    a.id_of_slot[s] = -1;
+    a.usage[s] = 0;
+  }
+}
+
+hipError_t launch_materialize_layer(const PlaceArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL(materialize_layer_kernel, dim3(1), dim3(kLruThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_release_slots(const PlaceArgs& a, hipStream_t stream) {
+  const int n = a.slot_end - a.slot_begin;
+  if (n <= 0) return hipSuccess;
+  const int blocks = (n + kLruThreads - 1) / kLruThreads;
+  hipLaunchKernelGGL(release_slots_kernel, dim3(blocks), dim3(kLruThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+// ----------------------------------------------------------------------------
 // Gather of admitted experts: entry i copies row src_indices[i] of every host
 // bank to row evict_slots[i] of the matching slot bank, for i < num_indices[0]
 // (reference: fast_index_copy_multi over the banks of copy_missing,

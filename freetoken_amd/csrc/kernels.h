@@ -155,6 +155,21 @@ struct LruArgs {
   long long* stats;       // nullable [4] accumulated: active, missing, calls, missed routes
 };
 hipError_t launch_lru_ensure(const LruArgs& a, hipStream_t stream);
+
+// Whole-layer placement and slot release of the prefill movement.
+struct PlaceArgs {
+  int layer, num_layers, num_experts, cache_size;
+  int32_t* slot_for_id;  // [num_layers * num_experts]
+  int32_t* id_of_slot;   // [cache_size]
+  int64_t* usage;        // [cache_size]
+  int64_t* step;         // [1] (materialize)
+  int32_t* evict_slots;  // [num_experts] (materialize)
+  int32_t* src_indices;  // [num_experts] (materialize)
+  int32_t* num_indices;  // [1] (materialize)
+  int slot_begin, slot_end;  // release range
+};
+hipError_t launch_materialize_layer(const PlaceArgs& a, hipStream_t stream);
+hipError_t launch_release_slots(const PlaceArgs& a, hipStream_t stream);
 size_t lru_lds_bytes(int num_experts, int cache_size, int sort_len);
 
 constexpr int kMaxFetchBanks = 8;

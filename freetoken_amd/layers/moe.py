@@ -233,8 +233,26 @@ class OffloadMoELayer(MoELayer):
         return shared + dec.decode_sync(pending)
 
     def _prefill_routed(self, hidden_states, topk_weights, topk_ids) -> torch.Tensor:
+        """Prefill movement (reference ``:374-423``): with the double buffer,
+        layer l+1's host copy is started behind this layer's GEMMs; with host
+        sources and no overlap, the layer is materialized at slot == expert id
+        and gathered first; otherwise the first E slots are taken to hold the
+        layer.  In all cases position == expert id, so the ids pass unmapped."""
         cache = self.offload_cache
         assert cache is not None
+        if cache.prefill_overlap:
+            if self.layer_id == 0:
+                cache.begin_prefill()
+            cache.prefetch_prefill_layer(self.layer_id)
+            cache.prefetch_prefill_layer(self.layer_id + 1)
+            bank = self._views_bank(cache.wait_prefill_layer(self.layer_id))
+            out = ops.experts_prefill(hidden_states, topk_weights, topk_ids, bank, shared=self.shared_expert,
+                                      activation=self.activation)
+            cache.release_prefill_layer(self.layer_id)
+            return out
+        if cache.sources:
+            cache.materialize_layer(self.layer_id)
+            cache.copy_missing()
         bank = self._views_bank(cache.bank_views(self.num_experts))
         return ops.experts_prefill(hidden_states, topk_weights, topk_ids, bank, shared=self.shared_expert,
                                    activation=self.activation)

@@ -44,7 +44,7 @@ def bank_from_views(quant_format: str, views) -> ops.ExpertBank:
 class ExpertSlotCache:
     def __init__(self, num_layers: int, num_experts: int, cache_size: int, quant_format: str,
                  device: torch.device | str = "cuda", decode_target: str = "gpu", hybrid_max_fetch: int = 1,
-                 hybrid_fetch_fraction: float = 0.0):
+                 hybrid_fetch_fraction: float = 0.0, prefill_overlap: bool = False):
         assert quant_format in ("bf16", "fp8_block", "ds_fp4"), quant_format
         assert decode_target in ("gpu", "cpu", "hybrid"), decode_target
         # decode placement (moe/offload_cache.py:117-136): "gpu" fetches every
@@ -56,6 +56,18 @@ class ExpertSlotCache:
         self.hybrid_fetch_fraction = hybrid_fetch_fraction
         self.cpu_executor = None
         self.cpu_layer_ids: frozenset = frozenset()
+        # prefill movement (:563-798): with prefill_overlap two full-layer
+        # buffers borrow slots [0, 2E) and layer l+1's host copy runs on a copy
+        # stream behind layer l's GEMMs; otherwise materialize_layer stages the
+        # layer into slots [0, E) before its GEMMs
+        assert not prefill_overlap or cache_size >= 2 * num_experts, \
+            "prefill overlap borrows two expert layers of slots: cache_size >= 2 * num_experts"
+        self.prefill_overlap = prefill_overlap
+        self._pf_views: list[torch.Tensor] | None = None
+        self._pf_layer: list[int | None] = [None, None]
+        self._pf_released = [True, True]
+        self._pf_has_release = [False, False]
+        self.prefill_copy_stream = None
         self.num_layers = num_layers
         self.num_experts = num_experts
         self.cache_size = cache_size
@@ -97,6 +109,7 @@ class ExpertSlotCache:
             for t in layers:
                 assert t.device.type == "cpu" and t.is_pinned() and t.is_contiguous(), name
                 assert t.shape[0] == self.num_experts and t.shape[1:] == self.banks[name].shape[1:], (name, t.shape)
+                assert t.element_size() == self.banks[name].element_size(), (name, t.dtype, self.banks[name].dtype)
         self.sources = OrderedDict((name, list(sources[name])) for name in self.banks)
 
     def set_cpu_executor(self, executor) -> None:
@@ -187,6 +200,83 @@ class ExpertSlotCache:
         assert layer_id is not None, "no staged misses (ensure_experts first)"
         ops.fetch_experts([layers[layer_id] for layers in self.sources.values()], list(self.banks.values()),
                           self.evict_slots, self.src_indices, self.num_indices)
+
+    def materialize_layer(self, layer_id: int) -> None:
+        """Stages the whole layer at slot == expert id for a prefill
+        (``:833-838``); ``copy_missing`` then moves it over PCIe."""
+        assert self.cache_size >= self.num_experts, "materialize needs cache_size >= num_experts"
+        ops.materialize_layer(layer_id, self.slot_for_id, self.id_of_slot, self.usage, self.step, self.evict_slots,
+                              self.src_indices, self.num_indices)
+        self._pending_src_layer = layer_id
+
+    # -------------------------------------------------------------- prefill double buffer
+    def _prefill_buffers(self) -> list[torch.Tensor]:
+        if self._pf_views is None:
+            assert self.sources, "set_bank_sources must register the host banks first"
+            E = self.num_experts
+            self._pf_views = [t[: 2 * E].view(2, E, *t.shape[1:]) for t in self.banks.values()]
+            self.prefill_copy_stream = torch.cuda.Stream(device=self.device)
+            self._pf_ready = [torch.cuda.Event() for _ in range(2)]
+            self._pf_release = [torch.cuda.Event() for _ in range(2)]
+            self._pf_begin = torch.cuda.Event()
+        return self._pf_views
+
+    def begin_prefill(self) -> None:
+        """Fences the copy stream behind the work already queued on the current
+        stream (a running decode may read the slots the buffers borrow; :602-624)."""
+        if not self.prefill_overlap:
+            return
+        self._prefill_buffers()
+        self._pf_layer = [None, None]
+        self._pf_released = [True, True]
+        self._pf_begin.record(torch.cuda.current_stream(self.device))
+        self.prefill_copy_stream.wait_event(self._pf_begin)
+
+    def prefetch_prefill_layer(self, layer_id: int) -> None:
+        """Starts the host copy of a whole layer into buffer ``layer_id % 2`` on
+        the copy stream, after that buffer's previous layer was released; the
+        buffer's slots are emptied first (``:625-658``)."""
+        if not self.prefill_overlap or layer_id >= self.num_layers:
+            return
+        if layer_id < 0:
+            raise ValueError(f"invalid prefill layer id {layer_id}")
+        buf = layer_id % 2
+        if self._pf_layer[buf] == layer_id:
+            return
+        assert self._pf_layer[buf] is None or self._pf_released[buf], "prefill buffer reused before release"
+        views = self._prefill_buffers()
+        E = self.num_experts
+        with torch.cuda.stream(self.prefill_copy_stream):
+            if self._pf_has_release[buf]:
+                self.prefill_copy_stream.wait_event(self._pf_release[buf])
+            ops.release_slots(buf * E, (buf + 1) * E, self.slot_for_id, self.id_of_slot, self.usage)
+            for layers, v in zip(self.sources.values(), views):  # bytes, whatever the dtypes
+                v[buf].view(torch.uint8).copy_(layers[layer_id].view(torch.uint8), non_blocking=True)
+            self._pf_ready[buf].record(self.prefill_copy_stream)
+        self._pf_layer[buf] = layer_id
+        self._pf_released[buf] = False
+
+    def wait_prefill_layer(self, layer_id: int) -> tuple[torch.Tensor, ...]:
+        """The layer's full ``[E, ...]`` bank views, the current stream made to
+        wait for their copy (``:775-787``)."""
+        assert self.prefill_overlap
+        self.prefetch_prefill_layer(layer_id)
+        buf = layer_id % 2
+        assert self._pf_layer[buf] == layer_id
+        torch.cuda.current_stream(self.device).wait_event(self._pf_ready[buf])
+        return tuple(v[buf] for v in self._pf_views)
+
+    def release_prefill_layer(self, layer_id: int) -> None:
+        """Marks the layer's buffer free once the current stream's work queued so
+        far (its GEMMs) is done (``:789-798``)."""
+        if not self.prefill_overlap:
+            return
+        buf = layer_id % 2
+        if self._pf_layer[buf] != layer_id:
+            return
+        self._pf_release[buf].record(torch.cuda.current_stream(self.device))
+        self._pf_has_release[buf] = True
+        self._pf_released[buf] = True
 
     def slot_lookup(self, layer_id: int) -> tuple[torch.Tensor, torch.Tensor | None]:
         """(slot table, stats counters or None) of a layer, for decode calls that

@@ -164,6 +164,39 @@ def lru_ensure(expert_ids: torch.Tensor, layer_id: int, slot_for_id: torch.Tenso
     return expert_ids
 
 
+def materialize_layer(layer_id: int, slot_for_id: torch.Tensor, id_of_slot: torch.Tensor, usage: torch.Tensor,
+                      step: torch.Tensor, evict_slots: torch.Tensor, src_indices: torch.Tensor,
+                      num_indices: torch.Tensor) -> None:
+    """Places every expert of ``layer_id`` at slot == expert id and stages the
+    whole layer for ``fetch_experts`` (see ftmoe_materialize_layer)."""
+    num_layers, num_experts = slot_for_id.shape
+    if evict_slots.numel() < num_experts or src_indices.numel() < num_experts:
+        raise ValueError("evict_slots / src_indices must hold num_experts entries")
+    for t in (slot_for_id, id_of_slot, evict_slots, src_indices, num_indices):
+        if t.dtype != torch.int32:
+            raise ValueError("tables, lists and count must be int32")
+    if usage.dtype != torch.int64 or step.dtype != torch.int64:
+        raise ValueError("usage and step must be int64")
+    _require_gpu(slot_for_id, id_of_slot, usage, step, evict_slots, src_indices, num_indices)
+    check(lib().ftmoe_materialize_layer(layer_id, num_layers, num_experts, _ptr(slot_for_id), _ptr(id_of_slot),
+                                        _ptr(usage), _ptr(step), id_of_slot.numel(), _ptr(evict_slots),
+                                        _ptr(src_indices), _ptr(num_indices), _stream(slot_for_id.device)),
+          "materialize_layer")
+
+
+def release_slots(slot_begin: int, slot_end: int, slot_for_id: torch.Tensor, id_of_slot: torch.Tensor,
+                  usage: torch.Tensor) -> None:
+    """Empties slots [slot_begin, slot_end) and unmaps their experts (see
+    ftmoe_release_slots)."""
+    num_layers, num_experts = slot_for_id.shape
+    if slot_for_id.dtype != torch.int32 or id_of_slot.dtype != torch.int32 or usage.dtype != torch.int64:
+        raise ValueError("slot tables int32, usage int64")
+    _require_gpu(slot_for_id, id_of_slot, usage)
+    check(lib().ftmoe_release_slots(slot_begin, slot_end, num_layers, num_experts, _ptr(slot_for_id),
+                                    _ptr(id_of_slot), _ptr(usage), id_of_slot.numel(), _stream(slot_for_id.device)),
+          "release_slots")
+
+
 def fetch_experts(host_rows, slot_banks, evict_slots: torch.Tensor, src_indices: torch.Tensor,
                   num_indices: torch.Tensor, max_entries: int | None = None) -> None:
     """Copies the admitted experts' rows from pinned host tensors (one per

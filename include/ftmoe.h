@@ -146,6 +146,24 @@ int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layer
                      int32_t* src_indices, int capacity, int32_t* num_indices, int32_t* num_missing,
                      int32_t* cpu_ids, int64_t* stats, ftmoe_stream_t stream);
 
+/* Whole-layer placement of the prefill movement: replaces materialize_layer
+ * (moe/offload_cache.py:833-838, _materialize_layer_kernel,
+ * moe/offload_kernels.py:250-281).  Expert e of layer_id goes to slot e:
+ * slots holding this layer's experts are emptied (usage 0); other layers'
+ * experts in slots [0, num_experts) lose their mapping; step += 1; slots
+ * [0, num_experts) map to the layer with usage = step; evict_slots /
+ * src_indices (int32 [num_experts]) = 0..E-1 and num_indices = E, the
+ * entries of a following ftmoe_fetch_experts.  cache_size >= num_experts. */
+int ftmoe_materialize_layer(int layer_id, int num_layers, int num_experts, int32_t* slot_for_id, int32_t* id_of_slot,
+                            int64_t* usage, int64_t* step, int cache_size, int32_t* evict_slots,
+                            int32_t* src_indices, int32_t* num_indices, ftmoe_stream_t stream);
+
+/* Release of slots [slot_begin, slot_end): replaces the prefill double
+ * buffer's _invalidate_prefill_buffer (moe/offload_cache.py:592-600): the
+ * experts held there lose their mapping; the slots become empty, usage 0. */
+int ftmoe_release_slots(int slot_begin, int slot_end, int num_layers, int num_experts, int32_t* slot_for_id,
+                        int32_t* id_of_slot, int64_t* usage, int cache_size, ftmoe_stream_t stream);
+
 /* One bank of the gather below: this layer's expert rows in pinned host
  * memory ([num_experts, row_bytes]) and the slot bank ([cache_size,
  * row_bytes]) on the device. */

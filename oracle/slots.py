@@ -97,6 +97,48 @@ def hybrid_split(raw_ids, slot_ids, num_experts: int):
     return np.where(valid & (np.asarray(slot_ids) < 0), raw, -1).astype(np.int32)
 
 
+def materialize_layer(state: CacheState, layer: int):
+    """Whole-layer placement (``_materialize_layer_kernel``,
+    ``moe/offload_kernels.py:250-281``): slots holding this layer's experts
+    are emptied (usage 0), other layers' experts in slots [0, E) lose their
+    mapping, step += 1, and expert e takes slot e with usage = step.  Returns
+    the gather entries (evict_slots, src_indices) = (0..E-1, 0..E-1).
+
+    Pinned (tests/test_oracle_slots.py) by invariants: tables stay inverse,
+    position == expert id for the layer, untouched experts of other layers
+    keep their slots, freed slots are the next LRU victims."""
+    E, S = state.E, state.S
+    assert S >= E, "materialize needs cache_size >= num_experts"
+    base = layer * E
+    flat = state.slot_for_id.reshape(-1)
+    old = state.id_of_slot.copy()
+    for s in range(S):
+        o = int(old[s])
+        if base <= o < base + E:
+            state.id_of_slot[s] = -1
+            state.usage[s] = 0
+        elif s < E and o >= 0:
+            flat[o] = -1
+    state.step += 1
+    for e in range(E):
+        state.id_of_slot[e] = base + e
+        flat[base + e] = e
+        state.usage[e] = state.step
+    return np.arange(E, dtype=np.int32), np.arange(E, dtype=np.int32)
+
+
+def release_slots(state: CacheState, begin: int, end: int) -> None:
+    """Empties slots [begin, end) and unmaps their experts (the prefill double
+    buffer's ``_invalidate_prefill_buffer``, ``moe/offload_cache.py:592-600``)."""
+    flat = state.slot_for_id.reshape(-1)
+    for s in range(begin, end):
+        o = int(state.id_of_slot[s])
+        if o >= 0:
+            flat[o] = -1
+        state.id_of_slot[s] = -1
+        state.usage[s] = 0
+
+
 def lru_ensure(state: CacheState, layer: int, expert_ids, max_fetch: int = -1, by_recency: bool = False,
                capacity: int | None = None, frac_q16: int = 0):
     """One admission call (``moe/offload_kernels.py:128-188``); mutates ``state``.

@@ -148,3 +148,36 @@ def test_fraction_cap_admission_and_split():
         assert ((cpu >= 0) == (out < 0)).all() and (cpu[cpu >= 0] == ids[cpu >= 0]).all()
         assert _inverse_ok(st)
     assert S.hybrid_split([-1, 40, 3], [-1, -1, -1], 32).tolist() == [-1, -1, 3]
+
+
+def test_materialize_layer_invariants():
+    """Position == expert id for the layer; the tables stay inverse; experts of
+    other layers outside [0, E) keep their slots; the layer's old slots are
+    freed (usage 0) and are the next LRU victims."""
+    L, E, Sz = 3, 8, 20
+    st = S.CacheState(L, E, Sz)
+    S.lru_ensure(st, 1, list(range(8)))          # layer 1 fills slots 0..7
+    S.lru_ensure(st, 2, [0, 1, 2])               # layer 2 in 8..10
+    S.lru_ensure(st, 0, [5, 6])                  # layer 0 in 11..12
+    before = st.copy()
+    evict, src = S.materialize_layer(st, 0)
+    assert evict.tolist() == list(range(E)) and src.tolist() == list(range(E))
+    assert st.slot_for_id[0].tolist() == list(range(E)) and _inverse_ok(st)
+    assert (st.slot_for_id[1] == -1).all()       # evicted from slots 0..7
+    assert st.slot_for_id[2].tolist()[:3] == before.slot_for_id[2].tolist()[:3]  # untouched
+    assert st.id_of_slot[11] == -1 and st.id_of_slot[12] == -1 and st.usage[11] == 0 and st.usage[12] == 0
+    assert st.step == before.step + 1 and (st.usage[:E] == st.step).all()
+    # the freed slots (and the never-used ones) are taken first by the next admission
+    _, ev, _, _, _ = S.lru_ensure(st, 2, [7])
+    assert ev.tolist() == [11]
+
+
+def test_release_slots_unmaps():
+    st = S.CacheState(2, 8, 16)
+    S.lru_ensure(st, 0, list(range(8)))
+    S.lru_ensure(st, 1, [3, 4])
+    S.release_slots(st, 4, 9)
+    assert _inverse_ok(st)
+    assert (st.id_of_slot[4:9] == -1).all() and (st.usage[4:9] == 0).all()
+    assert st.slot_for_id[0].tolist() == [0, 1, 2, 3, -1, -1, -1, -1]
+    assert st.slot_for_id[1, 3] == -1 and st.slot_for_id[1, 4] == 9
