@@ -429,6 +429,78 @@ def run_hybrid(gen, dev, M: int = 1, n_sets: int = 4, slots: int = 8, max_fetch:
                 cpu_threads=threads, cpu_isa=isa)
 
 
+def run_prefill_offload(gen, dev, L: int = 3, E: int = 32, M: int = 8192, reps: int = 2):
+    """Prefill movement of the expert cache at C4 expert shape (FP8), L layers
+    of E experts each held only in pinned host memory, M tokens routed top-8
+    uniformly: per-layer time of (a) materialize + PCIe gather + experts, one
+    after the other, and (b) the double buffer, layer l+1's host copy on a copy
+    stream behind layer l's experts.  E is reduced from 256 so that L layers
+    of host banks stay a few GB."""
+    from freetoken_amd.core import moe_phase
+    from freetoken_amd.layers.moe import OffloadMoELayer
+    from freetoken_amd.moe.offload_cache import ExpertSlotCache
+
+    c = C4
+    H, I, k = c["H"], c["I"], c["k"]
+    shapes = {"gate_up": (2 * I, H), "gate_up_scale": (2 * I // 128, H // 128), "down": (H, I),
+              "down_scale": (H // 128, I // 128)}
+    host = {n: [] for n in shapes}
+    for _ in range(L):
+        for name, shape in shapes.items():
+            if name.endswith("scale"):
+                d = torch.rand((E,) + shape, generator=gen, device=dev) * 1e-3 + 1e-4
+            else:
+                d = torch.randint(0, 256, (E,) + shape, generator=gen, device=dev, dtype=torch.uint8)
+                d[(d & 0x7F) == 0x7F] = 0
+            h = torch.empty(d.shape, dtype=d.dtype, pin_memory=True)
+            h.copy_(d)
+            host[name].append(h)
+            del d
+    layer_bytes = sum(int(h[0].numel()) * h[0].element_size() for h in host.values())
+    x = torch.randn((M, H), generator=gen, device=dev).to(torch.bfloat16)
+    w, ids = ops.route_softmax_topk(torch.randn((M, E), generator=gen, device=dev), k, True)
+    res = {"layers": L, "experts_per_layer": E, "tokens": M, "layer_bytes": layer_bytes}
+    for overlap in (False, True):
+        S = 2 * E if overlap else E
+        cache = ExpertSlotCache(L, E, S, "fp8_block", device=dev, prefill_overlap=overlap)
+        cache.set_bank_caches(**{n: torch.zeros((S,) + h[0].shape[1:], dtype=h[0].dtype, device=dev)
+                                 for n, h in host.items()})
+        cache.set_bank_sources(host)
+        cache.reset()
+        layers = [OffloadMoELayer(l, E, k, H, I, device=dev) for l in range(L)]
+        for lay in layers:
+            lay.offload_cache = cache
+        times = []
+        with moe_phase("prefill", backend="offload"):
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                e0.record()
+                for lay in layers:
+                    lay.routed_forward(x, w, ids.clone())
+                e1.record()
+                torch.cuda.synchronize()
+                times.append(e0.elapsed_time(e1))
+        t = min(times) / L
+        key = "double_buffer" if overlap else "materialize"
+        res[f"{key}_ms_per_layer"] = t
+        res[f"{key}_gbs"] = layer_bytes / (t * 1e-3) / 1e9
+        del cache, layers
+        torch.cuda.empty_cache()
+    # the experts alone on resident banks, for the overlap bound
+    bank = ops.ExpertBank("fp8_block", *(h[0].to(dev) for h in (host["gate_up"], host["down"])),
+                          host["gate_up_scale"][0].to(dev), host["down_scale"][0].to(dev))
+    ops.experts_prefill(x, w, ids, bank)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    ops.experts_prefill(x, w, ids, bank)
+    e1.record()
+    torch.cuda.synchronize()
+    res["experts_ms"] = e0.elapsed_time(e1)
+    return res
+
+
 def cpu_baseline(layer: DecodeLayer, M: int, budget_s: float, gen, dev):
     """C++ restatement of the reference CPU executor on this host: the same C4
     routing (resident slots), bf16-dequantised banks (the reference's CPU route
@@ -514,6 +586,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--miss-only", action="store_true", help="time the miss path (admission + PCIe gather) alone")
     ap.add_argument("--hybrid-only", action="store_true", help="time the hybrid CPU/GPU decode alone")
+    ap.add_argument("--prefill-offload-only", action="store_true",
+                    help="time the expert cache's prefill movement (materialize vs double buffer) alone")
     ap.add_argument("--prefill-only", choices=("fp8_block", "mxfp4"), default=None,
                     help="profiling aid: run only the C5 prefill of this format and print its result")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -539,6 +613,11 @@ def main() -> int:
 
     if args.miss_only:
         res = run_miss_fetch(gen, dev)
+        print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}), flush=True)
+        return 0
+
+    if args.prefill_offload_only:
+        res = run_prefill_offload(gen, dev)
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}), flush=True)
         return 0
 
@@ -589,6 +668,8 @@ def main() -> int:
             sweep[f"c5_prefill_8192_{fmt}"] = run_prefill(fmt, 10, 3, gen, dev)
         log("[bench] sweep C4 miss path (admission + PCIe gather of 8 experts per step)")
         sweep["c4_miss_fetch_8_experts"] = run_miss_fetch(gen, dev)
+        log("[bench] sweep C4 prefill movement (3 layers x 32 host-resident experts, 8192 tokens)")
+        sweep["c4_prefill_offload_3x32_experts"] = run_prefill_offload(gen, dev)
         log("[bench] sweep C4 hybrid decode (1 expert fetched per step, the other misses on the CPU)")
         sweep["c4_hybrid_b1"] = run_hybrid(gen, dev, M=1)
 
