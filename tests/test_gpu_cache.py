@@ -280,3 +280,48 @@ def test_offload_prefill_moves_layers(dev, overlap):
     torch.cuda.synchronize()
     if not overlap:  # the last layer stays materialized at slot == expert id
         np.testing.assert_array_equal(to_np(cache.slot_for_id)[L - 1], np.arange(E))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("per_layer", [True, False])
+def test_offload_layer_from_ftw_banks(dev, tmp_path, per_layer):
+    """Expert banks written as an FTW checkpoint (bf16 block scales, as the
+    reference's FP8 banks are stored), loaded into pinned host memory with the
+    scales widened, and served to an offload layer's decode through the miss
+    path: outputs equal the oracle on the same (bf16-rounded-scale) banks."""
+    from freetoken_amd.checkpoint import load_ftw_banks, save_ftw_banks
+    from oracle.numerics import bf16_round
+
+    rng = np.random.default_rng(107)
+    L, E, Sz, H, I, k, M = 2, 12, 6, 512, 256, 2, 3  # slots >= the distinct experts of a call
+    banks = [synth.make_bank("fp8", E, H, I, rng) for _ in range(L)]
+    for b in banks:
+        b.gate_up_scale = bf16_round(b.gate_up_scale)
+        b.down_scale = bf16_round(b.down_scale)
+    src = {
+        "gate_up": [torch.from_numpy(b.gate_up).view(torch.float8_e4m3fn) for b in banks],
+        "gate_up_scale": [torch.from_numpy(b.gate_up_scale).to(torch.bfloat16) for b in banks],
+        "down": [torch.from_numpy(b.down).view(torch.float8_e4m3fn) for b in banks],
+        "down_scale": [torch.from_numpy(b.down_scale).to(torch.bfloat16) for b in banks],
+    }
+    save_ftw_banks(str(tmp_path), "fp8_block", src, per_layer=per_layer, shard_limit=1 << 20)
+    fmt, sources, _ = load_ftw_banks(str(tmp_path), L)
+    assert fmt == "fp8_block" and all(t.is_pinned() for ts in sources.values() for t in ts)
+    cache = ExpertSlotCache(L, E, Sz, fmt, device=dev)
+    cache.set_bank_caches(**{n: torch.zeros((Sz,) + ts[0].shape[1:], dtype=ts[0].dtype, device=dev)
+                             for n, ts in sources.items()})
+    cache.set_bank_sources(sources)
+    cache.reset()
+    layers = [OffloadMoELayer(l, E, k, H, I, device=dev) for l in range(L)]
+    for lay in layers:
+        lay.offload_cache = cache
+    for call in range(4):
+        l = call % L
+        x = synth.activations(rng, M, H)
+        w_ref, ids_ref = oracle.routing.softmax_topk(synth.normal(rng, (M, E)), k, True)
+        y_ref = oracle.experts.moe_layer("decode", x, w_ref, ids_ref, banks[l], None)
+        with moe_phase("decode", backend="offload"):
+            y = layers[l].routed_forward(bf16_dev(x, dev), torch.from_numpy(w_ref).to(dev),
+                                         torch.from_numpy(ids_ref.copy()).to(dev))
+        g = to_np(y)
+        assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, (per_layer, call)
