@@ -26,6 +26,8 @@
 #include <condition_variable>
 #include <cstdint>
 #include <cstring>
+#include <type_traits>
+#include <cstdlib>
 #include <deque>
 #include <functional>
 #include <mutex>
@@ -229,6 +231,109 @@ void dot_avx512(const Mat& m, int n, const float* const* xs, int nx, float* out)
 
 static_assert(kMaxVec == 8, "dot_avx512_f dispatches 1..8 vectors");
 
+// AVX512-BF16: the activation vectors stay bf16 and vdpbf16ps multiplies 32
+// weight / activation pairs per instruction.  Every weight value is exact in
+// bf16 (FP8 and e2m1 values have at most 4 significant bits; FP8 goes through
+// the same fp16 shift as above, then fp32, then bf16 exactly), so the products
+// are the fp32 ones; only the summation order differs (pairs, then lanes).
+// The instruction treats bf16 subnormal inputs as zero: FP8 weights at 2^-8
+// scale are normal, activations that small contribute below bf16 resolution.
+__attribute__((target("avx512f,avx512bw,avx512bf16"))) inline __m512bh load_bh(const bf16* p) {
+  return (__m512bh)_mm512_loadu_si512(p);
+}
+
+template <int FMT, int NX>
+__attribute__((target("avx512f,avx512bw,avx512bf16"))) void dot_bf16_t(const Mat& m, int n, const bf16* const* xs,
+                                                                        float* out) {
+  constexpr int A = NX <= 4 ? 2 : 1;
+  __m512 acc[A][NX];
+#pragma unroll
+  for (int a = 0; a < A; ++a)
+#pragma unroll
+    for (int v = 0; v < NX; ++v) acc[a][v] = _mm512_setzero_ps();
+  if constexpr (FMT == FTMOE_FMT_BF16) {
+    const bf16* w = reinterpret_cast<const bf16*>(m.w) + static_cast<size_t>(n) * m.K;
+    for (int k = 0; k < m.K; k += 64) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const __m512bh wv = (__m512bh)_mm512_loadu_si512(w + k + 32 * c);
+#pragma unroll
+        for (int v = 0; v < NX; ++v) acc[c % A][v] = _mm512_dpbf16_ps(acc[c % A][v], wv, load_bh(xs[v] + k + 32 * c));
+      }
+    }
+  } else if constexpr (FMT == FTMOE_FMT_FP8_B128) {
+    const uint8_t* w = m.w + static_cast<size_t>(n) * m.K;
+    const float* s = static_cast<const float*>(m.s) + static_cast<size_t>(n / 128) * (m.K / 128);
+    const __m512i sgn = _mm512_set1_epi16(0x80), mag = _mm512_set1_epi16(0x7F);
+    for (int kb = 0; kb < m.K / 128; ++kb) {
+      __m512 part[A][NX];
+#pragma unroll
+      for (int a = 0; a < A; ++a)
+#pragma unroll
+        for (int v = 0; v < NX; ++v) part[a][v] = _mm512_setzero_ps();
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int k = kb * 128 + 32 * c;
+        const __m512i b = _mm512_cvtepu8_epi16(_mm256_loadu_si256(reinterpret_cast<const __m256i*>(w + k)));
+        const __m512i h = _mm512_or_si512(_mm512_slli_epi16(_mm512_and_si512(b, sgn), 8),
+                                          _mm512_slli_epi16(_mm512_and_si512(b, mag), 7));
+        const __m512bh wv = _mm512_cvtne2ps_pbh(_mm512_cvtph_ps(_mm512_extracti64x4_epi64(h, 1)),
+                                                _mm512_cvtph_ps(_mm512_castsi512_si256(h)));
+#pragma unroll
+        for (int v = 0; v < NX; ++v) part[c % A][v] = _mm512_dpbf16_ps(part[c % A][v], wv, load_bh(xs[v] + k));
+      }
+      const __m512 sc = _mm512_set1_ps(s[kb] * 256.0f);
+#pragma unroll
+      for (int v = 0; v < NX; ++v) {
+        const __m512 p = A == 2 ? _mm512_add_ps(part[0][v], part[A - 1][v]) : part[0][v];
+        acc[kb % A][v] = _mm512_fmadd_ps(p, sc, acc[kb % A][v]);
+      }
+    }
+  } else {
+    const uint8_t* w = m.w + static_cast<size_t>(n) * (m.K / 2);
+    const uint8_t* s = static_cast<const uint8_t*>(m.s) + static_cast<size_t>(n) * (m.K / 32);
+    // e2m1 -> bf16 bits, indexed by the code
+    alignas(64) static const uint16_t kLut[32] = {0x0000, 0x3F00, 0x3F80, 0x3FC0, 0x4000, 0x4040, 0x4080, 0x40C0,
+                                                  0x8000, 0xBF00, 0xBF80, 0xBFC0, 0xC000, 0xC040, 0xC080, 0xC0C0};
+    const __m512i lut = _mm512_load_si512(kLut);
+    for (int kb = 0; kb < m.K / 32; ++kb) {
+      // 16 bytes = 32 values; byte j holds k = 2j (low nibble) and 2j + 1, so
+      // (low | high << 16) per 32-bit lane is k order
+      const __m512i b = _mm512_cvtepu8_epi32(_mm_loadu_si128(reinterpret_cast<const __m128i*>(w + kb * 16)));
+      const __m512i idx = _mm512_or_si512(_mm512_and_si512(b, _mm512_set1_epi32(15)),
+                                          _mm512_slli_epi32(_mm512_srli_epi32(b, 4), 16));
+      const __m512bh wv = (__m512bh)_mm512_permutexvar_epi16(idx, lut);
+      const __m512 sc = _mm512_set1_ps(std::ldexp(1.0f, static_cast<int>(s[kb]) - 127));
+#pragma unroll
+      for (int v = 0; v < NX; ++v)
+        acc[kb % A][v] = _mm512_fmadd_ps(_mm512_dpbf16_ps(_mm512_setzero_ps(), wv, load_bh(xs[v] + kb * 32)), sc, acc[kb % A][v]);
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < NX; ++v)
+    out[v] = _mm512_reduce_add_ps(A == 2 ? _mm512_add_ps(acc[0][v], acc[A - 1][v]) : acc[0][v]);
+}
+
+template <int FMT>
+void dot_bf16_f(const Mat& m, int n, const bf16* const* xs, int nx, float* out) {
+  switch (nx) {
+    case 1: return dot_bf16_t<FMT, 1>(m, n, xs, out);
+    case 2: return dot_bf16_t<FMT, 2>(m, n, xs, out);
+    case 3: return dot_bf16_t<FMT, 3>(m, n, xs, out);
+    case 4: return dot_bf16_t<FMT, 4>(m, n, xs, out);
+    case 5: return dot_bf16_t<FMT, 5>(m, n, xs, out);
+    case 6: return dot_bf16_t<FMT, 6>(m, n, xs, out);
+    case 7: return dot_bf16_t<FMT, 7>(m, n, xs, out);
+    default: return dot_bf16_t<FMT, 8>(m, n, xs, out);
+  }
+}
+
+void dot_bf16(const Mat& m, int n, const bf16* const* xs, int nx, float* out) {
+  if (m.format == FTMOE_FMT_BF16) return dot_bf16_f<FTMOE_FMT_BF16>(m, n, xs, nx, out);
+  if (m.format == FTMOE_FMT_FP8_B128) return dot_bf16_f<FTMOE_FMT_FP8_B128>(m, n, xs, nx, out);
+  dot_bf16_f<FTMOE_FMT_MXFP4>(m, n, xs, nx, out);
+}
+
 using dot_fn = void (*)(const Mat&, int, const float* const*, int, float*);
 
 float silu(float g) { return g / (1.0f + std::exp(-g)); }
@@ -255,12 +360,17 @@ class Executor {
  public:
   explicit Executor(int threads) : nthreads_(threads < 1 ? 1 : threads) {
     dot_ = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") ? dot_avx512 : dot_scalar;
+    const char* want = std::getenv("FTMOE_CPU_DOT");  // "fp32" keeps the fp32 dots (measurement)
+    bf16_dot_ = dot_ == dot_avx512 && __builtin_cpu_supports("avx512bf16") && !(want && !std::strcmp(want, "fp32"));
     for (int t = 0; t < nthreads_; ++t) workers_.emplace_back([this] { worker(); });
     driver_ = std::thread([this] { drive(); });
   }
   ~Executor() {
     {
-      std::lock_guard<std::mutex> g(m_);
+      // queued and running jobs finish first: a worker leaving mid-pass would
+      // leave the driver waiting for it
+      std::unique_lock<std::mutex> g(m_);
+      cv_done_.wait(g, [this] { return queue_.empty() && !busy_; });
       stop_ = true;
     }
     cv_job_.notify_all();
@@ -269,7 +379,7 @@ class Executor {
     for (auto& t : workers_) t.join();
     for (Job* j : jobs_) delete j;
   }
-  const char* isa() const { return dot_ == dot_avx512 ? "avx512f" : "scalar"; }
+  const char* isa() const { return bf16_dot_ ? "avx512bf16" : dot_ == dot_avx512 ? "avx512f" : "scalar"; }
 
   Job* new_job(bool permanent) {
     std::lock_guard<std::mutex> g(m_);
@@ -293,6 +403,11 @@ class Executor {
       queue_.push_back(j);
     }
     cv_job_.notify_all();
+  }
+  // a job record that was never started goes back to the free list
+  void discard(Job* j) {
+    std::lock_guard<std::mutex> g(m_);
+    if (!j->permanent) free_.push_back(j);
   }
   // host node: block until the job is done; recycle it unless a graph holds it
   void finish(Job* j) {
@@ -349,16 +464,27 @@ class Executor {
         if (stop_) return;
         j = queue_.front();
         queue_.pop_front();
+        busy_ = true;
       }
       compute(*j);
       {
         std::lock_guard<std::mutex> g(m_);
         j->done = true;
+        busy_ = false;
       }
       cv_done_.notify_all();
     }
   }
   void compute(const Job& j) {
+    if (bf16_dot_) compute_t<true>(j);
+    else compute_t<false>(j);
+  }
+
+  // BF: the activation vectors are bf16 (the input rows and a bf16 act) for
+  // the bf16 dot; otherwise fp32 copies for the fp32 dots
+  template <bool BF>
+  void compute_t(const Job& j) {
+    using X = std::conditional_t<BF, bf16, float>;
     const int H = j.bank.hidden, I = j.bank.inter, R = j.M * j.k;
     const Mat gu{j.bank.format, H, static_cast<const uint8_t*>(j.bank.gate_up), j.bank.gate_up_scale};
     const Mat dn{j.bank.format, I, static_cast<const uint8_t*>(j.bank.down), j.bank.down_scale};
@@ -386,9 +512,19 @@ class Executor {
         group_.push_back(static_cast<int>(i));
     const int G = static_cast<int>(group_.size());
     group_.push_back(static_cast<int>(order_.size()));
-    xf_.resize(static_cast<size_t>(j.M) * H);
-    for (size_t i = 0; i < xf_.size(); ++i) xf_[i] = b2f(j.x[i]);
-    act_.resize(static_cast<size_t>(R) * I);
+    if constexpr (!BF) {
+      xf_.resize(static_cast<size_t>(j.M) * H);
+      for (size_t i = 0; i < xf_.size(); ++i) xf_[i] = b2f(j.x[i]);
+      act_.resize(static_cast<size_t>(R) * I);
+    } else {
+      act16_.resize(static_cast<size_t>(R) * I);
+    }
+    const X* const xin = BF ? reinterpret_cast<const X*>(j.x) : reinterpret_cast<const X*>(xf_.data());
+    X* const act = BF ? reinterpret_cast<X*>(act16_.data()) : reinterpret_cast<X*>(act_.data());
+    const auto dot = [&](const Mat& m, int n, const X* const* xs, int nv, float* o) {
+      if constexpr (BF) dot_bf16(m, n, xs, nv, o);
+      else dot_(m, n, xs, nv, o);
+    };
     dout_.resize(static_cast<size_t>(R) * H);
     constexpr int kTile = 32;
     // pass 1: gate and up rows of (group, 32 rows of I) -> bf16 act
@@ -398,17 +534,18 @@ class Executor {
       const int* rs = order_.data() + group_[g];
       const int nv = group_[g + 1] - group_[g];
       const Mat m = rowmat(gu, gu_rows, j.ids[rs[0]]);
-      const float* xs[kMaxVec];
-      for (int v = 0; v < nv; ++v) xs[v] = xf_.data() + static_cast<size_t>(rs[v] / j.k) * H;
+      const X* xs[kMaxVec];
+      for (int v = 0; v < nv; ++v) xs[v] = xin + static_cast<size_t>(rs[v] / j.k) * H;
       float gv[kMaxVec], uv[kMaxVec];
       for (int i = i0; i < i0 + kTile; ++i) {
-        dot_(m, i, xs, nv, gv);
-        dot_(m, I + i, xs, nv, uv);
+        dot(m, i, xs, nv, gv);
+        dot(m, I + i, xs, nv, uv);
         for (int v = 0; v < nv; ++v) {
           const float g = rb(gv[v]), up = rb(uv[v]);
           const float a = j.activation == FTMOE_ACT_SILU ? silu(g) : j.activation == FTMOE_ACT_GELU ? gelu(g)
                                                                                                   : gelu_tanh(g);
-          act_[static_cast<size_t>(rs[v]) * I + i] = rb(a * up);
+          if constexpr (BF) act[static_cast<size_t>(rs[v]) * I + i] = f2b(a * up);
+          else act[static_cast<size_t>(rs[v]) * I + i] = rb(a * up);
         }
       }
     });
@@ -419,11 +556,11 @@ class Executor {
       const int* rs = order_.data() + group_[g];
       const int nv = group_[g + 1] - group_[g];
       const Mat m = rowmat(dn, dn_rows, j.ids[rs[0]]);
-      const float* xs[kMaxVec];
-      for (int v = 0; v < nv; ++v) xs[v] = act_.data() + static_cast<size_t>(rs[v]) * I;
+      const X* xs[kMaxVec];
+      for (int v = 0; v < nv; ++v) xs[v] = act + static_cast<size_t>(rs[v]) * I;
       float dv[kMaxVec];
       for (int h = h0; h < h0 + kTile; ++h) {
-        dot_(m, h, xs, nv, dv);
+        dot(m, h, xs, nv, dv);
         for (int v = 0; v < nv; ++v) dout_[static_cast<size_t>(rs[v]) * H + h] = rb(dv[v] * j.w[rs[v]]);
       }
     });
@@ -452,7 +589,10 @@ class Executor {
   uint64_t gen_ = 0;
   std::atomic<int> next_{0};
   bool stop_ = false;
+  bool busy_ = false;  // the driver is computing a job
   std::vector<float> xf_, act_, dout_;
+  std::vector<bf16> act16_;
+  bool bf16_dot_ = false;
   std::vector<int> order_, group_;
 };
 
@@ -535,8 +675,10 @@ int ftmoe_cpu_experts_submit(ftmoe_cpu_executor* ex, const ftmoe_bank* bank, con
   // a job captured into a graph is replayed with the same record: never recycled
   ftmoe_cpu::Job* j = e->new_job(cs != hipStreamCaptureStatusNone);
   ftmoe_cpu::fill(j, bank, x, w, ids, M, k, activation, y);
-  if (hipLaunchHostFunc(stream, ftmoe_cpu::host_start, j) != hipSuccess)
+  if (hipLaunchHostFunc(stream, ftmoe_cpu::host_start, j) != hipSuccess) {
+    e->discard(j);
     return ftmoe::report_error(FTMOE_ERR_HIP, "cpu_experts_submit: hipLaunchHostFunc failed");
+  }
   *job = j;
   return FTMOE_OK;
 }

@@ -83,7 +83,7 @@ def test_cpu_experts_validation(executor):
 
 
 def test_executor_reports_isa(executor):
-    assert executor.isa in ("avx512f", "scalar")
+    assert executor.isa in ("avx512bf16", "avx512f", "scalar")
 
 
 def test_cpu_experts_hot_experts(executor):
