@@ -319,7 +319,7 @@ def run_miss_fetch(gen, dev, n_fetch: int = 8, steps: int = 10):
             "down_scale": (H // 128 * (I // 128) * 4,)}
     host, slots = [], []
     for shape in rows.values():
-        h = torch.empty((E,) + shape, dtype=torch.uint8, pin_memory=True)
+        h = ops.alloc_pinned_tensor(E, *shape, dtype=torch.uint8)
         h.view(-1)[:: 4097] = 1
         host.append(h)
         slots.append(torch.empty((S,) + shape, dtype=torch.uint8, device=dev))
@@ -376,7 +376,7 @@ def run_hybrid(gen, dev, M: int = 1, n_sets: int = 4, slots: int = 8, max_fetch:
         else:
             d = torch.randint(0, 256, (E,) + shape, generator=gen, device=dev, dtype=torch.uint8)
             d[(d & 0x7F) == 0x7F] = 0  # no NaN codes
-        h = torch.empty(d.shape, dtype=d.dtype, pin_memory=True)
+        h = ops.alloc_pinned_tensor(*d.shape, dtype=d.dtype)
         h.copy_(d)
         host[name] = h
         del d
@@ -452,7 +452,7 @@ def run_prefill_offload(gen, dev, L: int = 3, E: int = 32, M: int = 8192, reps: 
             else:
                 d = torch.randint(0, 256, (E,) + shape, generator=gen, device=dev, dtype=torch.uint8)
                 d[(d & 0x7F) == 0x7F] = 0
-            h = torch.empty(d.shape, dtype=d.dtype, pin_memory=True)
+            h = ops.alloc_pinned_tensor(*d.shape, dtype=d.dtype)
             h.copy_(d)
             host[name].append(h)
             del d

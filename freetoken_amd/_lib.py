@@ -80,6 +80,8 @@ SIGNATURES = {
     "ftmoe_lru_ensure": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp,
                               _vp]),
     "ftmoe_fetch_experts": (_i, [_fbp, _i, _vp, _vp, _vp, _i, _vp]),
+    "ftmoe_host_alloc": (_i, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "ftmoe_host_free": (_i, [_vp]),
     "ftmoe_materialize_layer": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
     "ftmoe_release_slots": (_i, [_i, _i, _i, _i, _vp, _vp, _vp, _i, _vp]),
     "ftmoe_act_quant_fp8": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),

@@ -257,7 +257,12 @@ def _pread_all(fd: int, mv: memoryview, off: int) -> None:
 
 
 def _host_buffer(nbytes: int, pinned: bool) -> torch.Tensor:
-    return torch.empty((_align_up(max(nbytes, 1)),), dtype=torch.uint8, pin_memory=pinned)
+    n = _align_up(max(nbytes, 1))
+    if pinned:  # exact size: torch's pinned allocator would round each layer up to a power of two
+        from ..ops import alloc_pinned_tensor
+
+        return alloc_pinned_tensor(n, dtype=torch.uint8)
+    return torch.empty((n,), dtype=torch.uint8)
 
 
 def load_ftw_banks(path: str, num_layers: int, *, pinned: bool = True, scales_to_float32: bool = True,
@@ -327,7 +332,12 @@ def load_ftw_banks(path: str, num_layers: int, *, pinned: bool = True, scales_to
         for name in order:
             layers = [bufs[(name, l)] for l in range(num_layers)]
             if scales_to_float32 and name.endswith("_scale") and layers[0].dtype == torch.bfloat16:
-                layers = [t.float().pin_memory() if pinned else t.float() for t in layers]
+                widened = []
+                for t in layers:
+                    f = _host_buffer(t.numel() * 4, pinned)[: t.numel() * 4].view(torch.float32).view(t.shape)
+                    f.copy_(t)
+                    widened.append(f)
+                layers = widened
             sources[name] = layers
         return reader.meta("quant_format"), sources, alphas
     finally:

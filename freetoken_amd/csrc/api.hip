@@ -308,6 +308,14 @@ int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layer
   return check_hip(ftmoe::launch_lru_ensure(a, stream), "lru_ensure launch");
 }
 
+int ftmoe_host_alloc(size_t bytes, void** ptr) {
+  if (!ptr) return fail(FTMOE_ERR_INVALID, "host_alloc: NULL ptr");
+  *ptr = nullptr;
+  return check_hip(hipHostMalloc(ptr, bytes ? bytes : 1, hipHostMallocDefault), "host_alloc hipHostMalloc");
+}
+
+int ftmoe_host_free(void* ptr) { return ptr ? check_hip(hipHostFree(ptr), "host_free hipHostFree") : FTMOE_OK; }
+
 int ftmoe_materialize_layer(int layer_id, int num_layers, int num_experts, int32_t* slot_for_id, int32_t* id_of_slot,
                             int64_t* usage, int64_t* step, int cache_size, int32_t* evict_slots,
                             int32_t* src_indices, int32_t* num_indices, ftmoe_stream_t stream) {

@@ -8,9 +8,12 @@ torch tensors.  There is no CPU path: tensors must live on a ROCm device.
 from __future__ import annotations
 
 import ctypes
+import math
 import os
+import weakref
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -162,6 +165,19 @@ def lru_ensure(expert_ids: torch.Tensor, layer_id: int, slot_for_id: torch.Tenso
         "lru_ensure",
     )
     return expert_ids
+
+
+def alloc_pinned_tensor(*shape: int, dtype: torch.dtype) -> torch.Tensor:
+    """Exact-size pinned host tensor (hipHostMalloc; reference
+    ``kernel/pinned.py:42-45``), freed when its last view is gone.  torch's
+    ``pin_memory`` rounds each allocation up to a power of two."""
+    nbytes = math.prod(shape) * torch.empty((), dtype=dtype).element_size()
+    ptr = ctypes.c_void_p()
+    check(lib().ftmoe_host_alloc(nbytes, ctypes.byref(ptr)), "host_alloc")
+    addr = ptr.value
+    raw = (ctypes.c_uint8 * max(nbytes, 1)).from_address(addr)
+    weakref.finalize(raw, lib().ftmoe_host_free, addr)
+    return torch.from_numpy(np.frombuffer(raw, dtype=np.uint8))[:nbytes].view(dtype).view(shape)
 
 
 def materialize_layer(layer_id: int, slot_for_id: torch.Tensor, id_of_slot: torch.Tensor, usage: torch.Tensor,

@@ -146,6 +146,13 @@ int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layer
                      int32_t* src_indices, int capacity, int32_t* num_indices, int32_t* num_missing,
                      int32_t* cpu_ids, int64_t* stats, ftmoe_stream_t stream);
 
+/* Exact-size pinned host memory (hipHostMalloc), for the host expert banks:
+ * replaces alloc_pinned_tensor (kernel/pinned.py:42-45).  torch's pinned
+ * allocator rounds every request up to a power of two, which for multi-GB
+ * expert layers nearly doubles the pinned footprint. */
+int ftmoe_host_alloc(size_t bytes, void** ptr);
+int ftmoe_host_free(void* ptr);
+
 /* Whole-layer placement of the prefill movement: replaces materialize_layer
  * (moe/offload_cache.py:833-838, _materialize_layer_kernel,
  * moe/offload_kernels.py:250-281).  Expert e of layer_id goes to slot e:

@@ -90,12 +90,19 @@ def test_lru_ensure_matches_oracle(dev, L, E, Sz, max_k, max_fetch, by_recency):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n", [0, 1, 5])
-def test_fetch_experts_copies_rows(dev, n):
+@pytest.mark.parametrize("n,exact", [(0, False), (1, False), (5, False), (5, True)])
+def test_fetch_experts_copies_rows(dev, n, exact):
+    """exact: host rows in ops.alloc_pinned_tensor memory (hipHostMalloc)."""
     rng = np.random.default_rng(11 + n)
     E, Sz = 12, 8
     shapes = [(E, 96, 64), (E, 3, 16), (E, 40000)]  # rows of 6 KiB, 48 B and 40 KB (a partial chunk)
     host = [torch.from_numpy(rng.integers(0, 256, size=s, dtype=np.uint8)).pin_memory() for s in shapes]
+    if exact:
+        exact_host = [ops.alloc_pinned_tensor(*h.shape, dtype=h.dtype) for h in host]
+        for a, b in zip(exact_host, host):
+            a.copy_(b)
+            assert a.is_pinned() and a.untyped_storage().nbytes() == b.numel()
+        host = exact_host
     slots = [torch.full((Sz,) + s[1:], 0xEE, dtype=torch.uint8, device=dev) for s in shapes]
     evict = torch.tensor(list(rng.permutation(Sz)[:6]), dtype=torch.int32, device=dev)
     src = torch.tensor(list(rng.permutation(E)[:6]), dtype=torch.int32, device=dev)
