@@ -79,27 +79,34 @@ def _hybrid_setup(dev, fmt, L, E, Sz, H, I, k, rng, decode_target="hybrid", **kw
     return banks, cache, layers
 
 
-def _expected(st, layer, x, w, ids, bank, E, max_fetch, frac_q16, capacity):
+def _expected(st, layer, x, w, ids, bank, E, max_fetch, frac_q16, capacity, shared=None):
     """Oracle of one hybrid step: admission, then the GPU partial (routes with a
-    slot) and the CPU partial (unfetched misses) added in bf16 (layers/moe.py:372)."""
+    slot, plus the shared expert) and the CPU partial (unfetched misses) added
+    in bf16 (layers/moe.py:372)."""
     out, *_ = S.lru_ensure(st, layer, ids, max_fetch=max_fetch, by_recency=True, capacity=capacity,
                            frac_q16=frac_q16)
     cpu_ids = S.hybrid_split(ids, out, E)
     gpu_ids = np.where(out >= 0, ids, -1).astype(np.int32)
-    y_gpu = oracle.experts.moe_layer("decode", x, w, gpu_ids, bank, None)
+    y_gpu = oracle.experts.moe_layer("decode", x, w, gpu_ids, bank, shared)
     y_cpu = oracle.experts.moe_layer("decode", x, w, cpu_ids, bank, None)
     return out, cpu_ids, oracle.numerics.bf16_round(y_gpu + y_cpu)
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt,max_fetch,frac", [("fp8", 1, 0.0), ("mxfp4", 2, 0.0), ("fp8", 8, 0.4)])
-def test_hybrid_layer_matches_oracle(dev, fmt, max_fetch, frac):
+@pytest.mark.parametrize("fmt,max_fetch,frac,with_shared", [("fp8", 1, 0.0, False), ("mxfp4", 2, 0.0, False),
+                                                            ("fp8", 8, 0.4, False), ("fp8", 1, 0.0, True)])
+def test_hybrid_layer_matches_oracle(dev, fmt, max_fetch, frac, with_shared):
     """Two layers share 6 slots over 16 experts; every step fetches at most the
-    cap of its misses and the CPU computes the rest."""
+    cap of its misses and the CPU computes the rest (with a shared expert: on
+    the GPU, in the GPU partial)."""
     rng = np.random.default_rng(71 + max_fetch)
     L, E, Sz, H, I, k, M = 2, 16, 6, 512, 256, 4, 3
     banks, cache, layers = _hybrid_setup(dev, fmt, L, E, Sz, H, I, k, rng, hybrid_max_fetch=max_fetch,
                                          hybrid_fetch_fraction=frac)
+    shared = synth.make_bank(fmt, 1, H, I, rng) if with_shared else None
+    if shared is not None:
+        for lay in layers:
+            lay.shared_expert = to_device_bank(shared, dev)
     st = S.CacheState(L, E, Sz)
     fq = round(frac * Q16)
     cpu_routes = 0
@@ -107,7 +114,7 @@ def test_hybrid_layer_matches_oracle(dev, fmt, max_fetch, frac):
         l = call % L
         x = synth.activations(rng, M, H)
         w_ref, ids_ref = oracle.routing.softmax_topk(synth.normal(rng, (M, E)), k, True)
-        out, cpu_ids, y_ref = _expected(st, l, x, w_ref, ids_ref, banks[l], E, max_fetch, fq, min(E, Sz))
+        out, cpu_ids, y_ref = _expected(st, l, x, w_ref, ids_ref, banks[l], E, max_fetch, fq, min(E, Sz), shared)
         cpu_routes += int((cpu_ids >= 0).sum())
         ids = torch.from_numpy(ids_ref.copy()).to(dev)
         with moe_phase("decode", backend="hybrid"):
@@ -115,7 +122,7 @@ def test_hybrid_layer_matches_oracle(dev, fmt, max_fetch, frac):
         np.testing.assert_array_equal(to_np(ids), out, err_msg=f"call {call}")
         g = to_np(y)
         assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, (fmt, call, max_rel(g, y_ref))
-        y_all = oracle.experts.moe_layer("decode", x, w_ref, ids_ref, banks[l], None)
+        y_all = oracle.experts.moe_layer("decode", x, w_ref, ids_ref, banks[l], shared)
         assert cosine(g, y_all) >= COS_TOL, (fmt, call)
     assert cpu_routes > 0  # the CPU share was exercised
     np.testing.assert_array_equal(to_np(cache.slot_for_id), st.slot_for_id)
@@ -123,16 +130,21 @@ def test_hybrid_layer_matches_oracle(dev, fmt, max_fetch, frac):
 
 
 @pytest.mark.gpu
-def test_cpu_layer_matches_oracle(dev):
+@pytest.mark.parametrize("with_shared", [False, True])
+def test_cpu_layer_matches_oracle(dev, with_shared):
     """A layer listed in cpu_layer_ids decodes on the CPU from its host banks;
-    the slot cache is not touched (layers/moe.py:307-310)."""
+    the slot cache is not touched (layers/moe.py:307-310); a shared expert
+    runs on the GPU meanwhile."""
     rng = np.random.default_rng(83)
     L, E, Sz, H, I, k, M = 2, 16, 4, 512, 256, 4, 5
     banks, cache, layers = _hybrid_setup(dev, "fp8", L, E, Sz, H, I, k, rng, decode_target="cpu")
     cache.cpu_layer_ids = frozenset({1})
+    shared = synth.make_bank("fp8", 1, H, I, rng) if with_shared else None
+    if shared is not None:
+        layers[1].shared_expert = to_device_bank(shared, dev)
     x = synth.activations(rng, M, H)
     w_ref, ids_ref = oracle.routing.softmax_topk(synth.normal(rng, (M, E)), k, True)
-    y_ref = oracle.experts.moe_layer("decode", x, w_ref, ids_ref, banks[1], None)
+    y_ref = oracle.experts.moe_layer("decode", x, w_ref, ids_ref, banks[1], shared)
     ids = torch.from_numpy(ids_ref.copy()).to(dev)
     with moe_phase("decode", backend="cpu"):
         y = layers[1].routed_forward(bf16_dev(x, dev), torch.from_numpy(w_ref).to(dev), ids)
