@@ -18,6 +18,7 @@
 // layer), and both nodes replay in a captured graph.
 #include <hip/hip_runtime.h>
 #include <immintrin.h>
+#include <pthread.h>
 #include <sched.h>
 
 #include <algorithm>
@@ -363,6 +364,7 @@ class Executor {
     const char* want = std::getenv("FTMOE_CPU_DOT");  // "fp32" keeps the fp32 dots (measurement)
     bf16_dot_ = dot_ == dot_avx512 && __builtin_cpu_supports("avx512bf16") && !(want && !std::strcmp(want, "fp32"));
     for (int t = 0; t < nthreads_; ++t) workers_.emplace_back([this] { worker(); });
+    pin_workers();
     driver_ = std::thread([this] { drive(); });
   }
   ~Executor() {
@@ -378,6 +380,24 @@ class Executor {
     driver_.join();
     for (auto& t : workers_) t.join();
     for (Job* j : jobs_) delete j;
+  }
+  // One worker per CPU of the process's affinity mask, in mask order, while
+  // there are at least as many CPUs as workers (the reference pins its pool to
+  // physical cores, moe/cpu_executor.py:91-140); FTMOE_CPU_PIN=0 leaves the
+  // scheduler free.
+  void pin_workers() {
+    const char* pin = std::getenv("FTMOE_CPU_PIN");
+    if (pin && !std::strcmp(pin, "0")) return;
+    cpu_set_t allowed;
+    if (sched_getaffinity(0, sizeof(allowed), &allowed) != 0 || CPU_COUNT(&allowed) < nthreads_) return;
+    int t = 0;
+    for (int c = 0; c < CPU_SETSIZE && t < nthreads_; ++c) {
+      if (!CPU_ISSET(c, &allowed)) continue;
+      cpu_set_t one;
+      CPU_ZERO(&one);
+      CPU_SET(c, &one);
+      pthread_setaffinity_np(workers_[t++].native_handle(), sizeof(one), &one);
+    }
   }
   const char* isa() const { return bf16_dot_ ? "avx512bf16" : dot_ == dot_avx512 ? "avx512f" : "scalar"; }
 
