@@ -9,9 +9,15 @@
 // d = W_down act the same way, times the router weight, rounded to bf16; the
 // token's output is bf16 of the fp32 sum of its CPU routes in route order.
 //
-// Work: pass 1 over (route, 32 rows of I), pass 2 over (token, 32 rows of H),
-// grabbed from an atomic counter by a persistent pool; a driver thread runs
-// the passes of one job after the other.  The stream sees the job through two
+// Work: the routes are grouped by expert, so that every weight row is read
+// once per step for all the tokens routed to its expert (up to kMaxVec at a
+// time): pass 1 over (expert, 32 rows of I) -> act; pass 2 over (expert, 32
+// rows of H) -> the weighted, bf16-rounded down output of each route; pass 3
+// over tokens sums its routes in route order.  A route's numbers do not depend
+// on the grouping.  Units come from an atomic counter; a driver thread runs
+// the passes of one job after the other and works in them beside a pool of
+// workers, which spin briefly on the pass generation between passes.  The
+// stream sees the job through two
 // host-function nodes: "submit" hands the job to the driver and returns at
 // once, "wait" blocks the stream until the job is done -- so the CPU work
 // overlaps whatever the stream runs between them (the GPU's share of the
@@ -363,9 +369,9 @@ class Executor {
     dot_ = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") ? dot_avx512 : dot_scalar;
     const char* want = std::getenv("FTMOE_CPU_DOT");  // "fp32" keeps the fp32 dots (measurement)
     bf16_dot_ = dot_ == dot_avx512 && __builtin_cpu_supports("avx512bf16") && !(want && !std::strcmp(want, "fp32"));
-    for (int t = 0; t < nthreads_; ++t) workers_.emplace_back([this] { worker(); });
-    pin_workers();
+    for (int t = 1; t < nthreads_; ++t) workers_.emplace_back([this] { worker(); });  // the driver is the other one
     driver_ = std::thread([this] { drive(); });
+    pin_workers();
   }
   ~Executor() {
     {
@@ -381,22 +387,26 @@ class Executor {
     for (auto& t : workers_) t.join();
     for (Job* j : jobs_) delete j;
   }
-  // One worker per CPU of the process's affinity mask, in mask order, while
-  // there are at least as many CPUs as workers (the reference pins its pool to
-  // physical cores, moe/cpu_executor.py:91-140); FTMOE_CPU_PIN=0 leaves the
-  // scheduler free.
+  // The driver and the workers one per CPU of the process's affinity mask, on
+  // the last CPUs of the mask (the first ones stay free for the threads that
+  // enqueue GPU work and run the stream's host functions), while there are at
+  // least as many CPUs as threads (the reference pins its pool to physical
+  // cores, moe/cpu_executor.py:91-140); FTMOE_CPU_PIN=0 leaves the scheduler
+  // free.
   void pin_workers() {
     const char* pin = std::getenv("FTMOE_CPU_PIN");
     if (pin && !std::strcmp(pin, "0")) return;
     cpu_set_t allowed;
     if (sched_getaffinity(0, sizeof(allowed), &allowed) != 0 || CPU_COUNT(&allowed) < nthreads_) return;
-    int t = 0;
+    int t = 0, skip = CPU_COUNT(&allowed) - nthreads_;
     for (int c = 0; c < CPU_SETSIZE && t < nthreads_; ++c) {
-      if (!CPU_ISSET(c, &allowed)) continue;
+      if (!CPU_ISSET(c, &allowed) || skip-- > 0) continue;
       cpu_set_t one;
       CPU_ZERO(&one);
       CPU_SET(c, &one);
-      pthread_setaffinity_np(workers_[t++].native_handle(), sizeof(one), &one);
+      std::thread& th = t == 0 ? driver_ : workers_[t - 1];
+      pthread_setaffinity_np(th.native_handle(), sizeof(one), &one);
+      ++t;
     }
   }
   const char* isa() const { return bf16_dot_ ? "avx512bf16" : dot_ == dot_avx512 ? "avx512f" : "scalar"; }
@@ -443,36 +453,45 @@ class Executor {
   }
 
  private:
+  // One pass over `units`: the driver and every worker take units from an
+  // atomic counter; the driver then spins until each worker has finished.
+  // Workers spin on the pass generation for a while before sleeping, so the
+  // passes of a job follow one another without wake-ups (the reference's
+  // pool uses a spin barrier between its passes, cpu_moe_ext.cpp:1833-1857).
   void parallel(int units, const std::function<void(int)>& fn) {
+    fn_ = &fn;
+    units_ = units;
+    next_.store(0, std::memory_order_relaxed);
+    left_.store(static_cast<int>(workers_.size()), std::memory_order_relaxed);
     {
       std::lock_guard<std::mutex> g(m_);
-      fn_ = &fn;
-      units_ = units;
-      next_.store(0);
-      left_ = nthreads_;
-      ++gen_;
+      gen_.fetch_add(1, std::memory_order_release);  // publishes fn_, units_, the counters
     }
     cv_work_.notify_all();
-    std::unique_lock<std::mutex> g(m_);
-    cv_pass_.wait(g, [this] { return left_ == 0; });
+    for (int u = next_.fetch_add(1); u < units; u = next_.fetch_add(1)) fn(u);
+    while (left_.load(std::memory_order_acquire) != 0) _mm_pause();
     fn_ = nullptr;
   }
   void worker() {
+    constexpr int kSpin = 4096;  // pauses before sleeping (~0.1 ms)
     uint64_t seen = 0;
     for (;;) {
-      const std::function<void(int)>* fn;
-      int units;
-      {
-        std::unique_lock<std::mutex> g(m_);
-        cv_work_.wait(g, [&] { return stop_ || gen_ != seen; });
-        if (stop_) return;
-        seen = gen_;
-        fn = fn_;
-        units = units_;
+      uint64_t g = gen_.load(std::memory_order_acquire);
+      for (int spin = 0; g == seen && spin < kSpin && !stop_.load(std::memory_order_relaxed); ++spin) {
+        _mm_pause();
+        g = gen_.load(std::memory_order_acquire);
       }
+      if (g == seen) {
+        std::unique_lock<std::mutex> lk(m_);
+        cv_work_.wait(lk, [&] { return stop_.load() || gen_.load(std::memory_order_acquire) != seen; });
+        if (stop_.load()) return;
+        g = gen_.load(std::memory_order_acquire);
+      }
+      seen = g;
+      const std::function<void(int)>* fn = fn_;
+      const int units = units_;
       for (int u = next_.fetch_add(1); u < units; u = next_.fetch_add(1)) (*fn)(u);
-      std::lock_guard<std::mutex> g(m_);
-      if (--left_ == 0) cv_pass_.notify_all();
+      left_.fetch_sub(1, std::memory_order_acq_rel);
     }
   }
   void drive() {
@@ -601,14 +620,15 @@ class Executor {
   std::vector<std::thread> workers_;
   std::thread driver_;
   std::mutex m_;
-  std::condition_variable cv_job_, cv_done_, cv_work_, cv_pass_;
+  std::condition_variable cv_job_, cv_done_, cv_work_;
   std::deque<Job*> queue_;
   std::vector<Job*> jobs_, free_;
   const std::function<void(int)>* fn_ = nullptr;
-  int units_ = 0, left_ = 0;
-  uint64_t gen_ = 0;
+  int units_ = 0;
+  std::atomic<int> left_{0};
+  std::atomic<uint64_t> gen_{0};
   std::atomic<int> next_{0};
-  bool stop_ = false;
+  std::atomic<bool> stop_{false};
   bool busy_ = false;  // the driver is computing a job
   std::vector<float> xf_, act_, dout_;
   std::vector<bf16> act16_;

@@ -509,8 +509,10 @@ class CpuExecutor:
     it.  Inputs and outputs are host tensors (pinned for the stream path)."""
 
     def __init__(self, threads: int = 0):
-        if threads <= 0:  # the process's CPU share: OMP_NUM_THREADS when set, else the affinity mask
-            threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+        if threads <= 0:  # the process's CPU share (OMP_NUM_THREADS when set, else the affinity
+            # mask) less one CPU for the thread that enqueues the GPU's share and the stream's host functions
+            share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+            threads = max(1, share - 1)
         self.threads = threads
         self._h = lib().ftmoe_cpu_executor_create(threads)
         if not self._h:
