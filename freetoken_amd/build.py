@@ -23,7 +23,8 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
-    # packed fp32 VALU ops are kept out of the code objects (see DESIGN notes)
+    # packed fp32 VALU ops (v_pk_* f32) are kept out of the code objects: some of their forms
+    # have given wrong results now and then on these boxes
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}",
 ]
