@@ -176,7 +176,8 @@ def alloc_pinned_tensor(*shape: int, dtype: torch.dtype) -> torch.Tensor:
     check(lib().ftmoe_host_alloc(nbytes, ctypes.byref(ptr)), "host_alloc")
     addr = ptr.value
     raw = (ctypes.c_uint8 * max(nbytes, 1)).from_address(addr)
-    weakref.finalize(raw, lib().ftmoe_host_free, addr)
+    # freed with its last view; not at interpreter exit, where the HIP runtime may be gone first
+    weakref.finalize(raw, lib().ftmoe_host_free, addr).atexit = False
     return torch.from_numpy(np.frombuffer(raw, dtype=np.uint8))[:nbytes].view(dtype).view(shape)
 
 
