@@ -100,3 +100,23 @@ def test_cpu_experts_hot_experts(executor):
                      _host(ids, np.int32))
     g = y.float().numpy()
     assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, max_rel(g, y_ref)
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4"])
+def test_cpu_experts_deterministic_across_pools(fmt):
+    """A route's numbers do not depend on how the passes are split over the
+    pool: 1, 3 and 8 threads, and many jobs back to back, give identical bytes."""
+    rng = np.random.default_rng(17)
+    E, H, I, M, k = 8, 256, 256, 6, 4
+    bank = to_device_bank(synth.make_bank(fmt, E, H, I, rng), "cpu")
+    x = _host(synth.activations(rng, M, H), np.float32).to(torch.bfloat16)
+    w, ids = oracle.routing.softmax_topk(synth.normal(rng, (M, E)), k, True)
+    w, ids = _host(w, np.float32), _host(ids, np.int32)
+    outs = []
+    for threads in (1, 3, 8):
+        ex = ops.CpuExecutor(threads=threads)
+        ys = [ex.run(bank, x, w, ids).clone() for _ in range(10)]
+        ex.close()
+        assert all(torch.equal(y, ys[0]) for y in ys)
+        outs.append(ys[0])
+    assert all(torch.equal(o, outs[0]) for o in outs)
