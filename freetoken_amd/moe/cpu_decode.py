@@ -19,6 +19,18 @@ from .. import ops
 from .offload_cache import ExpertSlotCache, bank_from_views
 
 
+def hybrid_fetch_fraction(pcie_gbs: float, cpu_gbs: float, overlapped: bool = True) -> float | None:
+    """Bandwidth-matched share of a step's misses to fetch over PCIe, so that
+    the fetch and the CPU's share finish together (reference
+    ``load_hybrid_fetch_fraction``, ``moe/bench_profile.py:156-191``): from
+    rates measured while both run, pcie / (pcie + cpu); from standalone rates,
+    under full DRAM contention, pcie / cpu.  Clamped to [0, 1]; None without
+    both rates.  The result is ``ExpertSlotCache.hybrid_fetch_fraction``."""
+    if not pcie_gbs or not cpu_gbs or pcie_gbs <= 0 or cpu_gbs <= 0:
+        return None
+    return min(1.0, pcie_gbs / (pcie_gbs + cpu_gbs) if overlapped else pcie_gbs / cpu_gbs)
+
+
 class CpuMoeDecoder:
     def __init__(self, cache: ExpertSlotCache, top_k: int, threads: int = 0, activation: str = "silu"):
         assert cache.sources, "the CPU share reads the cache's host sources: set_bank_sources first"

@@ -120,3 +120,14 @@ def test_cpu_experts_deterministic_across_pools(fmt):
         assert all(torch.equal(y, ys[0]) for y in ys)
         outs.append(ys[0])
     assert all(torch.equal(o, outs[0]) for o in outs)
+
+
+def test_hybrid_fetch_fraction_rule():
+    # tests/moe/test_hybrid_fetch.py:44-63: standalone pcie / cpu, overlapped pcie / (pcie + cpu)
+    from freetoken_amd.moe.cpu_decode import hybrid_fetch_fraction
+
+    assert hybrid_fetch_fraction(40.0, 100.0, overlapped=False) == pytest.approx(0.4)
+    assert hybrid_fetch_fraction(30.0, 90.0) == pytest.approx(0.25)
+    assert hybrid_fetch_fraction(50.0, 80.0, overlapped=False) == pytest.approx(0.625)
+    assert hybrid_fetch_fraction(120.0, 100.0, overlapped=False) == 1.0
+    assert hybrid_fetch_fraction(0.0, 100.0) is None
