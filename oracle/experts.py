@@ -33,6 +33,14 @@ equivalence (fp8 block path == bf16 path on the dequantised weights, up to
 the documented rounding points); linearity in the router weights; a single
 expert with identity-like weights reducing to silu(x)*x; and the C++ CPU
 executor restatement (oracle/cpu_moe) on identical banks.
+Prefill pins (tests/test_oracle_prefill.py): ``_gemm_w8a8`` and the MXFP4
+prefill product against float64 products of independently dequantised
+operands (torch's e4m3 cast, a separate e2m1 table, frexp exponents); exact
+power-of-two equivariance per activation group and per weight scale block;
+the e4m3 activation-quantisation error bound; a per-element brute-force loop;
+the layer's prefill-vs-decode bound on FP8 and MXFP4 banks; a per-route loop
+of the whole prefill layer; each check rejects a missing activation scale, a
+transposed weight-scale table and a shifted K-block index.
 """
 
 from __future__ import annotations
