@@ -239,7 +239,10 @@ def run_decode(layer: DecodeLayer, M: int, steps: int, warmup: int, gen, graphs:
 # ----------------------------------------------------------------------------- prefill
 
 
-def run_prefill(fmt: str, steps: int, warmup: int, gen, dev, M: int = 8192):
+def prefill_workload(fmt: str, gen, dev, M: int = 8192) -> dict:
+    """The C5 workload: the C4 layer (256 experts + shared, in ``fmt``) and an
+    M-token ragged batch of 16 sequences whose router logits carry a Zipf(1.1)
+    expert-popularity bias, routed by the grouped sigmoid router."""
     c = C4
     H, I, E, k = c["H"], c["I"], c["E"], c["k"]
     bank = make_bank(fmt, E, H, I, gen, dev)
@@ -259,6 +262,15 @@ def run_prefill(fmt: str, steps: int, warmup: int, gen, dev, M: int = 8192):
     logits = torch.randn((M, E), generator=gen, device=dev) + zipf[None, :]
     x = torch.randn((M, H), generator=gen, device=dev).to(torch.bfloat16)
     w, ids = ops.route_grouped_sigmoid(logits, bias, 8, 4, k, True, 2.5)
+    return dict(bank=bank, shared=shared, lens=lens, bias=bias, logits=logits, x=x, w=w, ids=ids)
+
+
+def run_prefill(fmt: str, steps: int, warmup: int, gen, dev, M: int = 8192):
+    c = C4
+    H, I, E = c["H"], c["I"], c["E"]
+    wl = prefill_workload(fmt, gen, dev, M)
+    bank, shared, lens, x, w, ids = wl["bank"], wl["shared"], wl["lens"], wl["x"], wl["w"], wl["ids"]
+    del wl
     out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
     for _ in range(max(1, warmup)):
         ops.experts_prefill(x, w, ids, bank, shared=shared, out=out)
@@ -351,14 +363,16 @@ def run_miss_fetch(gen, dev, n_fetch: int = 8, steps: int = 10):
 
 
 def run_hybrid(gen, dev, M: int = 1, n_sets: int = 4, slots: int = 8, max_fetch: int = 1, steps: int = 8,
-               warmup: int = 8):
+               warmup: int = 8, fetch_fraction: float | None = None):
     """Hybrid decode at C4 shape (FP8 experts, one layer): each step routes the
     M tokens to one of n_sets disjoint sets of k experts in turn, over a slot
     cache of ``slots`` experts, so every step has misses; the admission fetches
     at most max_fetch of them over PCIe and the CPU executor computes the rest
     while the GPU runs its share.  Besides the step time it times the two
     shares alone on the same routing (the CPU job; the gather plus the GPU
-    experts), so the overlap is (cpu + gpu) / step."""
+    experts), so the overlap is (cpu + gpu) / step.  ``fetch_fraction`` (the
+    bandwidth-matched share of the misses, from measured rates) replaces the
+    fixed ``max_fetch`` cap when given."""
     from freetoken_amd.core import moe_phase
     from freetoken_amd.layers.moe import OffloadMoELayer
     from freetoken_amd.moe.cpu_decode import CpuMoeDecoder
@@ -380,7 +394,8 @@ def run_hybrid(gen, dev, M: int = 1, n_sets: int = 4, slots: int = 8, max_fetch:
         h.copy_(d)
         host[name] = h
         del d
-    cache = ExpertSlotCache(1, E, slots, "fp8_block", device=dev, decode_target="hybrid", hybrid_max_fetch=max_fetch)
+    cache = ExpertSlotCache(1, E, slots, "fp8_block", device=dev, decode_target="hybrid", hybrid_max_fetch=max_fetch,
+                            hybrid_fetch_fraction=fetch_fraction or 0.0)
     cache.set_bank_caches(**{n: torch.zeros((slots,) + h.shape[1:], dtype=h.dtype, device=dev)
                              for n, h in host.items()})
     cache.set_bank_sources({n: [h] for n, h in host.items()})
@@ -423,7 +438,7 @@ def run_hybrid(gen, dev, M: int = 1, n_sets: int = 4, slots: int = 8, max_fetch:
     med = lambda j: statistics.median(r[j] for r in rec)  # noqa: E731
     step, cpu_ms, gpu_ms = med(0), med(1), med(2)
     n_cpu, n_fetch, n_gpu = med(3), med(4), med(5)
-    return dict(batch=M, experts_per_step=k, slots=slots, max_fetch=max_fetch, step_ms=step,
+    return dict(batch=M, experts_per_step=k, slots=slots, max_fetch=max_fetch, fetch_fraction=fetch_fraction, step_ms=step,
                 cpu_experts=n_cpu, fetched_experts=n_fetch, gpu_experts=n_gpu, cpu_ms=cpu_ms, gpu_ms=gpu_ms,
                 overlap=(cpu_ms + gpu_ms) / step, cpu_gbs=n_cpu * eb / (cpu_ms * 1e-3) / 1e9,
                 cpu_threads=threads, cpu_isa=isa)
@@ -646,7 +661,7 @@ def main() -> int:
 
     sweep = {}
     if not args.no_sweep:
-        for M in (1, 8, 32):
+        for M in (1, 8, 32, 128, 256):
             log(f"[bench] sweep C4 decode batch {M}")
             sweep[f"{C4['name']}_b{M}"] = run_decode(c4, M, 20, 3, gen, stage_timing=True)
     cpu = None
@@ -672,6 +687,13 @@ def main() -> int:
         sweep["c4_prefill_offload_3x32_experts"] = run_prefill_offload(gen, dev)
         log("[bench] sweep C4 hybrid decode (1 expert fetched per step, the other misses on the CPU)")
         sweep["c4_hybrid_b1"] = run_hybrid(gen, dev, M=1)
+        # the reference's benched rule: the fetch share from the measured standalone PCIe and CPU rates
+        from freetoken_amd.moe.cpu_decode import hybrid_fetch_fraction
+
+        frac = hybrid_fetch_fraction(sweep["c4_miss_fetch_8_experts"]["fetch_gbs"], sweep["c4_hybrid_b1"]["cpu_gbs"],
+                                     overlapped=False)
+        log(f"[bench] sweep C4 hybrid decode with the measured fetch fraction {frac}")
+        sweep["c4_hybrid_b1_measured_fraction"] = run_hybrid(gen, dev, M=1, fetch_fraction=frac)
 
     def rnd(d):
         return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}

@@ -16,6 +16,8 @@ FTMOE_ERR_INVALID = -1
 FTMOE_ERR_UNSUPPORTED = -2
 FTMOE_ERR_HIP = -3
 FTMOE_ERR_WORKSPACE = -4
+FTMOE_ERR_BUSY = -5
+FTMOE_ERR_TIMEOUT = -6
 
 DTYPE_F32, DTYPE_BF16 = 0, 1
 FMT_NONE, FMT_BF16, FMT_FP8_B128, FMT_MXFP4 = -1, 0, 1, 2
@@ -78,7 +80,7 @@ SIGNATURES = {
     "ftmoe_align": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "ftmoe_slot_map": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp, _vp]),
     "ftmoe_lru_ensure": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp,
-                              _vp]),
+                              _vp, _vp]),
     "ftmoe_fetch_experts": (_i, [_fbp, _i, _vp, _vp, _vp, _i, _vp]),
     "ftmoe_host_alloc": (_i, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
     "ftmoe_host_free": (_i, [_vp]),
@@ -94,7 +96,10 @@ SIGNATURES = {
     "ftmoe_experts_prefill_workspace": (_sz, [_i, _i, _bp, _bp]),
     "ftmoe_experts_prefill": (_i, [_vp, _i, _i, _vp, _vp, _bp, _bp, _i, _vp, _vp, _sz, _vp]),
     "ftmoe_cpu_executor_create": (_vp, [_i]),
-    "ftmoe_cpu_executor_destroy": (None, [_vp]),
+    "ftmoe_cpu_executor_destroy": (_i, [_vp, _i]),
+    "ftmoe_cpu_executor_healthy": (_i, [_vp]),
+    "ftmoe_cpu_executor_set_watchdog": (None, [_vp, _i]),
+    "ftmoe_cpu_executor_hold": (None, [_vp, _i]),
     "ftmoe_cpu_executor_isa": (ctypes.c_char_p, [_vp]),
     "ftmoe_cpu_experts": (_i, [_vp, _bp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "ftmoe_cpu_experts_submit": (_i, [_vp, _bp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, ctypes.POINTER(_vp)]),

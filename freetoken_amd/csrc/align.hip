@@ -385,6 +385,162 @@ hipError_t launch_align_large(const AlignArgs& a, int32_t* gcount, hipStream_t s
 // One-wave align for decode-sized calls (align_wave.h).
 __global__ void __launch_bounds__(kWave) align_wave_kernel(AlignArgs a) { align_wave(a, a.ids); }
 
+// ----------------------------------------------------------------------------
+// Decode-form align for banks of many rows (an expert cache of thousands of
+// slots): block size 1, segments, no padding.  The counting kernel above keeps
+// per-wave counts of every row in LDS; here the LDS holds one key per route
+// instead, so the row count is free (up to kSortMaxRows) and the route count
+// is bounded (kSortMaxRoutes).  One workgroup:
+//   1. optional slot lookup (as pass 0 of align_kernel; distinct seen and
+//      missing experts marked in LDS bitmaps), key = row << 14 | route, or
+//      ~0 for routes outside [0, rows + 1);
+//   2. ascending bitonic sort of the keys in LDS: the stable order, since
+//      equal rows order by route;
+//   3. position p of the sorted keys is the route's place (block size 1);
+//      a row's run is found by binary search, segment starts are every
+//      seg_cap-th place of a run, numbered by a block scan.
+// The outputs are identical to align_kernel's for the same call.
+// ----------------------------------------------------------------------------
+constexpr int kSortShift = 14;
+constexpr uint32_t kSortRouteMask = (1u << kSortShift) - 1u;
+
+__device__ __forceinline__ int sorted_lower_bound(const uint32_t* keys, int n, uint32_t v) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (keys[mid] < v) lo = mid + 1; else hi = mid;
+  }
+  return lo;
+}
+
+__global__ void __launch_bounds__(kAlignThreads) align_sort_kernel(AlignArgs a, int P) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t skeys[];  // [P] keys, then the bitmaps
+  const int words = a.stats && a.slot_for_id ? (a.table_size + 31) / 32 : 0;
+  uint32_t* seen_bits = skeys + P;
+  uint32_t* miss_bits = seen_bits + words;
+  __shared__ int s_tmp[2 * kAlignWaves];
+  const int tid = threadIdx.x, lane = lane_id();
+  const int eff = a.num_experts + 1;
+  for (int i = tid; i < words; i += kAlignThreads) {
+    seen_bits[i] = 0;
+    miss_bits[i] = 0;
+  }
+  __syncthreads();
+  unsigned long long missed = 0;
+  for (int i = tid; i < P; i += kAlignThreads) {
+    uint32_t key = ~0u;
+    if (i < a.numel) {
+      int e = a.ids[i];
+      if (a.slot_for_id) {
+        const bool idv = e >= 0 && e < a.table_size;
+        const int s = idv ? a.slot_for_id[e] : -1;
+        if (a.slot_ids) a.slot_ids[i] = s;  // may alias ids: this thread read ids[i] above
+        if (a.miss_mask) a.miss_mask[i] = (idv && s < 0) ? 1 : 0;
+        if (words && idv) {
+          atomicOr(&seen_bits[e >> 5], 1u << (e & 31));
+          if (s < 0) atomicOr(&miss_bits[e >> 5], 1u << (e & 31));
+        }
+        if (idv && s < 0) ++missed;
+        e = s;
+      }
+      if (e >= 0 && e < eff) key = (static_cast<uint32_t>(e) << kSortShift) | static_cast<uint32_t>(i);
+    }
+    skeys[i] = key;
+  }
+  __syncthreads();
+  for (int k = 2; k <= P; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < P; i += kAlignThreads) {
+        const int p = i ^ j;
+        if (p > i) {
+          const uint32_t x = skeys[i], y = skeys[p];
+          if ((x > y) == ((i & k) == 0)) {
+            skeys[i] = y;
+            skeys[p] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // places, run bounds and segment starts over contiguous chunks of places
+  const int per = (a.numel + kAlignThreads - 1) / kAlignThreads;
+  const int p0 = min(a.numel, tid * per), p1 = min(a.numel, p0 + per);
+  int nstart = 0;
+  for (int p = p0; p < p1; ++p) {
+    const uint32_t key = skeys[p];
+    if (key == ~0u) break;  // invalid keys sort last
+    const int e = static_cast<int>(key >> kSortShift);
+    a.sorted_ids[p] = static_cast<int>(key & kSortRouteMask);
+    if (p + 1 == a.numel || skeys[p + 1] == ~0u) a.ntpp[0] = p + 1;
+    if (a.seg_expert && e < a.num_experts) {
+      const int run0 = sorted_lower_bound(skeys, a.numel, static_cast<uint32_t>(e) << kSortShift);
+      if ((p - run0) % a.seg_cap == 0) ++nstart;
+    }
+  }
+  if (tid == 0 && (a.numel == 0 || skeys[0] == ~0u)) a.ntpp[0] = 0;
+  int nseg = 0;
+  int si = block_exclusive_scan(nstart, s_tmp, &nseg);
+  if (a.seg_expert) {
+    for (int p = p0; p < p1; ++p) {
+      const uint32_t key = skeys[p];
+      if (key == ~0u) break;
+      const int e = static_cast<int>(key >> kSortShift);
+      if (e >= a.num_experts) continue;
+      const int run0 = sorted_lower_bound(skeys, a.numel, static_cast<uint32_t>(e) << kSortShift);
+      if ((p - run0) % a.seg_cap != 0) continue;
+      const int run1 = sorted_lower_bound(skeys, a.numel, static_cast<uint32_t>(e + 1) << kSortShift);
+      a.seg_expert[si] = e;
+      a.seg_start[si] = p;
+      a.seg_count[si] = min(a.seg_cap, run1 - p);
+      ++si;
+    }
+    if (tid == 0) a.n_seg[0] = nseg;
+  }
+  if (a.stats) {
+    unsigned long long act = 0, miss = 0;
+    for (int i = tid; i < words; i += kAlignThreads) {
+      act += __popc(seen_bits[i]);
+      miss += __popc(miss_bits[i]);
+    }
+    const unsigned long long t_act = wave_sum_u64(act), t_miss = wave_sum_u64(miss);
+    const unsigned long long t_missed = wave_sum_u64(missed);
+    auto* st = reinterpret_cast<unsigned long long*>(a.stats);
+    if (lane == 0) {
+      if (t_act) atomicAdd(st + 0, t_act);
+      if (t_miss) atomicAdd(st + 1, t_miss);
+      if (t_missed) atomicAdd(st + 3, t_missed);
+      if (tid == 0) atomicAdd(st + 2, 1ull);
+    }
+  }
+}
+
+// Whether a call takes align_sort_kernel: the decode form over a bank too
+// large for the counting kernel's per-row LDS.
+inline bool align_takes_sort(const AlignArgs& a) {
+  return a.num_experts > kCountMaxRows && a.block_size == 1 && a.max_padded == 0 && !a.expert_ids &&
+         !a.cum_out;
+}
+
+size_t align_sort_lds_bytes(const AlignArgs& a, int P) {
+  const int words = a.stats && a.slot_for_id ? (a.table_size + 31) / 32 : 0;
+  return sizeof(uint32_t) * (static_cast<size_t>(P) + 2 * static_cast<size_t>(words));
+}
+
+hipError_t launch_align_sort(const AlignArgs& a, hipStream_t stream) {
+  int P = 1;
+  while (P < a.numel) P <<= 1;
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(align_sort_kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
+    if (err != hipSuccess) return err;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(align_sort_kernel, dim3(1), dim3(kAlignThreads), align_sort_lds_bytes(a, P), stream, a, P);
+  return hipGetLastError();
+}
+
 size_t align_lds_bytes(int num_experts, int table_size, bool stats) {
   const int eff = num_experts + 1;
   return sizeof(int) * (static_cast<size_t>(kAlignWaves) * eff + (eff + 1) + eff + (stats ? table_size : 0));
@@ -395,6 +551,7 @@ hipError_t launch_align(const AlignArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(align_wave_kernel, dim3(1), dim3(kWave), 0, stream, a);
     return hipGetLastError();
   }
+  if (align_takes_sort(a)) return launch_align_sort(a, stream);
   const size_t lds = align_lds_bytes(a.num_experts, a.table_size, a.stats != nullptr);
   static bool attr_set = false;
   if (!attr_set) {

@@ -266,7 +266,7 @@ int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layer
                      int32_t* slot_for_id, int32_t* id_of_slot, int64_t* usage, int64_t* step, int cache_size,
                      int64_t* recency, int max_fetch, int fetch_frac_q16, int32_t* evict_slots,
                      int32_t* src_indices, int capacity, int32_t* num_indices, int32_t* num_missing,
-                     int32_t* cpu_ids, int64_t* stats, ftmoe_stream_t stream) {
+                     int32_t* cpu_ids, int64_t* stats, int64_t* unserved, ftmoe_stream_t stream) {
   if ((!expert_ids && numel) || !slot_for_id || !id_of_slot || !usage || !step || !num_indices || !num_missing ||
       ((!evict_slots || !src_indices) && capacity))
     return fail(FTMOE_ERR_INVALID, "lru_ensure: NULL pointer");
@@ -302,6 +302,7 @@ int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layer
   a.num_indices = num_indices;
   a.num_missing = num_missing;
   a.stats = reinterpret_cast<long long*>(stats);
+  a.unserved = reinterpret_cast<long long*>(unserved);
   if (ftmoe::lru_lds_bytes(num_experts, cache_size, a.sort_len) > 160 * 1024 - 4096)
     return fail(FTMOE_ERR_UNSUPPORTED, "lru_ensure: E=%d S=%d exceed the LDS of one workgroup", num_experts,
                 cache_size);
@@ -430,7 +431,11 @@ int experts_decode_impl(const void* x, int M, int top_k, const float* topk_w, co
   }
   if (!x || !topk_w || !topk_ids || !y) return fail(FTMOE_ERR_INVALID, "experts_decode: NULL pointer");
   if (M <= 0 || top_k <= 0) return fail(FTMOE_ERR_INVALID, "experts_decode: M=%d top_k=%d", M, top_k);
-  if (bank->num_rows > 1023) return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode: num_rows %d > 1023", bank->num_rows);
+  if (bank->num_rows > ftmoe::kSortMaxRows ||
+      (bank->num_rows > ftmoe::kCountMaxRows && M * top_k > ftmoe::kSortMaxRoutes))
+    return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode: num_rows %d with %d routes (rows <= %d, and routes <= %d "
+                "above %d rows)", bank->num_rows, M * top_k, ftmoe::kSortMaxRows, ftmoe::kSortMaxRoutes,
+                ftmoe::kCountMaxRows);
   if (activation < FTMOE_ACT_SILU || activation > FTMOE_ACT_GELU_TANH)
     return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode: activation %d", activation);
   const DecodeLayout need = decode_layout(nullptr, M, top_k, bank, shared);

@@ -10,12 +10,19 @@
 //   step += 1; the distinct ids of the call are "seen"; every resident seen
 //   expert's slot gets usage = step; the missing seen experts are ordered by
 //   ascending id, or with a recency table by (most recently seen first, then
-//   ascending id); the first min(misses, cap) of them take, one after
+//   ascending id); the first min(misses, cap, free) of them take, one after
 //   the other, the slot with the smallest (usage, slot) -- the previous owner
 //   (any layer) loses its mapping, the slot gets usage = step -- and are listed
 //   in (evict_slots, src_indices); the recency of every seen expert becomes
 //   step; finally every id is rewritten to its slot (-1 for unfetched misses
 //   and for ids outside [0, num_experts)).
+// "free" is the number of slots with usage < step after the touch: slots that
+// neither hold an expert of this call nor were admitted by it.  An admitted
+// slot gets usage = step, so while fewer than "free" misses have been placed
+// the smallest (usage, slot) is always such a slot: no victim repeats and no
+// expert of the call loses its slot (the reference's GPU kernel excludes the
+// same slots, offload_kernels.py:369-387).  Misses beyond it stay unfetched
+// and are counted in unserved (nullable, int64, accumulated).
 // The cap is max_fetch (< 0: none), or with a fetch fraction f (Q16, > 0) the
 // integer n in {floor(m f), floor(m f) + 1} with the smaller max(n (1 - f),
 // (m - n) f) -- PCIe fetch and CPU overflow balanced, lower n on a tie
@@ -99,12 +106,15 @@ __global__ void __launch_bounds__(kLruThreads) lru_ensure_kernel(LruArgs a) {
     }
   }
   int m = 0;
-  int pos = lru_block_scan(nmiss, s_tmp, &m);
+  int pos = lru_block_scan(nmiss, s_tmp, &m);  // its barriers publish the touched usage
   for (int q = 0; q < per; ++q) {
     const int e = tid * per + q;
     if (e < E && seen[e] == 2) list[pos++] = e;
   }
-  __syncthreads();
+  int nfree_local = 0;
+  for (int s = tid; s < S; s += kLruThreads) nfree_local += u[s] < step ? 1 : 0;
+  int nfree = 0;
+  (void)lru_block_scan(nfree_local, s_tmp, &nfree);
   if (a.recency) {
     // (most recent first, then ascending id): ascending sort of
     // (max - recency) << 13 | id over the miss list padded to sort_len
@@ -146,10 +156,13 @@ __global__ void __launch_bounds__(kLruThreads) lru_ensure_kernel(LruArgs a) {
     const long long c0 = max(lo * (q - f), (m - lo) * f), c1 = max((lo + 1) * (q - f), (m - lo - 1) * f);
     nfetch = min(m, static_cast<int>(c0 <= c1 ? lo : lo + 1));
   }
-  nfetch = min(nfetch, a.capacity);
+  const int wanted = nfetch;
+  nfetch = min(nfetch, min(a.capacity, nfree));
   if (tid == 0) {
     a.num_missing[0] = m;
     a.num_indices[0] = nfetch;
+    if (a.unserved && wanted > nfetch) atomicAdd(reinterpret_cast<unsigned long long*>(a.unserved),
+                                                 static_cast<unsigned long long>(wanted - nfetch));
   }
   // admission, one miss after the other: the slot with the smallest (usage, slot)
   for (int idx = 0; idx < nfetch; ++idx) {

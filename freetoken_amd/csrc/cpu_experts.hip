@@ -29,9 +29,11 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <condition_variable>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 #include <type_traits>
 #include <cstdlib>
@@ -361,6 +363,8 @@ struct Job {
   bf16* y;          // [M, H]
   bool permanent = false;
   bool done = true;
+  bool failed = false;     // poisoned by the watchdog (or refused by an unhealthy executor)
+  bool abandoned = false;  // poisoned while the driver held it: never recycled
 };
 
 class Executor {
@@ -369,14 +373,22 @@ class Executor {
     dot_ = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") ? dot_avx512 : dot_scalar;
     const char* want = std::getenv("FTMOE_CPU_DOT");  // "fp32" keeps the fp32 dots (measurement)
     bf16_dot_ = dot_ == dot_avx512 && __builtin_cpu_supports("avx512bf16") && !(want && !std::strcmp(want, "fp32"));
+    const char* wd = std::getenv("FTMOE_CPU_WATCHDOG_S");  // seconds without progress; 0 turns it off
+    watchdog_ms_ = wd ? static_cast<int>(std::atof(wd) * 1000.0) : 10000;
     for (int t = 1; t < nthreads_; ++t) workers_.emplace_back([this] { worker(); });  // the driver is the other one
     driver_ = std::thread([this] { drive(); });
     pin_workers();
   }
   ~Executor() {
     {
-      // queued and running jobs finish first: a worker leaving mid-pass would
-      // leave the driver waiting for it
+      std::lock_guard<std::mutex> g(m_);
+      hold_ = false;
+    }
+    cv_job_.notify_all();
+    {
+      // queued and running jobs finish first (a worker leaving mid-pass would
+      // leave the driver waiting for it); after the watchdog fired the queue
+      // was failed and only a running job is waited for
       std::unique_lock<std::mutex> g(m_);
       cv_done_.wait(g, [this] { return queue_.empty() && !busy_; });
       stop_ = true;
@@ -386,6 +398,22 @@ class Executor {
     driver_.join();
     for (auto& t : workers_) t.join();
     for (Job* j : jobs_) delete j;
+  }
+  // Jobs captured into graphs: their records are replayed by the graphs, so
+  // the executor must outlive them.
+  int captured_jobs() {
+    std::lock_guard<std::mutex> g(m_);
+    return captured_;
+  }
+  bool healthy() const { return !unhealthy_.load(); }
+  void set_watchdog_ms(int ms) { watchdog_ms_ = ms; }
+  // Holds the driver before its next job (maintenance; tests of the watchdog).
+  void hold(bool on) {
+    {
+      std::lock_guard<std::mutex> g(m_);
+      hold_ = on;
+    }
+    cv_job_.notify_all();
   }
   // The driver and the workers one per CPU of the process's affinity mask, on
   // the last CPUs of the mask (the first ones stay free for the threads that
@@ -423,33 +451,57 @@ class Executor {
     }
     j->ex = this;
     j->permanent = permanent;
+    if (permanent) ++captured_;
     return j;
   }
-  // host node: queue the job for the driver
+  // host node: queue the job for the driver (an unhealthy executor fails it at once)
   void start(Job* j) {
     {
       std::lock_guard<std::mutex> g(m_);
-      j->done = false;
-      queue_.push_back(j);
+      if (unhealthy_.load()) {
+        j->done = true;
+        j->failed = true;
+      } else {
+        j->done = false;
+        j->failed = false;
+        queue_.push_back(j);
+      }
     }
     cv_job_.notify_all();
+    cv_done_.notify_all();
   }
   // a job record that was never started goes back to the free list
   void discard(Job* j) {
     std::lock_guard<std::mutex> g(m_);
     if (!j->permanent) free_.push_back(j);
   }
-  // host node: block until the job is done; recycle it unless a graph holds it
-  void finish(Job* j) {
+  // host node: block until the job is done, or until the watchdog finds the
+  // driver and workers without progress for watchdog_ms (the reference's
+  // flag watchdog, moe/cpu_executor.py:602-656: a dead or wedged coordinator
+  // must not block the stream forever); recycle the record unless a graph
+  // holds it.  Returns false for a failed job.
+  bool finish(Job* j) {
     std::unique_lock<std::mutex> g(m_);
-    cv_done_.wait(g, [j] { return j->done; });
-    if (!j->permanent) free_.push_back(j);
-  }
-  // synchronous run (tests, callers without a stream)
-  void run(Job* j) {
-    start(j);
-    std::unique_lock<std::mutex> g(m_);
-    cv_done_.wait(g, [j] { return j->done; });
+    if (watchdog_ms_ <= 0) {
+      cv_done_.wait(g, [j] { return j->done; });
+    } else {
+      uint64_t seen = progress_.load(std::memory_order_relaxed);
+      auto since = std::chrono::steady_clock::now();
+      while (!cv_done_.wait_for(g, std::chrono::milliseconds(20), [j] { return j->done; })) {
+        const uint64_t p = progress_.load(std::memory_order_relaxed);
+        const auto now = std::chrono::steady_clock::now();
+        if (p != seen) {
+          seen = p;
+          since = now;
+        } else if (now - since >= std::chrono::milliseconds(watchdog_ms_)) {
+          poison(j);
+          break;
+        }
+      }
+    }
+    const bool ok = !j->failed;
+    if (!j->permanent && !j->abandoned) free_.push_back(j);
+    return ok;
   }
 
  private:
@@ -468,9 +520,29 @@ class Executor {
       gen_.fetch_add(1, std::memory_order_release);  // publishes fn_, units_, the counters
     }
     cv_work_.notify_all();
-    for (int u = next_.fetch_add(1); u < units; u = next_.fetch_add(1)) fn(u);
+    for (int u = next_.fetch_add(1); u < units; u = next_.fetch_add(1)) {
+      fn(u);
+      progress_.fetch_add(1, std::memory_order_relaxed);
+    }
     while (left_.load(std::memory_order_acquire) != 0) _mm_pause();
     fn_ = nullptr;
+  }
+  // The watchdog fired on j (m_ held): the executor is unhealthy for good, j
+  // and every queued job fail now so their waiters return; a job the driver
+  // is computing is abandoned (its record is never reused).
+  void poison(Job* j) {
+    unhealthy_.store(true);
+    const auto it = std::find(queue_.begin(), queue_.end(), j);
+    if (it != queue_.end()) queue_.erase(it);
+    else j->abandoned = true;
+    j->failed = true;
+    j->done = true;
+    for (Job* q : queue_) {
+      q->failed = true;
+      q->done = true;
+    }
+    queue_.clear();
+    cv_done_.notify_all();
   }
   void worker() {
     constexpr int kSpin = 4096;  // pauses before sleeping (~0.1 ms)
@@ -490,7 +562,10 @@ class Executor {
       seen = g;
       const std::function<void(int)>* fn = fn_;
       const int units = units_;
-      for (int u = next_.fetch_add(1); u < units; u = next_.fetch_add(1)) (*fn)(u);
+      for (int u = next_.fetch_add(1); u < units; u = next_.fetch_add(1)) {
+        (*fn)(u);
+        progress_.fetch_add(1, std::memory_order_relaxed);
+      }
       left_.fetch_sub(1, std::memory_order_acq_rel);
     }
   }
@@ -499,13 +574,14 @@ class Executor {
       Job* j;
       {
         std::unique_lock<std::mutex> g(m_);
-        cv_job_.wait(g, [this] { return stop_ || !queue_.empty(); });
+        cv_job_.wait(g, [this] { return stop_ || (!hold_ && !queue_.empty()); });
         if (stop_) return;
         j = queue_.front();
         queue_.pop_front();
         busy_ = true;
       }
       compute(*j);
+      progress_.fetch_add(1, std::memory_order_relaxed);
       {
         std::lock_guard<std::mutex> g(m_);
         j->done = true;
@@ -630,6 +706,11 @@ class Executor {
   std::atomic<int> next_{0};
   std::atomic<bool> stop_{false};
   bool busy_ = false;  // the driver is computing a job
+  bool hold_ = false;  // the driver takes no new job
+  int captured_ = 0;   // permanent (graph-captured) job records
+  int watchdog_ms_ = 10000;
+  std::atomic<uint64_t> progress_{0};  // work units and jobs completed
+  std::atomic<bool> unhealthy_{false};
   std::vector<float> xf_, act_, dout_;
   std::vector<bf16> act16_;
   bool bf16_dot_ = false;
@@ -683,7 +764,31 @@ ftmoe_cpu_executor* ftmoe_cpu_executor_create(int threads) {
   return reinterpret_cast<ftmoe_cpu_executor*>(new ftmoe_cpu::Executor(threads));
 }
 
-void ftmoe_cpu_executor_destroy(ftmoe_cpu_executor* ex) { delete reinterpret_cast<ftmoe_cpu::Executor*>(ex); }
+int ftmoe_cpu_executor_destroy(ftmoe_cpu_executor* ex, int graphs_released) {
+  if (!ex) return FTMOE_OK;
+  auto* e = reinterpret_cast<ftmoe_cpu::Executor*>(ex);
+  if (!graphs_released && e->captured_jobs() > 0) {
+    char msg[160];
+    std::snprintf(msg, sizeof(msg), "cpu_executor_destroy: %d job(s) captured into graphs may still replay",
+                  e->captured_jobs());
+    return ftmoe::report_error(FTMOE_ERR_BUSY, msg);
+  }
+  delete e;
+  return FTMOE_OK;
+}
+
+int ftmoe_cpu_executor_healthy(ftmoe_cpu_executor* ex) {
+  if (!ex) return FTMOE_ERR_INVALID;
+  return reinterpret_cast<ftmoe_cpu::Executor*>(ex)->healthy() ? FTMOE_OK : FTMOE_ERR_TIMEOUT;
+}
+
+void ftmoe_cpu_executor_set_watchdog(ftmoe_cpu_executor* ex, int ms) {
+  if (ex) reinterpret_cast<ftmoe_cpu::Executor*>(ex)->set_watchdog_ms(ms);
+}
+
+void ftmoe_cpu_executor_hold(ftmoe_cpu_executor* ex, int hold) {
+  if (ex) reinterpret_cast<ftmoe_cpu::Executor*>(ex)->hold(hold != 0);
+}
 
 const char* ftmoe_cpu_executor_isa(ftmoe_cpu_executor* ex) {
   return ex ? reinterpret_cast<ftmoe_cpu::Executor*>(ex)->isa() : "";
@@ -697,8 +802,10 @@ int ftmoe_cpu_experts(ftmoe_cpu_executor* ex, const ftmoe_bank* bank, const void
   auto* e = reinterpret_cast<ftmoe_cpu::Executor*>(ex);
   ftmoe_cpu::Job* j = e->new_job(false);
   ftmoe_cpu::fill(j, bank, x, w, ids, M, k, activation, y);
-  e->run(j);
-  e->finish(j);
+  e->start(j);
+  if (!e->finish(j))
+    return ftmoe::report_error(FTMOE_ERR_TIMEOUT, "cpu_experts: the executor's watchdog fired (no progress); "
+                               "the executor is unhealthy");
   return FTMOE_OK;
 }
 

@@ -71,6 +71,12 @@ hipError_t launch_grouped_sigmoid(const float* logits, const float* bias, int M,
                                   int topk_group, int k, int renorm, float scale, float* w, int32_t* ids,
                                   hipStream_t stream);
 hipError_t launch_align(const AlignArgs& a, hipStream_t stream);
+// Rows up to which the counting align keeps per-row counts in LDS; decode-form
+// calls over larger banks take the sort-based align, which bounds the routes
+// of one call instead.
+constexpr int kCountMaxRows = 1023;
+constexpr int kSortMaxRows = 16383;
+constexpr int kSortMaxRoutes = 16384;
 
 // A router call (softmax top-k or grouped sigmoid top-k) feeding the decode
 // permutation.
@@ -153,6 +159,7 @@ struct LruArgs {
   int32_t* num_missing;   // [1] distinct missing experts before the cap
   int32_t* cpu_ids;       // nullable [numel]: the expert id of an unfetched miss, else -1
   long long* stats;       // nullable [4] accumulated: active, missing, calls, missed routes
+  long long* unserved;    // nullable [1] accumulated: misses left unfetched for want of a free slot
 };
 hipError_t launch_lru_ensure(const LruArgs& a, hipStream_t stream);
 

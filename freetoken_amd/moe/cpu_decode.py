@@ -32,12 +32,13 @@ def hybrid_fetch_fraction(pcie_gbs: float, cpu_gbs: float, overlapped: bool = Tr
 
 
 class CpuMoeDecoder:
-    def __init__(self, cache: ExpertSlotCache, top_k: int, threads: int = 0, activation: str = "silu"):
+    def __init__(self, cache: ExpertSlotCache, top_k: int, threads: int = 0, activation: str = "silu",
+                 watchdog_s: float | None = None):
         assert cache.sources, "the CPU share reads the cache's host sources: set_bank_sources first"
         self.cache = cache
         self.top_k = top_k
         self.activation = activation
-        self.executor = ops.CpuExecutor(threads)
+        self.executor = ops.CpuExecutor(threads, watchdog_s=watchdog_s)
         self._io: dict[int, dict[str, torch.Tensor]] = {}
         self._banks: dict[int, ops.ExpertBank] = {}
 
@@ -70,6 +71,7 @@ class CpuMoeDecoder:
         bs, hidden = hidden_states.shape
         if topk_ids.shape != (bs, self.top_k):
             raise ValueError(f"topk_ids {tuple(topk_ids.shape)} != ({bs}, {self.top_k})")
+        self.raise_if_unhealthy()
         io = self._io_for(bs, hidden)
         io["x"].copy_(hidden_states, non_blocking=True)
         io["ids"].copy_(topk_ids, non_blocking=True)
@@ -88,5 +90,11 @@ class CpuMoeDecoder:
     def decode(self, layer_id: int, hidden_states, topk_weights, topk_ids) -> torch.Tensor:
         return self.decode_sync(self.decode_submit(layer_id, hidden_states, topk_weights, topk_ids))
 
-    def close(self) -> None:
-        self.executor.close()
+    def raise_if_unhealthy(self) -> None:
+        """Raises once the executor's watchdog has fired (a host read, no
+        device synchronisation): callers replaying captured steps check it
+        once per step, as the reference's engine does (moe/cpu_executor.py:643-656)."""
+        self.executor.raise_if_unhealthy()
+
+    def close(self, graphs_released: bool = False) -> None:
+        self.executor.close(graphs_released=graphs_released)

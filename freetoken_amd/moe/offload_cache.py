@@ -77,6 +77,8 @@ class ExpertSlotCache:
         self.id_of_slot = torch.full((cache_size,), -1, dtype=torch.int32, device=self.device)
         self.collect_stats = True
         self.lru_stats = torch.zeros((num_layers, N_STATS), dtype=torch.int64, device=self.device)
+        # misses left without a slot because every slot held an expert of the same call
+        self.unserved = torch.zeros((num_layers,), dtype=torch.int64, device=self.device)
         self.banks: "OrderedDict[str, torch.Tensor]" = OrderedDict()
         # admission state (moe/offload_cache.py:155-200)
         dev = self.device
@@ -188,7 +190,7 @@ class ExpertSlotCache:
         ops.lru_ensure(expert_ids, layer_id, self.slot_for_id, self.id_of_slot, self.usage, self.step,
                        self.evict_slots, self.src_indices, self.num_indices, self.num_missing_full,
                        recency=recency, max_fetch=max_fetch, stats=stats, fetch_fraction=fetch_fraction,
-                       cpu_ids=cpu_ids)
+                       cpu_ids=cpu_ids, unserved=self.unserved[layer_id:layer_id + 1])
         self._pending_src_layer = layer_id
         return expert_ids
 
@@ -287,6 +289,16 @@ class ExpertSlotCache:
     # -------------------------------------------------------------- statistics
     def reset_stats(self) -> None:
         self.lru_stats.zero_()
+        self.unserved.zero_()
+
+    def check_capacity(self) -> None:
+        """Raises when an admission since the last ``reset_stats`` left misses
+        without a slot (a call routed to more distinct experts than the cache
+        holds: their routes were skipped).  Synchronises with the device."""
+        n = int(self.unserved.sum())
+        if n:
+            raise RuntimeError(f"expert cache too small: {n} missing experts found no free slot "
+                               f"(cache_size {self.cache_size}); their routes were skipped")
 
     def decode_miss_stats(self) -> dict:
         active, missing, calls, missed_routes = (int(x) for x in self.lru_stats.sum(0))
@@ -296,4 +308,5 @@ class ExpertSlotCache:
             "missing_per_layer": missing / calls if calls else 0.0,
             "miss_rate": missing / active if active else 0.0,
             "missed_routes": missed_routes,
+            "unserved_experts": int(self.unserved.sum()),
         }

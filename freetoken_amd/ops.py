@@ -128,8 +128,8 @@ def slot_map(topk_ids: torch.Tensor, slot_for_id: torch.Tensor, out: torch.Tenso
 def lru_ensure(expert_ids: torch.Tensor, layer_id: int, slot_for_id: torch.Tensor, id_of_slot: torch.Tensor,
                usage: torch.Tensor, step: torch.Tensor, evict_slots: torch.Tensor, src_indices: torch.Tensor,
                num_indices: torch.Tensor, num_missing: torch.Tensor, recency: torch.Tensor | None = None,
-               max_fetch: int = -1, stats: torch.Tensor | None = None, fetch_fraction: float = 0.0,
-               cpu_ids: torch.Tensor | None = None) -> torch.Tensor:
+               max_fetch: int = -1, stats: torch.Tensor | None = None, fetch_fraction: float | None = 0.0,
+               cpu_ids: torch.Tensor | None = None, unserved: torch.Tensor | None = None) -> torch.Tensor:
     """LRU admission of a call's experts into the slot cache; ``expert_ids``
     (int32) are rewritten to slots in place (see ftmoe_lru_ensure).
     ``slot_for_id`` [L, E] int32, ``id_of_slot`` [S] int32, ``usage`` [S] and
@@ -138,8 +138,11 @@ def lru_ensure(expert_ids: torch.Tensor, layer_id: int, slot_for_id: torch.Tenso
     ``max_fetch`` cap with the bandwidth-matched share of the misses, in Q16
     as the reference rounds it (moe/offload_kernels.py:58); ``cpu_ids``
     (int32, shaped like ``expert_ids``) receives the unfetched misses' expert
-    ids and -1 elsewhere."""
-    frac_q16 = min(1 << 16, max(0, round(fetch_fraction * (1 << 16))))
+    ids and -1 elsewhere.  At most as many misses are admitted as there are
+    slots that hold no expert of this call; ``unserved`` (int64 [1]) accumulates
+    the misses left without a slot for that reason.  A ``fetch_fraction`` of
+    None (no measured rates) means the fixed ``max_fetch`` cap."""
+    frac_q16 = 0 if fetch_fraction is None else min(1 << 16, max(0, round(fetch_fraction * (1 << 16))))
     i32 = (expert_ids, slot_for_id, id_of_slot, evict_slots, src_indices, num_indices, num_missing)
     if cpu_ids is not None and (cpu_ids.dtype != torch.int32 or cpu_ids.shape != expert_ids.shape
                                 or not cpu_ids.is_contiguous()):
@@ -150,7 +153,9 @@ def lru_ensure(expert_ids: torch.Tensor, layer_id: int, slot_for_id: torch.Tenso
         raise ValueError("usage, step and recency must be int64")
     if stats is not None and stats.dtype != torch.int64:
         raise ValueError("stats must be int64[4]")
-    _require_gpu(*i32, usage, step, recency, stats, cpu_ids)
+    if unserved is not None and unserved.dtype != torch.int64:
+        raise ValueError("unserved must be int64[1]")
+    _require_gpu(*i32, usage, step, recency, stats, cpu_ids, unserved)
     if not expert_ids.is_contiguous():
         raise ValueError("expert_ids must be contiguous")
     num_layers, num_experts = slot_for_id.shape
@@ -161,7 +166,7 @@ def lru_ensure(expert_ids: torch.Tensor, layer_id: int, slot_for_id: torch.Tenso
                                _ptr(slot_for_id), _ptr(id_of_slot), _ptr(usage), _ptr(step), id_of_slot.numel(),
                                _ptr(recency), max_fetch, frac_q16, _ptr(evict_slots), _ptr(src_indices),
                                min(evict_slots.numel(), src_indices.numel()), _ptr(num_indices), _ptr(num_missing),
-                               _ptr(cpu_ids), _ptr(stats), _stream(expert_ids.device)),
+                               _ptr(cpu_ids), _ptr(stats), _ptr(unserved), _stream(expert_ids.device)),
         "lru_ensure",
     )
     return expert_ids
@@ -322,23 +327,48 @@ class ExpertBank:
 
 class _Workspace:
     """Per-device scratch buffer, grown on demand (never during graph capture:
-    size it with a warm-up call at the largest batch first)."""
+    size it with a warm-up call at the largest batch first).
+
+    A captured graph keeps the raw address of the buffer it was captured
+    with.  A buffer handed to a capture is therefore never given back to the
+    allocator when a later, larger eager call (a prefill after the decode
+    graphs were captured) grows the workspace: it is retired and kept, so
+    replays of those graphs still write memory they own.  ``release_retired``
+    frees the retired buffers once the graphs that used them are gone."""
 
     def __init__(self):
         self.buf: dict[int, torch.Tensor] = {}
+        self.captured: dict[int, bool] = {}
+        self.retired: dict[int, list[torch.Tensor]] = {}
 
     def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
         idx = device.index if device.index is not None else torch.cuda.current_device()
         cur = self.buf.get(idx)
+        capturing = torch.cuda.is_current_stream_capturing()
         if cur is None or cur.numel() < nbytes:
-            if torch.cuda.is_current_stream_capturing():
+            if capturing:
                 raise RuntimeError("ftmoe workspace must be sized before graph capture (run one eager call)")
+            if cur is not None and self.captured.get(idx):
+                self.retired.setdefault(idx, []).append(cur)
             cur = torch.empty((max(nbytes, 1 << 20),), dtype=torch.uint8, device=device)
             self.buf[idx] = cur
+            self.captured[idx] = False
+        if capturing:
+            self.captured[idx] = True
         return cur
+
+    def release_retired(self, device: torch.device | None = None) -> None:
+        for idx in ([device.index] if device is not None else list(self.retired)):
+            self.retired.pop(idx, None)
 
 
 _WS = _Workspace()
+
+
+def release_retired_workspaces(device: torch.device | None = None) -> None:
+    """Frees workspace buffers superseded after a graph capture used them; call
+    only once every graph captured with them has been destroyed."""
+    _WS.release_retired(device)
 
 
 def experts_decode(x: torch.Tensor, topk_w: torch.Tensor, topk_ids: torch.Tensor, bank: ExpertBank,
@@ -503,13 +533,24 @@ def experts_prefill(x: torch.Tensor, topk_w: torch.Tensor, topk_ids: torch.Tenso
 # --------------------------------------------------------------------------- CPU executor
 
 
+# executors whose jobs were captured into graphs that may still replay: kept
+# for the life of the process rather than freed under those graphs
+_KEPT_EXECUTORS: list = []
+
+
 class CpuExecutor:
     """Host-side expert executor of the hybrid decode (ftmoe_cpu_executor):
     ``run`` computes synchronously; ``submit`` / ``wait`` order the job on a
     stream (host-function nodes) so that GPU work queued between them overlaps
-    it.  Inputs and outputs are host tensors (pinned for the stream path)."""
+    it.  Inputs and outputs are host tensors (pinned for the stream path).
 
-    def __init__(self, threads: int = 0):
+    A watchdog (``watchdog_s``, default ``FTMOE_CPU_WATCHDOG_S`` or 10 s)
+    fails a job whose wait sees no progress of the pool for that long, so a
+    stalled pool cannot block a stream for ever; the executor is then
+    unhealthy and ``raise_if_unhealthy`` raises (the reference's flag
+    watchdog and ``raise_if_unhealthy``, moe/cpu_executor.py:602-656)."""
+
+    def __init__(self, threads: int = 0, watchdog_s: float | None = None):
         if threads <= 0:  # the process's CPU share (OMP_NUM_THREADS when set, else the affinity
             # mask) less one CPU for the thread that enqueues the GPU's share and the stream's host functions
             share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
@@ -518,15 +559,45 @@ class CpuExecutor:
         self._h = lib().ftmoe_cpu_executor_create(threads)
         if not self._h:
             raise RuntimeError("ftmoe_cpu_executor_create failed")
+        if watchdog_s is not None:
+            self.set_watchdog(watchdog_s)
 
     @property
     def isa(self) -> str:
         return lib().ftmoe_cpu_executor_isa(self._h).decode()
 
-    def close(self) -> None:
-        if self._h:
-            lib().ftmoe_cpu_executor_destroy(self._h)
-            self._h = None
+    def set_watchdog(self, seconds: float) -> None:
+        """Seconds without progress before a waited-for job fails (0: never)."""
+        lib().ftmoe_cpu_executor_set_watchdog(self._h, int(round(seconds * 1000)))
+
+    def hold(self, on: bool) -> None:
+        """Keeps the pool from starting jobs while ``on`` (maintenance; tests of the watchdog)."""
+        lib().ftmoe_cpu_executor_hold(self._h, int(bool(on)))
+
+    @property
+    def healthy(self) -> bool:
+        return lib().ftmoe_cpu_executor_healthy(self._h) == _lib.FTMOE_OK
+
+    def raise_if_unhealthy(self) -> None:
+        """Raises once the watchdog has fired: outputs of the failed jobs were
+        never written and the executor must be replaced."""
+        if self._h and not self.healthy:
+            raise RuntimeError("CPU expert executor watchdog fired: a job saw no progress of the pool within "
+                               "the watchdog period; its outputs were not computed. Replace the executor.")
+
+    def close(self, graphs_released: bool = False) -> None:
+        """Frees the executor once the host functions queued on streams have run
+        (the device is synchronised first).  While jobs captured into graphs
+        exist the executor is kept alive instead, unless ``graphs_released``
+        says those graphs are destroyed: a replay would touch a freed executor."""
+        if not self._h:
+            return
+        if torch.cuda.is_available() and torch.cuda.is_initialized():
+            torch.cuda.synchronize()
+        rc = lib().ftmoe_cpu_executor_destroy(self._h, int(graphs_released))
+        if rc == _lib.FTMOE_ERR_BUSY:
+            _KEPT_EXECUTORS.append(self._h)
+        self._h = None
 
     def __del__(self):
         try:

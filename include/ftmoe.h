@@ -36,7 +36,9 @@ enum ftmoe_status {
   FTMOE_ERR_INVALID = -1,     /* bad argument (null pointer, shape mismatch) */
   FTMOE_ERR_UNSUPPORTED = -2, /* valid but unsupported shape or format */
   FTMOE_ERR_HIP = -3,         /* a HIP runtime call failed */
-  FTMOE_ERR_WORKSPACE = -4    /* workspace smaller than *_workspace() */
+  FTMOE_ERR_WORKSPACE = -4,   /* workspace smaller than *_workspace() */
+  FTMOE_ERR_BUSY = -5,        /* the object is still referenced (captured graphs) */
+  FTMOE_ERR_TIMEOUT = -6      /* a watchdog found no progress; the object is unhealthy */
 };
 
 enum ftmoe_dtype { FTMOE_DTYPE_F32 = 0, FTMOE_DTYPE_BF16 = 1 };
@@ -124,7 +126,10 @@ int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_i
  *   recent first then ascending id; the first min(misses, cap, capacity) of
  *   them take, one after the other, the slot with the
  *   smallest (usage, slot) -- its previous owner, of any layer, is unmapped
- *   -- and are listed in evict_slots / src_indices (layer-local rows);
+ *   -- and are listed in evict_slots / src_indices (layer-local rows), at
+ *   most as many as there are slots with usage < step after the touch (no
+ *   slot is taken twice, and no slot of an expert of this call is taken: the
+ *   exclusion of the reference's GPU kernel, offload_kernels.py:369-387);
  *   recency of every seen expert = step; expert_ids are rewritten in place to
  *   slots (-1 for unfetched misses and ids outside [0, num_experts)).
  *   cap = max_fetch (< 0: no cap); with fetch_frac_q16 in (0, 65536] (the
@@ -138,13 +143,16 @@ int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_i
  *   id_of_slot int32 [cache_size] (flat ids, -1 empty), usage int64
  *   [cache_size], step int64 [1]; num_indices / num_missing int32 [1] receive
  *   the admitted and the missing counts; stats (nullable) int64 [4] is
- *   accumulated as in ftmoe_slot_map, counted before admission.
+ *   accumulated as in ftmoe_slot_map, counted before admission; unserved
+ *   (nullable) int64 [1] accumulates the misses the cap admitted but no free
+ *   slot (or staging entry) could take -- nonzero means the cache is smaller
+ *   than a call's distinct experts.
  * num_experts, cache_size <= 8192. */
 int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layers, int num_experts,
                      int32_t* slot_for_id, int32_t* id_of_slot, int64_t* usage, int64_t* step, int cache_size,
                      int64_t* recency, int max_fetch, int fetch_frac_q16, int32_t* evict_slots,
                      int32_t* src_indices, int capacity, int32_t* num_indices, int32_t* num_missing,
-                     int32_t* cpu_ids, int64_t* stats, ftmoe_stream_t stream);
+                     int32_t* cpu_ids, int64_t* stats, int64_t* unserved, ftmoe_stream_t stream);
 
 /* Exact-size pinned host memory (hipHostMalloc), for the host expert banks:
  * replaces alloc_pinned_tensor (kernel/pinned.py:42-45).  torch's pinned
@@ -207,7 +215,9 @@ int ftmoe_act_quant_fp8(const void* x, int rows, int K, int mode, void* q, void*
  *   (ids outside [0, num_rows) are skipped); shared: nullable bank with
  *   num_rows == 1 whose output is added; y bf16 [M,H] (may not alias x).
  * apply_router_weight_on_input scales the gate_up outputs instead of the
- * down outputs (moe/fused.py:240). */
+ * down outputs (moe/fused.py:240).
+ * num_rows <= 16383 (an expert cache's slots); above 1023 rows a call holds
+ * at most 16384 routes (M * k). */
 size_t ftmoe_experts_decode_workspace(int M, int top_k, const ftmoe_bank* bank, const ftmoe_bank* shared);
 int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
                          const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
@@ -281,9 +291,29 @@ int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, 
  * threads <= 0: one per hardware thread. */
 typedef struct ftmoe_cpu_executor ftmoe_cpu_executor;
 ftmoe_cpu_executor* ftmoe_cpu_executor_create(int threads);
-void ftmoe_cpu_executor_destroy(ftmoe_cpu_executor* ex);
+/* Waits for queued jobs and frees the executor.  Refused (FTMOE_ERR_BUSY,
+ * nothing freed) while jobs captured into graphs exist, unless
+ * graphs_released says that every such graph is destroyed: a replay would
+ * run their host functions against the freed executor.  Host functions still
+ * queued on a stream must have run (synchronise the stream first). */
+int ftmoe_cpu_executor_destroy(ftmoe_cpu_executor* ex, int graphs_released);
 const char* ftmoe_cpu_executor_isa(ftmoe_cpu_executor* ex);
-/* Synchronous run on the calling thread's behalf. */
+/* Watchdog (replaces the flag watchdog of moe/cpu_executor.py:602-656): a
+ * wait for a job (the stream's wait host function, or a synchronous run) that
+ * sees neither the job done nor any progress of the pool (a work unit or a
+ * job completed) for the watchdog period fails the job and every queued one,
+ * returns (so the stream is not blocked for ever), and marks the executor
+ * unhealthy for good: later jobs fail at once.  Their outputs are not
+ * written; callers check ftmoe_cpu_executor_healthy once per step (0 =
+ * healthy, FTMOE_ERR_TIMEOUT after the watchdog fired).  The period is
+ * FTMOE_CPU_WATCHDOG_S seconds (default 10; 0 turns the watchdog off) or
+ * set_watchdog's milliseconds.  hold != 0 keeps the driver from starting
+ * jobs (maintenance; tests force a stalled pool with it). */
+int ftmoe_cpu_executor_healthy(ftmoe_cpu_executor* ex);
+void ftmoe_cpu_executor_set_watchdog(ftmoe_cpu_executor* ex, int ms);
+void ftmoe_cpu_executor_hold(ftmoe_cpu_executor* ex, int hold);
+/* Synchronous run on the calling thread's behalf (FTMOE_ERR_TIMEOUT when the
+ * watchdog fired). */
 int ftmoe_cpu_experts(ftmoe_cpu_executor* ex, const ftmoe_bank* host_bank, const void* x, const float* w,
                       const int32_t* ids, int M, int k, int activation, void* y);
 /* Stream-ordered run: _submit enqueues a host function that starts the job when

@@ -16,7 +16,9 @@ the invariant slot_for_id[id_of_slot[s]] == s.
 ``lru_ensure`` restates the admission of the miss path from the reference's
 CPU mirror of its admission kernel (``moe/offload_kernels.py:128-188``,
 ``_ensure_experts_hybrid_cpu``, which the reference holds bit-identical to its
-GPU kernel; fixed cap, ``frac_q16 == 0``), with the miss order "lowest_id"
+GPU kernel; fixed cap, ``frac_q16 == 0``), limited to the slots its GPU
+kernel may take (``:369-387``: none holding an expert of the call or admitted
+by it), with the miss order "lowest_id"
 (``by_recency=False``) or "recency" (``:9-16``).  The uncapped lowest-id form
 stands for flashlib's ``lru_ensure`` (``:19-40``), whose own order is not
 available (third-party, absent): parity with flashlib is unpinned; the form
@@ -62,6 +64,7 @@ class CacheState:
         self.usage = np.zeros(cache_size, dtype=np.int64)
         self.step = 0
         self.recency = np.zeros((num_layers, num_experts), dtype=np.int64)
+        self.unserved = np.zeros(num_layers, dtype=np.int64)
 
     def copy(self) -> "CacheState":
         c = CacheState(self.L, self.E, self.S)
@@ -70,6 +73,7 @@ class CacheState:
         c.usage = self.usage.copy()
         c.step = self.step
         c.recency = self.recency.copy()
+        c.unserved = self.unserved.copy()
         return c
 
 
@@ -168,8 +172,16 @@ def lru_ensure(state: CacheState, layer: int, expert_ids, max_fetch: int = -1, b
     n = len(missing) if max_fetch < 0 else min(len(missing), max_fetch)
     if frac_q16 > 0:
         n = fraction_cap(len(missing), frac_q16)
+    wanted = n
     if capacity is not None:
         n = min(n, capacity)
+    # only slots that hold no expert of this call and were not admitted by it
+    # (usage < step) may be taken: the exclusion of the reference's GPU kernel
+    # (offload_kernels.py:369-387).  Its CPU mirror (:163-174) takes the
+    # smallest (usage, slot) unconditionally, which re-picks a slot admitted in
+    # the same call once the free slots run out; both agree while they last.
+    n = min(n, int((state.usage < step).sum()))
+    state.unserved[layer] += wanted - n
     evict, src = [], []
     miss_set = set(missing)
     for idx in range(n):  # one victim after the other (:163-174)

@@ -131,3 +131,66 @@ def test_hybrid_fetch_fraction_rule():
     assert hybrid_fetch_fraction(50.0, 80.0, overlapped=False) == pytest.approx(0.625)
     assert hybrid_fetch_fraction(120.0, 100.0, overlapped=False) == 1.0
     assert hybrid_fetch_fraction(0.0, 100.0) is None
+
+
+def _small_job(rng, fmt="bf16", M=2, k=2):
+    E, H, I = 4, 128, 128
+    bank = synth.make_bank(fmt, E, H, I, rng)
+    x = synth.activations(rng, M, H)
+    w, ids = oracle.routing.softmax_topk(synth.normal(rng, (M, E)), k, True)
+    args = (to_device_bank(bank, "cpu"), _host(x, np.float32).to(torch.bfloat16), _host(w, np.float32),
+            _host(ids, np.int32))
+    return args, oracle.experts.moe_layer("decode", x, w, ids, bank, None)
+
+
+def test_watchdog_fails_a_stalled_job_and_poisons_the_executor():
+    """A pool that makes no progress (the driver held from the host) turns the
+    wait into an error after the watchdog period instead of blocking for ever;
+    the executor stays unhealthy and fails later jobs at once (the reference's
+    flag watchdog, moe/cpu_executor.py:602-656)."""
+    import time
+
+    rng = np.random.default_rng(41)
+    ex = ops.CpuExecutor(threads=2, watchdog_s=0.3)
+    args, y_ref = _small_job(rng)
+    y = ex.run(*args)
+    assert max_rel(y.float().numpy(), y_ref) <= MAX_REL_TOL and ex.healthy
+    ex.hold(True)
+    t0 = time.monotonic()
+    with pytest.raises(_lib.FtmoeError, match="watchdog"):
+        ex.run(*args)
+    assert 0.25 <= time.monotonic() - t0 < 5.0
+    assert not ex.healthy
+    with pytest.raises(RuntimeError, match="watchdog fired"):
+        ex.raise_if_unhealthy()
+    ex.hold(False)
+    t0 = time.monotonic()
+    with pytest.raises(_lib.FtmoeError, match="watchdog"):  # unhealthy for good: fails without waiting
+        ex.run(*args)
+    assert time.monotonic() - t0 < 0.25
+    ex.close()
+
+
+def test_watchdog_spares_a_working_pool():
+    """With the watchdog armed, jobs of a working pool complete normally, many
+    times in a row, and a job that waits behind others is not failed."""
+    rng = np.random.default_rng(43)
+    ex = ops.CpuExecutor(threads=2, watchdog_s=0.5)
+    args, y_ref = _small_job(rng, "fp8", M=4, k=2)
+    for _ in range(20):
+        y = ex.run(*args)
+        assert max_rel(y.float().numpy(), y_ref) <= MAX_REL_TOL
+    assert ex.healthy
+    ex.raise_if_unhealthy()
+    ex.close()
+
+
+def test_destroy_refused_while_captured_jobs_may_replay():
+    """The C ABI refuses to free an executor that holds no captured jobs only
+    when asked to keep them: with none captured, destroy succeeds at once."""
+    L = _lib.lib()
+    h = L.ftmoe_cpu_executor_create(1)
+    assert h
+    assert L.ftmoe_cpu_executor_healthy(h) == _lib.FTMOE_OK
+    assert L.ftmoe_cpu_executor_destroy(h, 0) == _lib.FTMOE_OK
+    assert L.ftmoe_cpu_executor_destroy(None, 0) == _lib.FTMOE_OK

@@ -37,12 +37,13 @@ class _DevCache:
         self.n = torch.zeros(1, dtype=torch.int32, device=dev)
         self.nmiss = torch.zeros(1, dtype=torch.int32, device=dev)
         self.stats = torch.zeros(4, dtype=torch.int64, device=dev)
+        self.unserved = torch.zeros(st.L, dtype=torch.int64, device=dev)
 
     def ensure(self, layer, ids, max_fetch, by_recency):
         t = torch.from_numpy(np.ascontiguousarray(ids, dtype=np.int32)).to(self.slot_for_id.device)
         ops.lru_ensure(t, layer, self.slot_for_id, self.id_of_slot, self.usage, self.step, self.evict, self.src,
                        self.n, self.nmiss, recency=self.recency[layer] if by_recency else None,
-                       max_fetch=max_fetch, stats=self.stats)
+                       max_fetch=max_fetch, stats=self.stats, unserved=self.unserved[layer:layer + 1])
         return t
 
     def check(self, st: S.CacheState, by_recency: bool):
@@ -52,11 +53,13 @@ class _DevCache:
         assert int(self.step.item()) == st.step
         if by_recency:
             np.testing.assert_array_equal(to_np(self.recency), st.recency)
+        np.testing.assert_array_equal(to_np(self.unserved), st.unserved)
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("L,E,Sz,max_k,max_fetch,by_recency", [
-    (1, 16, 4, 6, -1, False),      # more misses than slots: the sequential rule
+    (1, 16, 4, 6, -1, False),      # more misses than free slots: only the free ones are taken
+    (2, 32, 5, 12, -1, True),      # likewise, most recent first
     (3, 64, 24, 12, -1, False),
     (2, 256, 64, 64, -1, False),   # C4-like table, decode batch 8
     (2, 128, 40, 40, 5, True),     # capped, most recent first
@@ -85,6 +88,7 @@ def test_lru_ensure_matches_oracle(dev, L, E, Sz, max_k, max_fetch, by_recency):
         assert k == evict.size and int(dc.nmiss.item()) == nmiss, (call, k, evict.size)
         np.testing.assert_array_equal(to_np(dc.evict)[:k], evict)
         np.testing.assert_array_equal(to_np(dc.src)[:k], src)
+        assert np.unique(evict).size == evict.size, (call, evict)  # no slot taken twice
         dc.check(st, by_recency)
     np.testing.assert_array_equal(to_np(dc.stats), acc)
 
@@ -162,7 +166,45 @@ def test_offload_layer_admits_and_fetches_misses(dev, fmt):
         g = to_np(y)
         assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, (fmt, call, max_rel(g, y_ref))
     st = cache.decode_miss_stats()
-    assert st["layer_calls"] == 6 and st["missing_per_layer"] > 0
+    assert st["layer_calls"] == 6 and st["missing_per_layer"] > 0 and st["unserved_experts"] == 0
+    cache.check_capacity()
+
+
+@pytest.mark.gpu
+def test_undersized_cache_counts_unserved_misses(dev):
+    """A call routed to more distinct experts than the cache has slots: the free
+    slots are taken once each (no slot admitted twice in the call), the misses
+    left over are skipped and counted, and check_capacity raises.  The served
+    routes equal the oracle with the unserved ones skipped."""
+    rng = np.random.default_rng(71)
+    E, Sz, H, I, k, M = 16, 4, 512, 256, 2, 3
+    bank = synth.make_bank("fp8", E, H, I, rng)
+    cache = ExpertSlotCache(1, E, Sz, "fp8_block", device=dev)
+    eb = to_device_bank(bank, dev, rows=np.arange(Sz))
+    cache.set_bank_caches(gate_up=eb.gate_up, gate_up_scale=eb.gate_up_scale, down=eb.down, down_scale=eb.down_scale)
+    names, host = _pinned_bank_sources(bank)
+    cache.set_bank_sources({n: [h] for n, h in zip(names, host)})
+    cache.reset()
+    layer = OffloadMoELayer(0, E, k, H, I, device=dev)
+    layer.offload_cache = cache
+    ids_ref = np.array([[0, 1], [2, 3], [4, 5]], dtype=np.int32)
+    w_ref = np.full((M, k), 0.5, dtype=np.float32)
+    x = synth.activations(rng, M, H)
+    ids = torch.from_numpy(ids_ref.copy()).to(dev)
+    with moe_phase("decode", backend="offload"):
+        y = layer.routed_forward(bf16_dev(x, dev), torch.from_numpy(w_ref).to(dev), ids)
+    torch.cuda.synchronize()
+    got_ids = to_np(ids)
+    assert got_ids[:2].tolist() == [[0, 1], [2, 3]] and got_ids[2].tolist() == [-1, -1]
+    served = np.where(got_ids >= 0, ids_ref, -1).astype(np.int32)
+    y_ref = oracle.experts.moe_layer("decode", x, w_ref, served, bank, None)
+    g = to_np(y)
+    assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL
+    assert cache.decode_miss_stats()["unserved_experts"] == 2
+    with pytest.raises(RuntimeError, match="expert cache too small"):
+        cache.check_capacity()
+    cache.reset_stats()
+    cache.check_capacity()
 
 
 @pytest.mark.gpu

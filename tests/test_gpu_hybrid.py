@@ -203,4 +203,38 @@ def test_hybrid_replays_in_a_graph(dev):
     np.testing.assert_array_equal(to_np(cache.slot_for_id), st.slot_for_id)
     del graph
     torch.cuda.synchronize()
-    cache.cpu_executor.close()
+    cache.cpu_executor.close(graphs_released=True)
+
+
+@pytest.mark.gpu
+def test_stream_wait_unblocks_on_watchdog(dev):
+    """The stream-ordered CPU job with a stalled pool (held from the host): the
+    stream's wait host function returns after the watchdog period instead of
+    blocking the stream for ever, later stream work runs, and the executor
+    reports the failure (moe/cpu_executor.py:602-656)."""
+    import time
+
+    from freetoken_amd import ops
+
+    rng = np.random.default_rng(97)
+    E, H, I, M, k = 4, 256, 128, 2, 2
+    bank = synth.make_bank("bf16", E, H, I, rng)
+    hb = to_device_bank(bank, "cpu")
+    x = torch.from_numpy(synth.activations(rng, M, H)).to(torch.bfloat16).pin_memory()
+    w = torch.full((M, k), 0.5, dtype=torch.float32).pin_memory()
+    ids = torch.tensor([[0, 1], [2, 3]], dtype=torch.int32).pin_memory()
+    y = torch.zeros((M, H), dtype=torch.bfloat16).pin_memory()
+    ex = ops.CpuExecutor(threads=2, watchdog_s=0.3)
+    ex.hold(True)
+    marker = torch.zeros(1, device=dev)
+    t0 = time.monotonic()
+    job = ex.submit(hb, x, w, ids, y, device=dev)
+    ex.wait(job, device=dev)
+    marker += 1  # stream work after the wait
+    torch.cuda.synchronize()
+    assert 0.25 <= time.monotonic() - t0 < 10.0
+    assert float(marker.item()) == 1.0 and not ex.healthy
+    with pytest.raises(RuntimeError, match="watchdog fired"):
+        ex.raise_if_unhealthy()
+    ex.hold(False)
+    ex.close()

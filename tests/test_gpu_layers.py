@@ -196,3 +196,61 @@ def test_registry_and_construction_seam():
     assert type(off) is OffloadMoELayer and off.layer_id == 3 and not hasattr(off, "gate_up_proj")
     with pytest.raises(AssertionError):
         make_moe_layer(cfg)  # offload layers need their layer id
+
+
+@pytest.mark.gpu
+def test_graph_replay_after_workspace_growth(dev, monkeypatch):
+    """Capture-then-prefill (the reference's engine/graph.py:127-187 order):
+    decode captured in a graph, then an eager prefill that needs a larger
+    workspace, then replays.  The buffer the graph captured must stay owned by
+    the workspace: a tensor allocated after the growth is never written by a
+    replay, and every replay and the prefill match the oracle."""
+    monkeypatch.setattr(ops, "_WS", ops._Workspace())  # start from an empty workspace
+    rng = np.random.default_rng(131)
+    E, H, I, k, M, Mp = 32, 1024, 512, 8, 8, 512
+    bank = synth.make_bank("fp8", E, H, I, rng)
+    shared = synth.make_bank("fp8", 1, H, I, rng)
+    dbank, dshared = to_device_bank(bank, dev), to_device_bank(shared, dev)
+    x_buf = torch.zeros((M, H), dtype=torch.bfloat16, device=dev)
+    w_buf = torch.zeros((M, k), dtype=torch.float32, device=dev)
+    ids_buf = torch.zeros((M, k), dtype=torch.int32, device=dev)
+
+    def routing(m):
+        w_ref, ids_ref = oracle.routing.softmax_topk(synth.normal(rng, (m, E)), k, True)
+        return synth.activations(rng, m, H), w_ref, ids_ref
+
+    x, w_ref, ids_ref = routing(M)
+    x_buf.copy_(bf16_dev(x, dev))
+    w_buf.copy_(torch.from_numpy(w_ref))
+    ids_buf.copy_(torch.from_numpy(ids_ref))
+    ops.experts_decode(x_buf, w_buf, ids_buf, dbank, dshared)  # eager call sizes the workspace
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            y = ops.experts_decode(x_buf, w_buf, ids_buf, dbank, dshared)
+    torch.cuda.synchronize()
+    captured = ops._WS.buf[dev.index or 0]
+    cap_ptr, cap_bytes = captured.data_ptr(), captured.numel()
+    del captured
+
+    xp, wp, idp = routing(Mp)
+    yp = ops.experts_prefill(bf16_dev(xp, dev), torch.from_numpy(wp).to(dev), torch.from_numpy(idp).to(dev),
+                             dbank, dshared)
+    torch.cuda.synchronize()
+    assert ops._WS.buf[dev.index or 0].data_ptr() != cap_ptr, "the prefill should have grown the workspace"
+    # memory freed by the growth would be handed to the next allocation of its size
+    junk = torch.full((cap_bytes,), 0x5A, dtype=torch.uint8, device=dev)
+    _check(yp, oracle.experts.moe_layer("prefill", xp, wp, idp, bank, shared), "prefill after capture")
+    for rep in range(3):
+        x, w_ref, ids_ref = routing(M)
+        x_buf.copy_(bf16_dev(x, dev))
+        w_buf.copy_(torch.from_numpy(w_ref))
+        ids_buf.copy_(torch.from_numpy(ids_ref))
+        graph.replay()
+        torch.cuda.synchronize()
+        _check(y, oracle.experts.moe_layer("decode", x, w_ref, ids_ref, bank, shared), ("replay", rep))
+        assert bool((junk == 0x5A).all()), f"replay {rep} wrote into memory released by the workspace"
+    del graph
+    ops.release_retired_workspaces()

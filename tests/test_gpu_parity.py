@@ -317,3 +317,60 @@ def test_decode_slot_cache_misses(dev):
     got = to_np(y)
     assert max_rel(got, y_ref) <= MAX_REL_TOL
     assert cosine(got, y_ref) >= COS_TOL
+
+
+@pytest.mark.parametrize("M", [4, 40, 256])
+def test_decode_large_slot_bank(dev, M):
+    """Decode over a 1664-slot bank (40 layers x 256 experts, the cache size of
+    the reference's tests/moe/test_offload.py:379-404).  Above 1023 rows the
+    permutation of more than 64 routes takes the sort-based align (M = 40: 320
+    routes, M = 256: 2048 routes); M = 4 takes the one-wave align.  Both entry
+    points: plain slot ids, and expert ids looked up in the permutation with
+    the miss counters."""
+    rng = np.random.default_rng(1664 + M)
+    S, E, H, I, k = 1664, 2048, 256, 128, 8
+    bank = code_bank("fp8", S, H, I, rng)
+    dbank = to_device_bank(bank, dev)
+    table = np.full(E, -1, dtype=np.int32)
+    resident = rng.choice(E, S - 64, replace=False)
+    table[resident] = rng.permutation(S)[: S - 64].astype(np.int32)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(M)]).astype(np.int32)
+    w = rng.random((M, k), dtype=np.float32)
+    w = (w / w.sum(1, keepdims=True)).astype(np.float32)
+    x = synth.activations(rng, M, H)
+    slots_ref, miss_ref, stats_ref = oracle.slots.slot_map(ids, table)
+    y_ref = oracle.experts.moe_layer("decode", x, w, slots_ref, bank)
+    xd, wd = bf16_dev(x, dev), torch.from_numpy(w).to(dev)
+
+    y_a = ops.experts_decode(xd, wd, torch.from_numpy(slots_ref).to(dev), dbank)
+    ids_b = torch.from_numpy(ids).to(dev)
+    miss_b = torch.empty(ids.shape, dtype=torch.uint8, device=dev)
+    stats_b = torch.zeros(4, dtype=torch.int64, device=dev)
+    y_b = ops.experts_decode(xd, wd, ids_b, dbank, slot_for_id=torch.from_numpy(table).to(dev), miss_mask=miss_b,
+                             stats=stats_b)
+    np.testing.assert_array_equal(to_np(ids_b), slots_ref)
+    np.testing.assert_array_equal(to_np(miss_b), miss_ref)
+    np.testing.assert_array_equal(to_np(stats_b), stats_ref)
+    for y in (y_a, y_b):
+        got = to_np(y)
+        assert max_rel(got, y_ref) <= MAX_REL_TOL, (M, max_rel(got, y_ref))
+        assert cosine(got, y_ref) >= COS_TOL, (M, cosine(got, y_ref))
+    assert torch.equal(y_a, y_b)
+
+
+def test_decode_large_bank_matches_small_bank(dev):
+    """The sort-based align (bank of 2048 rows) and the counting align (the
+    same touched experts as a 1000-row bank) give bit-identical outputs."""
+    rng = np.random.default_rng(5)
+    H, I, k, M = 256, 128, 8, 48
+    small = code_bank("fp8", 1000, H, I, rng)
+    big = code_bank("fp8", 2048, H, I, rng)
+    for name in ("gate_up", "down", "gate_up_scale", "down_scale"):
+        getattr(big, name)[:1000] = getattr(small, name)
+    ids = np.stack([rng.choice(1000, k, replace=False) for _ in range(M)]).astype(np.int32)
+    ids[0, :3] = ids[1, :3]  # shared experts across tokens
+    w = rng.random((M, k), dtype=np.float32)
+    xd, wd, idd = bf16_dev(synth.activations(rng, M, H), dev), torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev)
+    y_small = ops.experts_decode(xd, wd, idd, to_device_bank(small, dev)).clone()
+    y_big = ops.experts_decode(xd, wd, idd, to_device_bank(big, dev))
+    assert torch.equal(y_small, y_big)

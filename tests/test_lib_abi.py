@@ -45,15 +45,15 @@ def test_validation_errors_without_launch():
     rc = L.ftmoe_experts_decode(w, 1, 8, w, w, ctypes.byref(bank), None, 0, 0, w, w, 1 << 20, None)
     assert rc == _lib.FTMOE_ERR_UNSUPPORTED  # hidden not a multiple of 128
     # miss path: admission tables beyond one workgroup's LDS, unaligned gather rows
-    rc = L.ftmoe_lru_ensure(w, 8, 0, 1, 256, w, w, w, w, 9000, None, -1, 0, w, w, 8, w, w, None, None, None)
+    rc = L.ftmoe_lru_ensure(w, 8, 0, 1, 256, w, w, w, w, 9000, None, -1, 0, w, w, 8, w, w, None, None, None, None)
     assert rc == _lib.FTMOE_ERR_UNSUPPORTED and b"S=9000" in L.ftmoe_last_error()
-    rc = L.ftmoe_lru_ensure(w, 8, 2, 2, 256, w, w, w, w, 64, None, -1, 0, w, w, 8, w, w, None, None, None)
+    rc = L.ftmoe_lru_ensure(w, 8, 2, 2, 256, w, w, w, w, 64, None, -1, 0, w, w, 8, w, w, None, None, None, None)
     assert rc == _lib.FTMOE_ERR_UNSUPPORTED  # layer outside [0, num_layers)
-    rc = L.ftmoe_lru_ensure(w, 8, 0, 1, 256, None, w, w, w, 64, None, -1, 0, w, w, 8, w, w, None, None, None)
+    rc = L.ftmoe_lru_ensure(w, 8, 0, 1, 256, None, w, w, w, 64, None, -1, 0, w, w, 8, w, w, None, None, None, None)
     assert rc == _lib.FTMOE_ERR_INVALID
-    rc = L.ftmoe_lru_ensure(w, 8, 0, 1, 256, w, w, w, w, 64, None, -1, 70000, w, w, 8, w, w, None, None, None)
+    rc = L.ftmoe_lru_ensure(w, 8, 0, 1, 256, w, w, w, w, 64, None, -1, 70000, w, w, 8, w, w, None, None, None, None)
     assert rc == _lib.FTMOE_ERR_UNSUPPORTED and b"frac_q16=70000" in L.ftmoe_last_error()
-    rc = L.ftmoe_lru_ensure(None, 8, 0, 1, 256, w, w, w, w, 64, None, -1, 0, w, w, 8, w, w, None, None, None)
+    rc = L.ftmoe_lru_ensure(None, 8, 0, 1, 256, w, w, w, w, 64, None, -1, 0, w, w, 8, w, w, None, None, None, None)
     assert rc == _lib.FTMOE_ERR_INVALID
     fb = (_lib.FtmoeFetchBank * 1)(_lib.FtmoeFetchBank(16, 16, 24))
     rc = L.ftmoe_fetch_experts(fb, 1, w, w, w, 4, None)

@@ -108,14 +108,49 @@ def test_out_of_range_ids_are_not_seen():
     assert out.tolist() == [-1, -1, 0] and src.tolist() == [2] and stats.tolist() == [1, 1, 1, 1]
 
 
-def test_more_misses_than_slots_follows_the_sequential_rule():
-    # every slot is taken in (usage, slot) order; the later misses then reuse
-    # slot 0 (all usages equal), each evicting the previous one
+def test_more_misses_than_slots_admits_only_free_slots():
+    # every free slot is taken in (usage, slot) order; the misses after them get
+    # no slot (never one admitted in the same call) and are counted as unserved
     st = S.CacheState(1, 8, 2)
     out, evict, src, nmiss, _ = S.lru_ensure(st, 0, [0, 1, 2, 3])
-    assert evict.tolist() == [0, 1, 0, 0] and src.tolist() == [0, 1, 2, 3]
-    assert out.tolist() == [-1, 1, -1, 0]
+    assert evict.tolist() == [0, 1] and src.tolist() == [0, 1] and nmiss == 4
+    assert out.tolist() == [0, 1, -1, -1]
+    assert st.unserved.tolist() == [2]
     assert _inverse_ok(st)
+
+
+def test_resident_experts_of_the_call_are_never_victims():
+    # S = 4 with experts 6 and 7 resident; a call routed to {0, 1, 2, 3, 6, 7}
+    # has two free slots: 0 and 1 take them, 2 and 3 stay unserved, 6 and 7 keep
+    # their slots, every victim is distinct (tests/moe/test_offload.py:379-404)
+    st = S.CacheState(1, 8, 4)
+    S.lru_ensure(st, 0, [6, 7])
+    before = st.slot_for_id[0].copy()
+    out, evict, src, nmiss, _ = S.lru_ensure(st, 0, [0, 1, 2, 3, 6, 7])
+    assert nmiss == 4 and src.tolist() == [0, 1]
+    assert np.unique(evict).size == evict.size == 2
+    assert not set(evict.tolist()) & {int(before[6]), int(before[7])}
+    assert out.tolist()[4:] == [int(before[6]), int(before[7])] and out.tolist()[2:4] == [-1, -1]
+    assert st.unserved.tolist() == [2]
+    assert _inverse_ok(st)
+
+
+def test_victims_unique_under_random_pressure():
+    rng = np.random.default_rng(12)
+    for L, E, Sz in ((1, 16, 4), (2, 32, 6), (3, 64, 16)):
+        st = S.CacheState(L, E, Sz)
+        for _ in range(80):
+            layer = int(rng.integers(L))
+            ids = rng.integers(0, E, size=int(rng.integers(1, 3 * Sz)))
+            before = st.copy()
+            out, evict, src, nmiss, _ = S.lru_ensure(st, layer, ids, max_fetch=int(rng.integers(-1, 4)))
+            assert np.unique(evict).size == evict.size
+            seen = set(ids.tolist())
+            held = {int(before.slot_for_id[layer, e]) for e in seen if before.slot_for_id[layer, e] >= 0}
+            assert not set(evict.tolist()) & held
+            for e, s in zip(ids.tolist(), out.tolist()):
+                assert s == -1 or st.id_of_slot[s] == layer * E + e
+            assert _inverse_ok(st)
 
 
 def test_fraction_cap_known_answers():
