@@ -516,61 +516,187 @@ def run_prefill_offload(gen, dev, L: int = 3, E: int = 32, M: int = 8192, reps: 
     return res
 
 
-def cpu_baseline(layer: DecodeLayer, M: int, budget_s: float, gen, dev):
-    """C++ restatement of the reference CPU executor on this host: the same C4
-    routing (resident slots), bf16-dequantised banks (the reference's CPU route
-    for FP8 checkpoints), routed experts only (the reference's CPU executor does
-    not run the shared expert)."""
+def _host_cpu_info() -> dict:
+    """CPU model, physical cores of the machine, SMT state and NUMA nodes with
+    the CPUs of this process's share on each."""
+    from pathlib import Path
+
+    from oracle.cpu_moe import physical_cores
+
+    info = {"model": "unknown", "smt_active": None, "physical_cores_total": None, "numa_nodes": {}}
+    try:
+        info["model"] = [ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo") if ln.startswith("model name")][0]
+    except (OSError, IndexError):
+        pass
+    try:
+        info["smt_active"] = Path("/sys/devices/system/cpu/smt/active").read_text().strip() == "1"
+    except OSError:
+        pass
+    keys = set()
+    for d in Path("/sys/devices/system/cpu").glob("cpu[0-9]*"):
+        try:
+            keys.add((d.joinpath("topology/physical_package_id").read_text().strip(),
+                      d.joinpath("topology/core_id").read_text().strip()))
+        except OSError:
+            pass
+    info["physical_cores_total"] = len(keys) or None
+    allowed = set(os.sched_getaffinity(0))
+
+    def parse(text):
+        out = set()
+        for part in text.strip().split(","):
+            if part:
+                a, _, b = part.partition("-")
+                out.update(range(int(a), int(b or a) + 1))
+        return out
+
+    for node in sorted(Path("/sys/devices/system/node").glob("node[0-9]*")):
+        try:
+            cpus = parse(node.joinpath("cpulist").read_text())
+        except OSError:
+            continue
+        mine = sorted(cpus & allowed)
+        if mine:
+            info["numa_nodes"][node.name] = mine
+    phys = physical_cores()
+    info["share_physical_cores"] = phys
+    return info
+
+
+# (name, CPU format, H, I, host experts, top_k, batches, bf16 shared expert I or 0).  C2 and C4 run
+# bf16-dequantised banks (the reference's CPU route for block-FP8 checkpoints); C4 holds the 64
+# experts of the GPU's resident set on the host, the others every expert of the config.
+CPU_CONFIGS = [
+    ("c1_tiny_bf16", "bf16", 1024, 512, 16, 2, (4,), 0),
+    ("c2_qwen3_30b_a3b_bf16_dequant", "bf16", 2048, 768, 128, 8, (1, 8, 32, 64), 0),
+    ("c3_glm_mxfp4_bf16_shared", "mxfp4", 5120, 1536, 160, 8, (1, 8, 32, 64), 1536),
+    ("c4_deepseek_v3_bf16_dequant_64_experts", "bf16", 7168, 2048, 64, 8, (1, 8, 32, 64), 0),
+]
+
+
+def _cpu_config_runs(cfg, cores, step_budget_s: float, seed: int) -> list[dict]:
+    """One CPU configuration at its batch sizes on ``cores``: the reference's
+    bs=1 method (``moe/benchbw.py:463-499``: 8 warm-up steps, then the median
+    of up to 64 timed steps, each routed to the next window of k experts so
+    consecutive steps touch disjoint experts and read DRAM); at batch > 1
+    (2 warm-up steps, at least 3 timed) each token takes k distinct experts
+    drawn from all host experts."""
     import numpy as np
 
-    from oracle.cpu_moe import CpuMoe, lib as cpulib, physical_cores
+    from oracle.cpu_moe import CpuMoe, lib as cpulib
 
-    c = layer.cfg
-    H, I, S, k = c["H"], c["I"], c["slots"], c["k"]
-    cores = physical_cores()[:16]
-    gu = np.empty((S, 2 * I, H), dtype=np.uint16)
-    dn = np.empty((S, H, I), dtype=np.uint16)
-    cpulib().cpumoe_fill_bf16(gu.ctypes.data, gu.size, 0.02 * math.sqrt(3), 1, len(cores))
-    cpulib().cpumoe_fill_bf16(dn.ctypes.data, dn.size, 0.02 * math.sqrt(3), 2, len(cores))
-    cpu = CpuMoe(H, I, k, S, "bf16", cpus=cores)
-    cpu.set_bank(gu, dn)
-    steps = []
-    routings = []
-    for _ in range(4):
-        lg = torch.randn((M, c["E"]), generator=gen, device=dev)
-        w, ids = layer.route(lg)
-        ops.slot_map(ids, layer.table, out=ids)
-        routings.append((w.cpu().numpy(), ids.cpu().numpy()))
-    x = (np.random.default_rng(0).standard_normal((M, H)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
-    cpu.run(x, *routings[0])  # warm-up
-    t_end = time.perf_counter() + budget_s
-    i = 0
-    us = []
-    while time.perf_counter() < t_end and i < 64:
-        w, ids = routings[i % len(routings)]
-        t0 = time.perf_counter()
-        cpu.run(x, w, ids)
-        steps.append(time.perf_counter() - t0)
-        us.append(len(np.unique(ids[ids >= 0])))
-        i += 1
+    name, fmt, H, I, E, k, batches, Is = cfg
+    nth = len(cores)
+    if fmt == "bf16":
+        gu = np.empty((E, 2 * I, H), dtype=np.uint16)
+        dn = np.empty((E, H, I), dtype=np.uint16)
+        cpulib().cpumoe_fill_bf16(gu.ctypes.data, gu.size, 0.02 * math.sqrt(3), seed, nth)
+        cpulib().cpumoe_fill_bf16(dn.ctypes.data, dn.size, 0.02 * math.sqrt(3), seed + 1, nth)
+        banks = (gu, dn)
+    else:  # any byte is a valid pair of e2m1 codes; scales 2^-7..2^-5
+        gu = np.empty((E, 2 * I, H // 2), dtype=np.uint8)
+        dn = np.empty((E, H, I // 2), dtype=np.uint8)
+        cpulib().cpumoe_fill_bf16(gu.ctypes.data, gu.size // 2, 1.0, seed, nth)
+        cpulib().cpumoe_fill_bf16(dn.ctypes.data, dn.size // 2, 1.0, seed + 1, nth)
+        rng = np.random.default_rng(seed)
+        banks = (gu, dn, rng.integers(120, 123, (E, 2 * I, H // 32), dtype=np.uint8),
+                 rng.integers(120, 123, (E, H, I // 32), dtype=np.uint8))
+    cpu = CpuMoe(H, I, k, E, fmt, cpus=cores)
+    cpu.set_bank(*banks)
+    sh = None
+    if Is:
+        sgu = np.empty((1, 2 * Is, H), dtype=np.uint16)
+        sdn = np.empty((1, H, Is), dtype=np.uint16)
+        cpulib().cpumoe_fill_bf16(sgu.ctypes.data, sgu.size, 0.02 * math.sqrt(3), seed + 2, nth)
+        cpulib().cpumoe_fill_bf16(sdn.ctypes.data, sdn.size, 0.02 * math.sqrt(3), seed + 3, nth)
+        sh = CpuMoe(H, Is, 1, 1, "bf16", cpus=cores)
+        sh.set_bank(sgu, sdn)
+    eb = expert_bytes("bf16" if fmt == "bf16" else "mxfp4", H, I)
+    sh_bytes = expert_bytes("bf16", H, Is) if Is else 0
+    rng = np.random.default_rng(seed + 7)
+    out = []
+    for M in batches:
+        x = (rng.standard_normal((M, H)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        w = np.full((M, k), 1.0 / k, dtype=np.float32)
+        base = np.arange(k, dtype=np.int32)
+
+        def ids_for(i):
+            if M == 1:
+                return ((i * k + base) % E).reshape(1, k).astype(np.int32)
+            return np.stack([rng.choice(E, k, replace=False) for _ in range(M)]).astype(np.int32)
+
+        def step(ids):
+            t0 = time.perf_counter()
+            cpu.run(x, w, ids)
+            if sh is not None:
+                sh.run(x, np.ones((M, 1), np.float32), np.zeros((M, 1), np.int32))
+            return time.perf_counter() - t0
+
+        warm = 8 if M == 1 else 2  # the reference's method is for bs=1; larger batches warm up briefly
+        for i in range(warm):
+            step(ids_for(i))
+        times, us = [], []
+        t_end = time.perf_counter() + step_budget_s
+        i = warm
+        while len(times) < 64 and (len(times) < 3 or time.perf_counter() < t_end):
+            ids = ids_for(i)
+            times.append(step(ids))
+            us.append(len(np.unique(ids)))
+            i += 1
+        t = statistics.median(times)
+        nbytes = statistics.mean(us) * eb + sh_bytes
+        out.append({"config": name, "batch": M, "ms": round(t * 1e3, 3), "tok_s": round(M / t, 1),
+                    "gbs": round(nbytes / t / 1e9, 2), "experts_per_step": round(statistics.mean(us), 2),
+                    "timed_steps": len(times)})
     isa = cpu.isa
     cpu.close()
-    t = statistics.median(steps)
-    eb = expert_bytes("bf16", H, I)
-    gbs = statistics.mean(us) * eb / t / 1e9
-    try:
-        model = [ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo") if ln.startswith("model name")][0]
-    except (OSError, IndexError):
-        model = "unknown"
+    if sh is not None:
+        sh.close()
+    for r in out:
+        r["isa"] = isa
+    return out
+
+
+def cpu_baseline(step_budget_s: float = 0.6) -> dict:
+    """The C++ restatement of the reference's CPU MoE executor on this host:
+    every CPU configuration at its batch sizes, on all physical cores of this
+    process's CPU share and on the physical cores of one NUMA node (the
+    reference assumes a single node, ``cpu_moe_ext.cpp:1094-1095``).  ``value``
+    is C4 at batch 64 on all cores (the headline workload); the rest is in
+    ``sweep``."""
+    host = _host_cpu_info()
+    all_cores = host["share_physical_cores"]
+    node, node_cpus = max(host["numa_nodes"].items(), key=lambda kv: len(kv[1])) if host["numa_nodes"] else (None, [])
+    node_cores = [c for c in all_cores if c in set(node_cpus)] or all_cores
+    variants = {"all_physical_cores": all_cores}
+    if node_cores != all_cores:
+        variants[f"numa_{node}"] = node_cores
+    sweep = []
+    for vname, cores in variants.items():
+        for i, cfg in enumerate(CPU_CONFIGS):
+            log(f"[bench] CPU baseline {cfg[0]} on {vname} ({len(cores)} threads)")
+            for r in _cpu_config_runs(cfg, cores, step_budget_s, seed=11 + i):
+                r["variant"] = vname
+                r["threads"] = len(cores)
+                sweep.append(r)
+    head = next(r for r in sweep if r["variant"] == "all_physical_cores" and r["config"].startswith("c4")
+                and r["batch"] == 64)
+    same = "" if len(variants) > 1 else (f"; the process's CPU share lies on one NUMA node ({node}), so the "
+                                         f"single-node variant is the all-cores run")
     return {
-        "value": gbs,
+        "value": head["gbs"],
         "unit": "GB/s",
-        "cores": len(cores),
+        "cores": len(all_cores),
         "kind": "port",
-        "sample": (f"C4 decode batch {M}, {len(steps)} timed steps (median {t * 1e3:.1f} ms/step, "
-                   f"{M / t:.1f} tok/s), routed experts only over the {S} resident slots as bf16 banks, "
-                   f"two-pass GEMV restatement, ISA {isa}, {len(cores)} pinned threads on physical cores, "
-                   f"CPU {model}"),
+        "sample": (f"C4 decode batch 64: {head['timed_steps']} timed steps after 2 warm-up (median "
+                   f"{head['ms']} ms/step, {head['tok_s']} tok/s), routed experts only over 64 host experts as "
+                   f"bf16 banks (the reference's CPU route for FP8 checkpoints), two-pass GEMV restatement of "
+                   f"cpu_moe_ext.cpp, ISA {head['isa']}, {len(all_cores)} pinned threads on physical cores{same}"),
+        "host": {"cpu_model": host["model"], "isa": head["isa"], "smt_active": host["smt_active"],
+                 "physical_cores_total": host["physical_cores_total"], "threads_all_cores": len(all_cores),
+                 "numa_node": node, "threads_numa_node": len(node_cores),
+                 "numa_nodes_of_share": {k: len(v) for k, v in host["numa_nodes"].items()}},
+        "sweep": sweep,
     }
 
 
@@ -596,9 +722,14 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--config", choices=("c2", "c3", "c4"), default="c4",
+                    help="decode configuration of the timed layer (c4: the headline line; c2/c3: that layer "
+                         "alone at --batch, printed as its own line -- a profiling aid)")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-step-seconds", type=float, default=0.6,
+                    help="time budget of each CPU baseline point (at least 3 timed steps, at most 64)")
+    ap.add_argument("--cpu-only", action="store_true", help="run only the CPU baseline and print it")
     ap.add_argument("--miss-only", action="store_true", help="time the miss path (admission + PCIe gather) alone")
     ap.add_argument("--hybrid-only", action="store_true", help="time the hybrid CPU/GPU decode alone")
     ap.add_argument("--prefill-offload-only", action="store_true",
@@ -612,6 +743,9 @@ def main() -> int:
         print(f"bench.py runs on one GPU only (the MoE-layer hot path is measured on one MI355X); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
+    if args.cpu_only:  # host cores only
+        print(json.dumps(cpu_baseline(args.cpu_step_seconds)), flush=True)
+        return 0
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
@@ -647,6 +781,14 @@ def main() -> int:
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}), flush=True)
         return 0
 
+    hcfg = {"c2": C2, "c3": C3, "c4": C4}[args.config]
+    if hcfg is not C4:  # one decode configuration alone (profiling aid)
+        log(f"[bench] building {hcfg['name']}")
+        layer = DecodeLayer(hcfg, dev, gen)
+        res = run_decode(layer, args.batch, args.steps, args.warmup, gen, stage_timing=True)
+        print(json.dumps({"config": hcfg["name"], **{k: (round(v, 4) if isinstance(v, float) else v)
+                                                    for k, v in res.items()}}), flush=True)
+        return 0
     log("[bench] building C4 layer (64 resident FP8 experts + shared)")
     c4 = DecodeLayer(C4, dev, gen)
     log(f"[bench] C4 decode batch {args.batch}: {args.steps} steps")
@@ -667,7 +809,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         log("[bench] CPU baseline")
-        cpu = cpu_baseline(c4, args.batch, args.cpu_seconds, gen, dev)
+        cpu = cpu_baseline(args.cpu_step_seconds)
     del c4
     torch.cuda.empty_cache()
     if not args.no_sweep:
@@ -687,13 +829,16 @@ def main() -> int:
         sweep["c4_prefill_offload_3x32_experts"] = run_prefill_offload(gen, dev)
         log("[bench] sweep C4 hybrid decode (1 expert fetched per step, the other misses on the CPU)")
         sweep["c4_hybrid_b1"] = run_hybrid(gen, dev, M=1)
-        # the reference's benched rule: the fetch share from the measured standalone PCIe and CPU rates
+        # the reference's benched rules (moe/bench_profile.py:156-191): the fetch share from the measured
+        # PCIe and CPU rates, pcie / cpu for rates taken under DRAM contention, pcie / (pcie + cpu) for
+        # rates of transfers that overlap without contending; both from this run's standalone rates
         from freetoken_amd.moe.cpu_decode import hybrid_fetch_fraction
 
-        frac = hybrid_fetch_fraction(sweep["c4_miss_fetch_8_experts"]["fetch_gbs"], sweep["c4_hybrid_b1"]["cpu_gbs"],
-                                     overlapped=False)
-        log(f"[bench] sweep C4 hybrid decode with the measured fetch fraction {frac}")
-        sweep["c4_hybrid_b1_measured_fraction"] = run_hybrid(gen, dev, M=1, fetch_fraction=frac)
+        pcie, cpu_rate = sweep["c4_miss_fetch_8_experts"]["fetch_gbs"], sweep["c4_hybrid_b1"]["cpu_gbs"]
+        for rule, overlapped in (("contention", False), ("overlap", True)):
+            frac = hybrid_fetch_fraction(pcie, cpu_rate, overlapped=overlapped)
+            log(f"[bench] sweep C4 hybrid decode, measured fetch fraction {frac} ({rule} rule)")
+            sweep[f"c4_hybrid_b1_fraction_{rule}_rule"] = run_hybrid(gen, dev, M=1, fetch_fraction=frac)
 
     def rnd(d):
         return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}

@@ -374,3 +374,44 @@ def test_offload_layer_from_ftw_banks(dev, tmp_path, per_layer):
                                          torch.from_numpy(ids_ref.copy()).to(dev))
         g = to_np(y)
         assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, (per_layer, call)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["fp8", "bf16"])
+def test_offload_layer_from_hf_checkpoint(dev, tmp_path, mode):
+    """Expert banks read from a block-FP8 HF safetensors checkpoint into pinned
+    host memory (models/qwen3_5_moe/weight.py:834-1055; mode "bf16" is the
+    FREETOKEN_FP8_EXPERTS=bf16 dequant route) and served to an offload layer's
+    decode through the miss path: outputs equal the oracle on the same banks."""
+    from freetoken_amd.checkpoint.hf import load_hf_expert_banks
+    from oracle.experts import Bank, dequant_fp8_block
+    from oracle.numerics import bf16_round
+    from test_hf_checkpoint import write_hf_checkpoint
+
+    rng = np.random.default_rng(113)
+    L, E, Sz, H, I, k, M = 2, 8, 6, 512, 256, 2, 3
+    banks = write_hf_checkpoint(tmp_path, "model.layers", 1, L, E, H, I, seed=3)
+    fmt, sources, lay = load_hf_expert_banks(str(tmp_path), mode=mode)
+    assert all(t.is_pinned() for ts in sources.values() for t in ts)
+    if mode == "bf16":
+        banks = [Bank("bf16", bf16_round(dequant_fp8_block(b.gate_up, b.gate_up_scale)),
+                      bf16_round(dequant_fp8_block(b.down, b.down_scale))) for b in banks]
+    cache = ExpertSlotCache(L, E, Sz, fmt, device=dev)
+    cache.set_bank_caches(**{n: torch.zeros((Sz,) + ts[0].shape[1:], dtype=ts[0].dtype, device=dev)
+                             for n, ts in sources.items()})
+    cache.set_bank_sources(sources)
+    cache.reset()
+    layers = [OffloadMoELayer(l, E, k, H, I, device=dev) for l in range(L)]
+    for lay_ in layers:
+        lay_.offload_cache = cache
+    for call in range(4):
+        l = call % L
+        x = synth.activations(rng, M, H)
+        w_ref, ids_ref = oracle.routing.softmax_topk(synth.normal(rng, (M, E)), k, True)
+        y_ref = oracle.experts.moe_layer("decode", x, w_ref, ids_ref, banks[l], None)
+        with moe_phase("decode", backend="offload"):
+            y = layers[l].routed_forward(bf16_dev(x, dev), torch.from_numpy(w_ref).to(dev),
+                                         torch.from_numpy(ids_ref.copy()).to(dev))
+        g = to_np(y)
+        assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, (mode, call, max_rel(g, y_ref))
+    cache.check_capacity()
