@@ -89,6 +89,8 @@ SIGNATURES = {
     "ftmoe_act_quant_fp8": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "ftmoe_experts_decode_workspace": (_sz, [_i, _i, _bp, _bp]),
     "ftmoe_experts_decode": (_i, [_vp, _i, _i, _vp, _vp, _bp, _bp, _i, _i, _vp, _vp, _sz, _vp]),
+    "ftmoe_experts_decode_noalloc": (_i, [_vp, _i, _i, _vp, _vp, _bp, _bp, _i, _i, _vp, _vp]),
+    "ftmoe_experts_decode_noalloc_capacity": (_sz, []),
     "ftmoe_experts_decode_cached": (_i, [_vp, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _bp, _bp, _i, _i, _vp, _vp, _sz,
                                          _vp]),
     "ftmoe_experts_decode_routed": (_i, [_vp, _i, _i, ctypes.POINTER(FtmoeRouter), _vp, _vp, _vp, _i, _vp, _vp, _vp,

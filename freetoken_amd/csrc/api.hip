@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -716,6 +717,73 @@ int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, 
   g_timer.mark();
   g_timer.end_call();
   return rc;
+}
+
+}  // extern "C"
+
+// ---- decode without allocation ---------------------------------------------
+// The workspace of ftmoe_experts_decode_noalloc is this file-scope device
+// array: each GPU the library runs on holds its own copy for the life of the
+// process.  Host code never uses its name as an address (on the host it is a
+// stand-in); the address on each device comes from hipGetSymbolAddress, taken
+// once per device with that device current.
+constexpr size_t kNoallocScratchBytes = size_t{64} << 20;
+static __device__ __align__(256) uint8_t scratch[kNoallocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch array's address on the current device (which must own stream).
+int noalloc_scratch(ftmoe_stream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(FTMOE_ERR_HIP, "experts_decode_noalloc: no current device (or device %d beyond %d)", dev, kMaxDevices);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess)
+      return fail(FTMOE_ERR_HIP, "experts_decode_noalloc: stream device query failed");
+    if (sdev != dev)
+      return fail(FTMOE_ERR_INVALID, "experts_decode_noalloc: stream of device %d, current device %d", sdev, dev);
+  }
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p)
+      return fail(FTMOE_ERR_HIP, "experts_decode_noalloc: scratch address on device %d: %s", dev,
+                  hipGetErrorString(err));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FTMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ftmoe_experts_decode_noalloc_capacity(void) { return kNoallocScratchBytes; }
+
+int ftmoe_experts_decode_noalloc(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
+                                 const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
+                                 int apply_router_weight_on_input, void* y, ftmoe_stream_t stream) {
+  if (!bank || M <= 0 || top_k <= 0)
+    return fail(FTMOE_ERR_INVALID, "experts_decode_noalloc: bank %p, M=%d top_k=%d", static_cast<const void*>(bank),
+                M, top_k);
+  const size_t need = decode_layout(nullptr, M, top_k, bank, shared).bytes;
+  if (need > kNoallocScratchBytes)
+    return fail(FTMOE_ERR_WORKSPACE, "experts_decode_noalloc: batch %d x top-%d needs %zu bytes of scratch, beyond the "
+                "static %zu (use ftmoe_experts_decode with a caller workspace)", M, top_k, need, kNoallocScratchBytes);
+  void* ws = nullptr;
+  const int rc = noalloc_scratch(stream, &ws);
+  if (rc) return rc;
+  // every workspace field the kernels read is written earlier in the same call:
+  // nothing needs clearing between calls
+  return experts_decode_impl(x, M, top_k, topk_w, topk_ids, nullptr, bank, shared, activation,
+                             apply_router_weight_on_input, y, ws, kNoallocScratchBytes, stream);
 }
 
 int ftmoe_stage_timing_begin(void) {

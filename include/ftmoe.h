@@ -224,6 +224,24 @@ int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, c
                          int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
                          ftmoe_stream_t stream);
 
+/* Decode that allocates nothing: ftmoe_experts_decode with its workspace in a
+ * static device array of ftmoe_experts_decode_noalloc_capacity() bytes
+ * (64 MiB: C4-shaped decode -- H 7168, I 2048, top-8, shared expert -- up to
+ * batch 256), which each GPU the library runs on holds until the process
+ * ends.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as
+ * ftmoe_experts_decode without the workspace; a call whose workspace would
+ * exceed the array fails with FTMOE_ERR_WORKSPACE before any launch.  stream
+ * must belong to the current device.  Every call on a GPU shares that GPU's
+ * array (nothing in it needs clearing between calls): calls that overlap on
+ * one GPU -- on different streams, or from different host threads -- race and
+ * must be serialised by the caller. */
+size_t ftmoe_experts_decode_noalloc_capacity(void);
+int ftmoe_experts_decode_noalloc(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
+                                 const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
+                                 int apply_router_weight_on_input, void* y, ftmoe_stream_t stream);
+
 /* Decode over an expert-slot cache in one call: the id -> slot rewrite of
  * OffloadMoeCache.ensure_experts (moe/offload_cache.py:800-810, as
  * ftmoe_slot_map: slot_ids[i] = slot_for_id[topk_ids[i]], -1 when absent or
