@@ -82,6 +82,7 @@ SIGNATURES = {
     "ftmoe_lru_ensure": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp,
                               _vp, _vp]),
     "ftmoe_fetch_experts": (_i, [_fbp, _i, _vp, _vp, _vp, _i, _vp]),
+    "ftmoe_prefill_hit_compact": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "ftmoe_host_alloc": (_i, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
     "ftmoe_host_free": (_i, [_vp]),
     "ftmoe_materialize_layer": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp]),

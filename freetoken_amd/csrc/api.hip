@@ -359,6 +359,18 @@ int ftmoe_release_slots(int slot_begin, int slot_end, int num_layers, int num_ex
   return check_hip(ftmoe::launch_release_slots(a, stream), "release_slots launch");
 }
 
+int ftmoe_prefill_hit_compact(const int32_t* slot_for_id_row, int num_experts, int threshold, int dst_base,
+                              int32_t* dst_rows, int32_t* src_rows, int32_t* num_hits, ftmoe_stream_t stream) {
+  if (!slot_for_id_row || !dst_rows || !src_rows || !num_hits)
+    return fail(FTMOE_ERR_INVALID, "prefill_hit_compact: NULL pointer");
+  if (num_experts <= 0 || num_experts > 8192 || threshold < 0 || dst_base < 0)
+    return fail(FTMOE_ERR_UNSUPPORTED, "prefill_hit_compact: num_experts=%d threshold=%d dst_base=%d", num_experts,
+                threshold, dst_base);
+  return check_hip(ftmoe::launch_hit_compact(slot_for_id_row, num_experts, threshold, dst_base, dst_rows, src_rows,
+                                             num_hits, stream),
+                   "prefill_hit_compact launch");
+}
+
 int ftmoe_fetch_experts(const ftmoe_fetch_bank* banks, int nbanks, const int32_t* evict_slots,
                         const int32_t* src_indices, const int32_t* num_indices, int max_entries,
                         ftmoe_stream_t stream) {

@@ -298,6 +298,47 @@ hipError_t launch_release_slots(const PlaceArgs& a, hipStream_t stream) {
 }
 
 // ----------------------------------------------------------------------------
+// Hit compaction of the prefill double buffer's hit/miss split (reference:
+// prefill_hit_compact and its kernel, moe/offload_kernels.py:63-86): the
+// experts of one layer resident outside the two buffers (slot >= threshold,
+// the buffers own the slots below) are listed in ascending expert order as
+// (buffer row dst_base + e, cache slot), for a device-to-device gather.  One
+// workgroup; a block scan keeps the order.
+// ----------------------------------------------------------------------------
+__global__ void __launch_bounds__(kLruThreads) hit_compact_kernel(const int32_t* slot_row, int num_experts,
+                                                                  int threshold, int dst_base, int32_t* dst_rows,
+                                                                  int32_t* src_rows, int32_t* num) {
+  __shared__ int s_tmp[2 * kLruWaves];
+  const int per = (num_experts + kLruThreads - 1) / kLruThreads;  // contiguous experts per thread
+  const int e0 = threadIdx.x * per;
+  int mine = 0;
+  for (int q = 0; q < per; ++q) {
+    const int e = e0 + q;
+    if (e < num_experts && slot_row[e] >= threshold) ++mine;
+  }
+  int total = 0;
+  int pos = lru_block_scan(mine, s_tmp, &total);
+  for (int q = 0; q < per; ++q) {
+    const int e = e0 + q;
+    if (e >= num_experts) break;
+    const int s = slot_row[e];
+    if (s >= threshold) {
+      dst_rows[pos] = dst_base + e;
+      src_rows[pos] = s;
+      ++pos;
+    }
+  }
+  if (threadIdx.x == 0) num[0] = total;
+}
+
+hipError_t launch_hit_compact(const int32_t* slot_row, int num_experts, int threshold, int dst_base, int32_t* dst_rows,
+                              int32_t* src_rows, int32_t* num, hipStream_t stream) {
+  hipLaunchKernelGGL(hit_compact_kernel, dim3(1), dim3(kLruThreads), 0, stream, slot_row, num_experts, threshold,
+                     dst_base, dst_rows, src_rows, num);
+  return hipGetLastError();
+}
+
+// ----------------------------------------------------------------------------
 // Gather of admitted experts: entry i copies row src_indices[i] of every host
 // bank to row evict_slots[i] of the matching slot bank, for i < num_indices[0]
 // (reference: fast_index_copy_multi over the banks of copy_missing,

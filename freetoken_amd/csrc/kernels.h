@@ -193,6 +193,8 @@ struct FetchArgs {
   const int32_t* num_indices;
 };
 hipError_t launch_fetch_experts(const FetchArgs& a, int max_entries, hipStream_t stream);
+hipError_t launch_hit_compact(const int32_t* slot_row, int num_experts, int threshold, int dst_base, int32_t* dst_rows,
+                              int32_t* src_rows, int32_t* num, hipStream_t stream);
 int fetch_chunks(uint64_t row_bytes);
 
 // Records the message of a failed C-ABI call (ftmoe_last_error) and returns code.

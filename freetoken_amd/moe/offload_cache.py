@@ -44,7 +44,7 @@ def bank_from_views(quant_format: str, views) -> ops.ExpertBank:
 class ExpertSlotCache:
     def __init__(self, num_layers: int, num_experts: int, cache_size: int, quant_format: str,
                  device: torch.device | str = "cuda", decode_target: str = "gpu", hybrid_max_fetch: int = 1,
-                 hybrid_fetch_fraction: float = 0.0, prefill_overlap: bool = False):
+                 hybrid_fetch_fraction: float = 0.0, prefill_overlap: bool = False, prefill_hit_d2d: bool = False):
         assert quant_format in ("bf16", "fp8_block", "ds_fp4"), quant_format
         assert decode_target in ("gpu", "cpu", "hybrid"), decode_target
         # decode placement (moe/offload_cache.py:117-136): "gpu" fetches every
@@ -63,6 +63,13 @@ class ExpertSlotCache:
         assert not prefill_overlap or cache_size >= 2 * num_experts, \
             "prefill overlap borrows two expert layers of slots: cache_size >= 2 * num_experts"
         self.prefill_overlap = prefill_overlap
+        # hit/miss split of the double buffer (:703-773): experts resident
+        # outside the buffers (slot >= 2E) reach the buffer device to device,
+        # only the others cross PCIe; needs slots beyond the two buffers
+        self.prefill_hit_d2d = prefill_hit_d2d
+        self._pf_split = False
+        self.prefill_hit_rows = 0
+        self.prefill_total_rows = 0
         self._pf_views: list[torch.Tensor] | None = None
         self._pf_layer: list[int | None] = [None, None]
         self._pf_released = [True, True]
@@ -221,11 +228,18 @@ class ExpertSlotCache:
             self._pf_ready = [torch.cuda.Event() for _ in range(2)]
             self._pf_release = [torch.cuda.Event() for _ in range(2)]
             self._pf_begin = torch.cuda.Event()
+            dev = self.device
+            self._pf_snapshot = torch.empty((self.num_layers, E), dtype=torch.int32, pin_memory=True)
+            self._pf_hit_dst = torch.empty((E,), dtype=torch.int32, device=dev)
+            self._pf_hit_src = torch.empty((E,), dtype=torch.int32, device=dev)
+            self._pf_hit_num = torch.zeros((1,), dtype=torch.int32, device=dev)
         return self._pf_views
 
     def begin_prefill(self) -> None:
         """Fences the copy stream behind the work already queued on the current
-        stream (a running decode may read the slots the buffers borrow; :602-624)."""
+        stream (a running decode may read the slots the buffers borrow; :602-624).
+        With the hit/miss split, snapshots the slot table once for the chunk
+        (one host synchronisation; the per-layer miss lists are host math)."""
         if not self.prefill_overlap:
             return
         self._prefill_buffers()
@@ -233,6 +247,11 @@ class ExpertSlotCache:
         self._pf_released = [True, True]
         self._pf_begin.record(torch.cuda.current_stream(self.device))
         self.prefill_copy_stream.wait_event(self._pf_begin)
+        self._pf_split = self.prefill_hit_d2d and self.cache_size > 2 * self.num_experts
+        if self._pf_split:
+            with torch.cuda.stream(self.prefill_copy_stream):
+                self._pf_snapshot.copy_(self.slot_for_id, non_blocking=True)
+            self.prefill_copy_stream.synchronize()
 
     def prefetch_prefill_layer(self, layer_id: int) -> None:
         """Starts the host copy of a whole layer into buffer ``layer_id % 2`` on
@@ -248,15 +267,54 @@ class ExpertSlotCache:
         assert self._pf_layer[buf] is None or self._pf_released[buf], "prefill buffer reused before release"
         views = self._prefill_buffers()
         E = self.num_experts
+        if self._pf_split:
+            self._prefetch_split(layer_id, buf)
+        else:
+            with torch.cuda.stream(self.prefill_copy_stream):
+                if self._pf_has_release[buf]:
+                    self.prefill_copy_stream.wait_event(self._pf_release[buf])
+                ops.release_slots(buf * E, (buf + 1) * E, self.slot_for_id, self.id_of_slot, self.usage)
+                for layers, v in zip(self.sources.values(), views):  # bytes, whatever the dtypes
+                    v[buf].view(torch.uint8).copy_(layers[layer_id].view(torch.uint8), non_blocking=True)
+                self._pf_ready[buf].record(self.prefill_copy_stream)
+        self._pf_layer[buf] = layer_id
+        self._pf_released[buf] = False
+
+    def _prefetch_split(self, layer_id: int, buf: int) -> None:
+        """Hit/miss split of one layer's move into buffer ``buf`` (``:703-773``).
+        Hits -- experts resident at slots >= 2E, outside the buffers -- are
+        listed on the device from the live slot table and gathered slot bank ->
+        buffer on the current stream (ordered after the buffer's earlier
+        GEMMs).  Misses (slots below 2E belong to the buffers and count as
+        misses) are listed from the chunk's snapshot and gathered host -> buffer
+        on the copy stream after the buffer's release and the emptying of its
+        slots.  The two row sets are disjoint; the live table and the snapshot
+        agree on them, since the only writer during a prefill chunk empties
+        buffer slots, which are below 2E on both sides."""
+        E = self.num_experts
+        banks = list(self.banks.values())
+        snap = self._pf_snapshot[layer_id]
+        hit = snap >= 2 * E
+        n_hit = int(hit.sum())
+        self.prefill_hit_rows += n_hit
+        self.prefill_total_rows += E
+        if n_hit:
+            ops.prefill_hit_compact(self.slot_for_id[layer_id], 2 * E, buf * E, self._pf_hit_dst, self._pf_hit_src,
+                                    self._pf_hit_num)
+            ops.fetch_experts(banks, banks, self._pf_hit_dst, self._pf_hit_src, self._pf_hit_num, max_entries=E)
+        miss = torch.nonzero(~hit).flatten().to(torch.int32)
         with torch.cuda.stream(self.prefill_copy_stream):
             if self._pf_has_release[buf]:
                 self.prefill_copy_stream.wait_event(self._pf_release[buf])
             ops.release_slots(buf * E, (buf + 1) * E, self.slot_for_id, self.id_of_slot, self.usage)
-            for layers, v in zip(self.sources.values(), views):  # bytes, whatever the dtypes
-                v[buf].view(torch.uint8).copy_(layers[layer_id].view(torch.uint8), non_blocking=True)
+            if miss.numel():
+                # host-built lists (pinned, fresh per call: the pinned allocator keeps a block
+                # until the copy that reads it has run)
+                lists = torch.stack([miss + buf * E, miss, torch.full_like(miss, miss.numel())]).pin_memory()
+                dev_lists = lists.to(self.device, non_blocking=True)
+                ops.fetch_experts([layers[layer_id] for layers in self.sources.values()], banks, dev_lists[0],
+                                  dev_lists[1], dev_lists[2, :1], max_entries=int(miss.numel()))
             self._pf_ready[buf].record(self.prefill_copy_stream)
-        self._pf_layer[buf] = layer_id
-        self._pf_released[buf] = False
 
     def wait_prefill_layer(self, layer_id: int) -> tuple[torch.Tensor, ...]:
         """The layer's full ``[E, ...]`` bank views, the current stream made to
@@ -299,6 +357,11 @@ class ExpertSlotCache:
         if n:
             raise RuntimeError(f"expert cache too small: {n} missing experts found no free slot "
                                f"(cache_size {self.cache_size}); their routes were skipped")
+
+    def prefill_hit_rate(self) -> float:
+        """Share of the layers' experts the hit/miss split gathered device to
+        device since construction (the counters of ``:275-276,729``)."""
+        return self.prefill_hit_rows / self.prefill_total_rows if self.prefill_total_rows else 0.0
 
     def decode_miss_stats(self) -> dict:
         active, missing, calls, missed_routes = (int(x) for x in self.lru_stats.sum(0))

@@ -223,14 +223,15 @@ def fetch_experts(host_rows, slot_banks, evict_slots: torch.Tensor, src_indices:
                   num_indices: torch.Tensor, max_entries: int | None = None) -> None:
     """Copies the admitted experts' rows from pinned host tensors (one per
     bank, ``[E, ...]`` of one layer) into the slot banks (``[S, ...]`` on the
-    device), for the first ``num_indices`` entries (see ftmoe_fetch_experts)."""
+    device), for the first ``num_indices`` entries (see ftmoe_fetch_experts).
+    A source may also be a device tensor (device-to-device gather)."""
     if len(host_rows) != len(slot_banks) or not host_rows:
         raise ValueError("one host tensor per slot bank")
     _require_gpu(evict_slots, src_indices, num_indices, *slot_banks)
     banks = (_lib.FtmoeFetchBank * len(host_rows))()
     for b, (h, d) in enumerate(zip(host_rows, slot_banks)):
-        if h.device.type != "cpu" or not h.is_pinned() or not h.is_contiguous():
-            raise ValueError("host rows must be contiguous pinned CPU tensors")
+        if not h.is_contiguous() or (h.device.type == "cpu" and not h.is_pinned()):
+            raise ValueError("sources must be contiguous: pinned CPU tensors or device tensors")
         if not d.is_contiguous():
             raise ValueError("slot banks must be contiguous")
         row = h[0].numel() * h.element_size()
@@ -243,6 +244,22 @@ def fetch_experts(host_rows, slot_banks, evict_slots: torch.Tensor, src_indices:
                                   _stream(evict_slots.device)),
         "fetch_experts",
     )
+
+
+def prefill_hit_compact(slot_row: torch.Tensor, threshold: int, dst_base: int, dst_rows: torch.Tensor,
+                        src_rows: torch.Tensor, num_hits: torch.Tensor) -> None:
+    """Lists the experts of one layer resident at slots >= ``threshold`` as
+    (buffer row ``dst_base + e``, slot) entries for a device-to-device gather
+    (see ftmoe_prefill_hit_compact)."""
+    for t in (slot_row, dst_rows, src_rows, num_hits):
+        if t.dtype != torch.int32:
+            raise ValueError("slot row, lists and count must be int32")
+    _require_gpu(slot_row, dst_rows, src_rows, num_hits)
+    n = slot_row.numel()
+    if dst_rows.numel() < n or src_rows.numel() < n:
+        raise ValueError("dst_rows / src_rows must hold one entry per expert")
+    check(lib().ftmoe_prefill_hit_compact(_ptr(slot_row), n, threshold, dst_base, _ptr(dst_rows), _ptr(src_rows),
+                                          _ptr(num_hits), _stream(slot_row.device)), "prefill_hit_compact")
 
 
 def act_quant_fp8(x: torch.Tensor, mode: int = 0):

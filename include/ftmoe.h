@@ -179,9 +179,22 @@ int ftmoe_materialize_layer(int layer_id, int num_layers, int num_experts, int32
 int ftmoe_release_slots(int slot_begin, int slot_end, int num_layers, int num_experts, int32_t* slot_for_id,
                         int32_t* id_of_slot, int64_t* usage, int cache_size, ftmoe_stream_t stream);
 
+/* Hit compaction of the prefill double buffer's hit/miss split: replaces
+ * prefill_hit_compact (moe/offload_kernels.py:63-86, used by _prefetch_split,
+ * moe/offload_cache.py:703-773).  Lists the experts e of one layer whose
+ * slot (slot_for_id_row[e], int32 [num_experts]) is >= threshold -- resident
+ * outside the buffers, which own the slots below -- in ascending e as
+ * dst_rows[i] = dst_base + e (the buffer row) and src_rows[i] = the slot
+ * (int32 [num_experts] each), and *num_hits (int32) = their count: the
+ * entries of an ftmoe_fetch_experts gather from the slot banks into the
+ * buffer, device to device.  num_experts <= 8192. */
+int ftmoe_prefill_hit_compact(const int32_t* slot_for_id_row, int num_experts, int threshold, int dst_base,
+                              int32_t* dst_rows, int32_t* src_rows, int32_t* num_hits, ftmoe_stream_t stream);
+
 /* One bank of the gather below: this layer's expert rows in pinned host
  * memory ([num_experts, row_bytes]) and the slot bank ([cache_size,
- * row_bytes]) on the device. */
+ * row_bytes]) on the device.  host_rows may be device memory instead (the
+ * slot bank itself, for the prefill hit gather). */
 typedef struct ftmoe_fetch_bank {
   const void* host_rows;
   void* slot_bank;

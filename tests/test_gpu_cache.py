@@ -415,3 +415,56 @@ def test_offload_layer_from_hf_checkpoint(dev, tmp_path, mode):
         g = to_np(y)
         assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, (mode, call, max_rel(g, y_ref))
     cache.check_capacity()
+
+
+@pytest.mark.gpu
+def test_offload_prefill_hit_miss_split(dev):
+    """The double buffer's hit/miss split (moe/offload_cache.py:703-773): experts
+    already resident outside the buffers (slots >= 2E) are gathered device to
+    device, only the others cross PCIe.  The host rows of the resident experts
+    are zeroed after their placement, so any of them taken from the host would
+    change the output; every layer's prefill must still equal the oracle, and
+    the hit counters must count exactly the placed experts."""
+    rng = np.random.default_rng(131)
+    L, E, H, I, k, M = 3, 8, 512, 256, 2, 300
+    Sz = 2 * E + 6
+    banks = [synth.make_bank("fp8", E, H, I, rng) for _ in range(L)]
+    cache = ExpertSlotCache(L, E, Sz, "fp8_block", device=dev, prefill_overlap=True, prefill_hit_d2d=True)
+    eb = to_device_bank(banks[0], dev, rows=np.arange(Sz) % E)
+    cache.set_bank_caches(gate_up=eb.gate_up, gate_up_scale=eb.gate_up_scale, down=eb.down, down_scale=eb.down_scale)
+    for t in cache.banks.values():
+        t.view(torch.uint8).fill_(0)
+    names, _ = _pinned_bank_sources(banks[0])
+    per_layer = [_pinned_bank_sources(b)[1] for b in banks]
+    sources = {n: [per_layer[l][j] for l in range(L)] for j, n in enumerate(names)}
+    cache.set_bank_sources(sources)
+    cache.reset()
+    placed = {1: ([1, 4, 6], [16, 17, 18]), 2: ([3], [20])}
+    for layer, (experts, slots) in placed.items():
+        for e, s in zip(experts, slots):
+            for n in names:
+                cache.banks[n][s].view(torch.uint8).copy_(sources[n][layer][e].view(torch.uint8))
+        cache.assign(layer, experts, slots)
+    torch.cuda.synchronize()
+    for layer, (experts, _) in placed.items():
+        for e in experts:
+            for n in names:
+                sources[n][layer][e].view(torch.uint8).zero_()
+    layers = [OffloadMoELayer(l, E, k, H, I, device=dev) for l in range(L)]
+    for lay in layers:
+        lay.offload_cache = cache
+    for rep in range(2):
+        for l in range(L):
+            x = synth.activations(rng, M, H)
+            w_ref, ids_ref = oracle.routing.softmax_topk(synth.normal(rng, (M, E)), k, True)
+            y_ref = oracle.experts.moe_layer("prefill", x, w_ref, ids_ref, banks[l], None)
+            with moe_phase("prefill", backend="offload"):
+                y = layers[l].routed_forward(bf16_dev(x, dev), torch.from_numpy(w_ref).to(dev),
+                                             torch.from_numpy(ids_ref.copy()).to(dev))
+            g = to_np(y)
+            assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, (rep, l, max_rel(g, y_ref))
+    torch.cuda.synchronize()
+    assert cache.prefill_total_rows == 2 * L * E
+    assert cache.prefill_hit_rows == 2 * 4, cache.prefill_hit_rows
+    sft = to_np(cache.slot_for_id)  # the placed experts stay where they were
+    assert sft[1][[1, 4, 6]].tolist() == [16, 17, 18] and sft[2][3] == 20
