@@ -1029,6 +1029,9 @@ static hipError_t launch_one(dim3 g, const DecodeArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Bytes per weight times two (bf16 4, FP8 2, MXFP4 1).
+static int bytes_per_weight_x2(int fmt) { return fmt == FMT_BF16 ? 4 : fmt == FMT_FP8 ? 2 : 1; }
+
 template <int FR, int FS>
 static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared, hipStream_t stream) {
   const int gy = a.max_seg + (has_shared ? (a.M + a.seg_cap - 1) / a.seg_cap : 0);
@@ -1044,6 +1047,12 @@ static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared
   constexpr auto k1 = decode_stage_kernel<FR, FS, 1, 1, 1>;
   constexpr auto k2 = decode_stage_kernel<FR, FS, 1, 2, 1>;
   const dim3 g1(a.H / 64, gy), g2(a.H / 128, gy);
+  // a shared expert whose rows are several times heavier than the routed ones
+  // (bf16 beside MXFP4) trails the small grid of a one- or two-token call:
+  // halve its tiles (C3 down at b=1 22.8 -> 16.5 us, b=2 unchanged; from b=4
+  // on the routed segments fill the GPU and one tile per wave is slower)
+  const bool heavy_shared = has_shared && bytes_per_weight_x2(FS) >= 4 * bytes_per_weight_x2(FR);
+  if (heavy_shared && a.M <= 2) return launch_one<k1>(g1, a, stream);
   if (fill_of<k2>(g2) >= fill_of<k1>(g1) - kSlack) return launch_one<k2>(g2, a, stream);
   return launch_one<k1>(g1, a, stream);
 }

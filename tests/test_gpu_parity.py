@@ -374,3 +374,27 @@ def test_decode_large_bank_matches_small_bank(dev):
     y_small = ops.experts_decode(xd, wd, idd, to_device_bank(small, dev)).clone()
     y_big = ops.experts_decode(xd, wd, idd, to_device_bank(big, dev))
     assert torch.equal(y_small, y_big)
+
+
+@pytest.mark.parametrize("with_shared", [False, True])
+@pytest.mark.parametrize("M", [1, 5])
+def test_decode_all_routes_skipped(dev, M, with_shared):
+    """Every route skipped (ids -1 or beyond the bank): the output is exactly
+    zero without a shared expert and exactly the shared expert's with one --
+    the folded combine has no routed arrivals to wait for."""
+    rng = np.random.default_rng(91 + M)
+    E, H, I, k = 8, 512, 256, 4
+    bank = synth.make_bank("fp8", E, H, I, rng)
+    shared = synth.make_bank("fp8", 1, H, I, rng) if with_shared else None
+    x = synth.activations(rng, M, H)
+    ids = np.full((M, k), -1, dtype=np.int32)
+    ids[:, 1] = E + 3
+    w = np.full((M, k), 0.25, dtype=np.float32)
+    y = ops.experts_decode(bf16_dev(x, dev), torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev),
+                           to_device_bank(bank, dev), to_device_bank(shared, dev) if shared else None)
+    got = to_np(y)
+    if not with_shared:
+        assert not got.any()
+    else:
+        ref = oracle.experts.moe_layer("decode", x, w, ids, bank, shared)
+        assert max_rel(got, ref) <= MAX_REL_TOL and cosine(got, ref) >= COS_TOL
