@@ -448,8 +448,10 @@ def run_prefill_offload(gen, dev, L: int = 3, E: int = 32, M: int = 8192, reps: 
     """Prefill movement of the expert cache at C4 expert shape (FP8), L layers
     of E experts each held only in pinned host memory, M tokens routed top-8
     uniformly: per-layer time of (a) materialize + PCIe gather + experts, one
-    after the other, and (b) the double buffer, layer l+1's host copy on a copy
-    stream behind layer l's experts.  E is reduced from 256 so that L layers
+    after the other, (b) the double buffer, layer l+1's host copy on a copy
+    stream behind layer l's experts, and (c) the double buffer with half of
+    every layer's experts already resident, with and without the hit/miss
+    split.  E is reduced from 256 so that L layers
     of host banks stay a few GB."""
     from freetoken_amd.core import moe_phase
     from freetoken_amd.layers.moe import OffloadMoELayer
@@ -500,6 +502,45 @@ def run_prefill_offload(gen, dev, L: int = 3, E: int = 32, M: int = 8192, reps: 
         key = "double_buffer" if overlap else "materialize"
         res[f"{key}_ms_per_layer"] = t
         res[f"{key}_gbs"] = layer_bytes / (t * 1e-3) / 1e9
+        del cache, layers
+        torch.cuda.empty_cache()
+    # half of every layer's experts already resident outside the two buffers (slots >= 2E, as a
+    # decode leaves them): the double buffer with and without the hit/miss split
+    # (moe/offload_cache.py:703-773), hits gathered device to device, only misses over PCIe
+    half = E // 2
+    for split in (False, True):
+        S = 2 * E + L * half
+        cache = ExpertSlotCache(L, E, S, "fp8_block", device=dev, prefill_overlap=True, prefill_hit_d2d=split)
+        cache.set_bank_caches(**{n: torch.zeros((S,) + h[0].shape[1:], dtype=h[0].dtype, device=dev)
+                                 for n, h in host.items()})
+        cache.set_bank_sources(host)
+        cache.reset()
+        for l in range(L):
+            experts = list(range(0, E, 2))
+            slots = [2 * E + l * half + j for j in range(half)]
+            for e, sl in zip(experts, slots):
+                for n, h in host.items():
+                    cache.banks[n][sl].copy_(h[l][e], non_blocking=True)
+            cache.assign(l, experts, slots)
+        torch.cuda.synchronize()
+        layers = [OffloadMoELayer(l, E, k, H, I, device=dev) for l in range(L)]
+        for lay in layers:
+            lay.offload_cache = cache
+        times = []
+        with moe_phase("prefill", backend="offload"):
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                e0.record()
+                for lay in layers:
+                    lay.routed_forward(x, w, ids.clone())
+                e1.record()
+                torch.cuda.synchronize()
+                times.append(e0.elapsed_time(e1))
+        key = "half_resident_split" if split else "half_resident_no_split"
+        res[f"{key}_ms_per_layer"] = min(times) / L
+        if split:
+            res["half_resident_hit_rate"] = cache.prefill_hit_rate()
         del cache, layers
         torch.cuda.empty_cache()
     # the experts alone on resident banks, for the overlap bound

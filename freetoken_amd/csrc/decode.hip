@@ -13,9 +13,11 @@
 // k_first() below.  A and B use the same K placement, so the products pair up
 // no matter how the hardware orders K inside an MFMA.
 //
-// The 4 waves of a workgroup split K (wave w takes K blocks w, w+4, ...), and
-// their partial sums are reduced through LDS in fixed wave order, so results are
-// deterministic.
+// The 4 waves of a workgroup split K (wave w takes a contiguous quarter of the
+// K blocks), and their partial sums are reduced through LDS in fixed wave
+// order, so results are deterministic.  Without a K split (the down stage, and
+// gate_up of large FP8 calls) every wave walks the whole K range over its own
+// rows, and the waves share the activation chunks through an LDS ring.
 //
 // Formats (A operand dequant, in registers, exact):
 //   FMT_BF16   bf16 rows, used as is.
@@ -505,11 +507,11 @@ template <int FMT, int NMAT, int NCH>
 constexpr int sh_per_step() {  // vector memory instructions of one sh_issue
   return 3 * NMAT + NCH * act_copies<FMT>();
 }
-template <int FMT, int NMAT>
-constexpr int sh_act_ring_bytes() {  // the larger of the NCH variants (MXFP4 down runs one chunk per pass)
+template <int FMT, int NMAT, int CMAX>
+constexpr int sh_act_ring_bytes() {  // the larger of the NCH variants up to CMAX chunks per pass
   constexpr int one = (dma_depth<FMT, NMAT, 1>() + 1) * act_slot_bytes<FMT, 1>();
   constexpr int two = (dma_depth<FMT, NMAT, 2>() + 1) * act_slot_bytes<FMT, 2>();
-  return FMT == FMT_MXFP4 || one > two ? one : two;
+  return CMAX == 1 || one > two ? one : two;
 }
 
 __device__ __forceinline__ void lds_dma16_cached(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, uint32_t soff) {
@@ -767,7 +769,7 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
         dt.soff[m] = FMT == FMT_FP8 ? wt.soff[m] : static_cast<uint32_t>(tile_row + r16) * (K / 32);
       }
       uint8_t* ring = smem + wave * dma_ring_bytes<FMT, NMAT>();
-      if constexpr (STAGE == 1 && KS == 1) {
+      if constexpr (KS == 1) {
         // activation copies: copy v of chunk c of this wave covers columns
         // q * (1024 / CB) + lane / (CB / 16), q = wave * act_copies + v
         constexpr int CB = act_col_bytes<FMT>();
@@ -780,7 +782,9 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
             const int piece = (lane % (CB / 16)) ^ colc;
             const int col = base + c * 16 + colc;
             if (col < sv.count) {
-              const int row = sv.shared ? a.M * a.k + sv.start + col : a.sorted[sv.start + col];
+              int row;
+              if (STAGE == 0) row = sv.shared ? sv.start + col : a.sorted[sv.start + col] / a.k;
+              else row = sv.shared ? a.M * a.k + sv.start + col : a.sorted[sv.start + col];
               avoff[c][v] = static_cast<uint32_t>(row) * bstride * 2 + piece * 16;
             } else {
               avoff[c][v] = kOutOfRange;
@@ -834,16 +838,19 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
 
 // Route chunks (of 16) per pass, sized so that two K stages of weights and
 // activations plus the accumulators fit 256 registers per lane (occupancy 2).
-template <int FMT, int STAGE, int RT>
+// With the activations shared through LDS (KS = 1) MXFP4 takes one chunk per
+// pass, which keeps LDS at 80 KB (two workgroups per CU).
+template <int FMT, int STAGE, int RT, int KS>
 constexpr int chunks_per_pass() {
+  if constexpr (KS == 1 && FMT == FMT_MXFP4) return 1;
   if constexpr (STAGE == 0) return RT == 1 ? 2 : (FMT == FMT_BF16 ? 1 : 2);
-  return FMT == FMT_MXFP4 ? 1 : 2;  // MXFP4 down: one chunk keeps LDS at 80 KB (two workgroups per CU)
+  return 2;
 }
 
 template <int FMT, int STAGE, int RT, int KS>
 __device__ __forceinline__ void decode_segment(const DecodeArgs& a, const BankView& bank, const SegView& sv, int row0,
                                                int inter, uint8_t* smem, uint8_t* aring) {
-  constexpr int CMAX = chunks_per_pass<FMT, STAGE, RT>();
+  constexpr int CMAX = chunks_per_pass<FMT, STAGE, RT, KS>();
   for (int base = 0; base < sv.count; base += 16 * CMAX) {
     if constexpr (CMAX == 1) {
       decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, smem, aring);
@@ -867,10 +874,14 @@ __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves
   constexpr int kRingF8 = (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? dma_ring_bytes<FMT_FP8, kNmat>() : 0;
   constexpr int kRingF4 = (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4) ? dma_ring_bytes<FMT_MXFP4, kNmat>() : 0;
   constexpr int kRing = kDecWaves * (kRingF8 > kRingF4 ? kRingF8 : kRingF4);
-  // the down stage's shared activation ring follows the waves' weight rings
-  constexpr bool kShAct = STAGE == 1 && KS == 1;
-  constexpr int kActF8 = kShAct && (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? sh_act_ring_bytes<FMT_FP8, kNmat>() : 0;
-  constexpr int kActF4 = kShAct && (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4) ? sh_act_ring_bytes<FMT_MXFP4, kNmat>() : 0;
+  // without a K split the activation ring shared by the waves follows the waves' weight rings
+  constexpr bool kShAct = KS == 1;
+  constexpr int kActF8 = kShAct && (FMT_R == FMT_FP8 || FMT_S == FMT_FP8)
+                             ? sh_act_ring_bytes<FMT_FP8, kNmat, chunks_per_pass<FMT_FP8, STAGE, RT, KS>()>()
+                             : 0;
+  constexpr int kActF4 = kShAct && (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4)
+                             ? sh_act_ring_bytes<FMT_MXFP4, kNmat, chunks_per_pass<FMT_MXFP4, STAGE, RT, KS>()>()
+                             : 0;
   constexpr int kAct = kActF8 > kActF4 ? kActF8 : kActF4;
   constexpr int kRed = KS > 1 ? kRedFloats4 * 16 : 0;
   constexpr int kSmem = kRing + kAct > kRed ? kRing + kAct : kRed > 16 ? kRed : 16;
@@ -1029,6 +1040,8 @@ static hipError_t launch_one(dim3 g, const DecodeArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+constexpr int kGateUpSharedMinM = 128;
+
 // Bytes per weight times two (bf16 4, FP8 2, MXFP4 1).
 static int bytes_per_weight_x2(int fmt) { return fmt == FMT_BF16 ? 4 : fmt == FMT_FP8 ? 2 : 1; }
 
@@ -1040,6 +1053,15 @@ static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared
   if (stage == 0) {
     constexpr auto k1 = decode_stage_kernel<FR, FS, 0, 1, 4>;
     constexpr auto k2 = decode_stage_kernel<FR, FS, 0, 2, 4>;
+    if (FR == FMT_FP8 && a.M >= kGateUpSharedMinM) {
+      // large FP8 calls: no K split, the 4 waves own 64 + 64 rows and share
+      // the activation chunks through LDS (half the activation reads per
+      // weight byte of the RT = 2 K-split grid); measured C4 b=128 326 ->
+      // 302 us, b=256 457 -> 386 us, b=16-64 unchanged, b=8 slower (its grid
+      // no longer fills the GPU); MXFP4 (one chunk per pass) slower at b=8-64
+      constexpr auto ks = decode_stage_kernel<FR, FS, 0, 1, 1>;
+      return launch_one<ks>(dim3((imax + 63) / 64, gy), a, stream);
+    }
     const dim3 g1((imax + 15) / 16, gy), g2((imax + 31) / 32, gy);
     if (fill_of<k2>(g2) >= fill_of<k1>(g1) - kSlack) return launch_one<k2>(g2, a, stream);
     return launch_one<k1>(g1, a, stream);
