@@ -666,24 +666,24 @@ __device__ __forceinline__ ColDst pick(const ColDst (&d)[N], int c) {
 template <int STAGE>
 __device__ __forceinline__ void tile_epilogue(const DecodeArgs& a, const SegView& sv, ColDst d, int rows_at, f32x4 g,
                                               f32x4 u) {
-  uint16_t o[4];
+  float o[4];
   uint16_t* dst;
   if constexpr (STAGE == 0) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const float gg = bf16_round(g[v] * d.w);
-      const float uu = bf16_round(u[v] * d.w);
-      o[v] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
+      // gate and up rounded to bf16 by one packed conversion
+      const uint32_t gu = pack_bf16x2(g[v] * d.w, u[v] * d.w);
+      o[v] = act_apply(a.act_kind, __uint_as_float(gu << 16)) * __uint_as_float(gu & 0xffff0000u);
     }
     dst = a.act + static_cast<size_t>(d.row) * a.act_stride + rows_at;
   } else {
     dst = (sv.shared ? a.sh_out : a.ic3) + static_cast<size_t>(d.row) * a.H + rows_at;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(g[v] * d.w);
+    for (int v = 0; v < 4; ++v) o[v] = g[v] * d.w;
   }
   uint2 pk;
-  pk.x = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
-  pk.y = static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16);
+  pk.x = pack_bf16x2(o[0], o[1]);
+  pk.y = pack_bf16x2(o[2], o[3]);
   *reinterpret_cast<uint2*>(dst) = pk;
 }
 
@@ -966,24 +966,25 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
       }
     }
   }
-  uint16_t o[8];
+  uint32_t o[4];
   if (sh_out) {
     const uint4 v = *reinterpret_cast<const uint4*>(sh_out + static_cast<size_t>(t) * H + h);
     const uint32_t wds[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      o[2 * q] = f32_to_bf16(bf16_round(acc[2 * q]) + bf16_to_f32(static_cast<uint16_t>(wds[q] & 0xffffu)));
-      o[2 * q + 1] = f32_to_bf16(bf16_round(acc[2 * q + 1]) + bf16_to_f32(static_cast<uint16_t>(wds[q] >> 16)));
+      const uint32_t r = pack_bf16x2(acc[2 * q], acc[2 * q + 1]);  // bf16(sum) of both features
+      o[q] = pack_bf16x2(__uint_as_float(r << 16) + __uint_as_float(wds[q] << 16),
+                         __uint_as_float(r & 0xffff0000u) + __uint_as_float(wds[q] & 0xffff0000u));
     }
   } else {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) o[q] = f32_to_bf16(acc[q]);
+    for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(acc[2 * q], acc[2 * q + 1]);
   }
   uint4 out;
-  out.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
-  out.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
-  out.z = o[4] | (static_cast<uint32_t>(o[5]) << 16);
-  out.w = o[6] | (static_cast<uint32_t>(o[7]) << 16);
+  out.x = o[0];
+  out.y = o[1];
+  out.z = o[2];
+  out.w = o[3];
   *reinterpret_cast<uint4*>(y + static_cast<size_t>(t) * H + h) = out;
 }
 

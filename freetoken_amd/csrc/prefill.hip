@@ -438,17 +438,17 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillGemmArgs
       const int arow = shared ? a.numel + route : route;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        uint16_t o[4];
+        float o[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float gg = bf16_round(acc[s][i][v]);
           const float uu = bf16_round(acc[2 + s][i][v]);
-          o[v] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
+          o[v] = act_apply(a.act_kind, gg) * uu;
         }
         const int n = n0 + 32 * wn + 16 * s + g * 4;
         uint2 pk;
-        pk.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
-        pk.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+        pk.x = pack_bf16x2(o[0], o[1]);
+        pk.y = pack_bf16x2(o[2], o[3]);
         *reinterpret_cast<uint2*>(a.out + static_cast<size_t>(arow) * a.inter + n) = pk;
       }
     } else {
@@ -456,13 +456,10 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillGemmArgs
       uint16_t* dst = shared ? a.sh_out + static_cast<size_t>(route) * a.N : a.out + static_cast<size_t>(route) * a.N;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        uint16_t o[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(acc[j][i][v] * wt);
         const int n = n0 + wrow_base[j] + g * 4;
         uint2 pk;
-        pk.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
-        pk.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+        pk.x = pack_bf16x2(acc[j][i][0] * wt, acc[j][i][1] * wt);
+        pk.y = pack_bf16x2(acc[j][i][2] * wt, acc[j][i][3] * wt);
         *reinterpret_cast<uint2*>(dst + n) = pk;
       }
     }
@@ -641,6 +638,7 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
   __shared__ int s_row[2][kQBM];    // per tile parity: activation row of each route column (-1: padding)
   __shared__ int s_route[2][kQBM];  // per tile parity: route of each column (-1: padding)
   __shared__ float s_amax[GATE_UP ? 4 * kQBM : 1];  // gate_up epilogue: [row group][column] amax
+  __shared__ float s_wt[GATE_UP ? 1 : 2][kQBM];      // down: per tile parity, router weight of each column
 
   int v = blockIdx.x;
   QTile cur;
@@ -654,8 +652,10 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
   const int K = a.K, nkb = K / 128;
   const uint32_t rb = FMT == FMT_FP8 ? static_cast<uint32_t>(K) : static_cast<uint32_t>(K) / 2;
 
-  // column tid of tile t from its align entry `raw` (routed tiles)
-  auto put_rows = [&](const QTile& t, int raw, int b) {
+  // column tid of tile t from its align entry `raw` (routed tiles) and, for
+  // the down GEMM, the route's router weight wraw (loaded with raw, well
+  // before this call, so its latency stays off the epilogue)
+  auto put_rows = [&](const QTile& t, int raw, float wraw, int b) {
     const int tid = wave * kWave + fresh_lane();
     int row = -1, route = -1;
     if (t.shared) {
@@ -670,8 +670,12 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
     }
     s_row[b][tid] = row;
     s_route[b][tid] = route;
+    if constexpr (!GATE_UP) s_wt[b][tid] = t.shared ? 1.0f : wraw;
   };
   auto raw_of = [&](const QTile& t) -> int { return t.shared ? 0 : a.sorted[t.mblock * kQBM + tid]; };
+  auto wt_of = [&](const QTile& t, int raw) -> float {
+    return (GATE_UP || t.shared || raw >= a.numel) ? 1.0f : a.topk_w[raw];
+  };
   auto n0_of = [&](const QTile& t) -> int { return GATE_UP ? t.ntile * (kQRows / 2) : t.ntile * kQRows; };
   // first weight row of tile j of row group q, relative to the tile's first row n0
   auto trow_rel = [&](int q, int j) -> int {
@@ -741,6 +745,19 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
     }
   };
 
+  // piece q of a K step's copies (weight copies, activation copies, scales)
+  constexpr int kPieces = L::kACopies + L::kBCopies + 1;
+  auto issue_piece = [&](int q, int kb, int stg) {
+    uint8_t* st = q_lds + stg * L::kStage;
+    if (q < L::kACopies) {
+      lds_buf16(rsrc_w, st + (wave * L::kACopies + q) * 1024, avoff[q], static_cast<uint32_t>(kb) * L::kALine);
+    } else if (q < L::kACopies + L::kBCopies) {
+      const int c = q - L::kACopies;
+      lds_buf16(rsrc_x, st + L::kOffB + (wave * L::kBCopies + c) * 1024, xvoff[c], static_cast<uint32_t>(kb) * 128);
+    } else if (scopy) {
+      lds_buf4(rsrc_s, sdst_base + stg * L::kStage, svoff, static_cast<uint32_t>(kb) * 4);
+    }
+  };
   auto issue = [&](int kb, int stg) {
     uint8_t* st = q_lds + stg * L::kStage;
 #pragma unroll
@@ -755,7 +772,14 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   f32x4 acc[4][8];
 
-  auto compute = [&](int stg) {
+  // One K step from stage stg.  With ikb >= 0 the copies of step ikb into
+  // stage istg are issued two per column tile in the first tiles, between the
+  // LDS reads and MFMAs, instead of as one burst before the step (a burst
+  // stalls the wave's in-order issue until the memory pipeline takes it:
+  // measured 3% of the FP8 gate_up GEMM; MXFP4, whose 3-stage ring already
+  // spills a few registers, keeps the burst).
+  constexpr bool kSpread = FMT == FMT_FP8;
+  auto compute = [&](int stg, int ikb, int istg) {
     const uint8_t* st = q_lds + stg * L::kStage;
     i32x8 wf[4];
     int wcode[4];
@@ -801,6 +825,11 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
     float fp = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
+      if (ikb >= 0) {
+#pragma unroll
+        for (int q = 2 * i; q < 2 * i + 2; ++q)
+          if (q < kPieces) issue_piece(q, ikb, istg);
+      }
       if (i + 1 < 8) read_x(i + 1, xf[(i + 1) & 1], xs[(i + 1) & 1]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -838,16 +867,19 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
         float m = 0.f;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-          uint16_t o[4];
+          float o[4];
 #pragma unroll
           for (int v4 = 0; v4 < 4; ++v4) {
-            const float gg = bf16_round(acc[s2][i][v4]);
-            const float uu = bf16_round(acc[2 + s2][i][v4]);
-            o[v4] = f32_to_bf16(act_apply(a.act_kind, gg) * uu);
-            m = fmaxf(m, fabsf(bf16_to_f32(o[v4])));
+            // gate and up of one feature rounded to bf16 by one packed conversion
+            const uint32_t gu = pack_bf16x2(acc[s2][i][v4], acc[2 + s2][i][v4]);
+            o[v4] = act_apply(a.act_kind, __uint_as_float(gu << 16)) * __uint_as_float(gu & 0xffff0000u);
           }
-          pk[i][s2][0] = o[0] | (static_cast<uint32_t>(o[1]) << 16);
-          pk[i][s2][1] = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t p2 = pack_bf16x2(o[2 * h], o[2 * h + 1]);
+            pk[i][s2][h] = p2;
+            m = fmaxf(m, fmaxf(fabsf(__uint_as_float(p2 << 16)), fabsf(__uint_as_float(p2 & 0xffff0000u))));
+          }
         }
         m = fmaxf(m, __shfl_xor(m, 16));
         m = fmaxf(m, __shfl_xor(m, 32));
@@ -895,18 +927,15 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
         const int col = 128 * ch + 16 * i + r16;
         const int route = s_route[b][col];
         if (route < 0) continue;
-        const float wt = t.shared ? 1.0f : a.topk_w[route];
+        const float wt = s_wt[b][col];
         uint16_t* dst = t.shared ? a.sh_out + static_cast<size_t>(route) * a.N : a.out + static_cast<size_t>(route) * a.N;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int n = n0 + trow_rel(rg, j) + g * 4;
           if (n >= a.N) continue;
-          uint16_t o[4];
-#pragma unroll
-          for (int v4 = 0; v4 < 4; ++v4) o[v4] = f32_to_bf16(acc[j][i][v4] * wt);
           uint2 pk2;
-          pk2.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
-          pk2.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+          pk2.x = pack_bf16x2(acc[j][i][0] * wt, acc[j][i][1] * wt);
+          pk2.y = pack_bf16x2(acc[j][i][2] * wt, acc[j][i][3] * wt);
           *reinterpret_cast<uint2*>(dst + n) = pk2;
         }
       }
@@ -919,7 +948,10 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
   // tile issue the next tile's first D steps, which land while this tile's
   // epilogue runs.  The next tile's align entries are loaded at the start of
   // a tile and published before its last D steps.
-  if (tid < kQBM) put_rows(cur, raw_of(cur), 0);
+  if (tid < kQBM) {
+    const int raw0 = raw_of(cur);
+    put_rows(cur, raw0, wt_of(cur, raw0), 0);
+  }
   __syncthreads();
   setup(cur, 0);
   int buf = 0, g0 = 0;
@@ -945,13 +977,18 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
     wait_vm<0>();
     bare_barrier();
     const int raw = has_next && tid < kQBM ? raw_of(nxt) : 0;
+    const float wraw = has_next && tid < kQBM ? wt_of(nxt, raw) : 1.0f;
     // steady steps: step kb + D of this tile is issued; step kb + 1 must have
     // landed at the end (later ones may still fly); every LDS read of the step
     // has returned before its MFMA used it
     int kb = 0;
     for (; kb < nkb - D; ++kb) {
-      issue(kb + D, (g0 + kb + D) % S);
-      compute((g0 + kb) % S);
+      if constexpr (kSpread) {
+        compute((g0 + kb) % S, kb + D, (g0 + kb + D) % S);
+      } else {
+        issue(kb + D, (g0 + kb + D) % S);
+        compute((g0 + kb) % S, -1, 0);
+      }
       if (D == 2 && (kb + 2 < nkb || cross)) wait_vm<L::kDmaPerStep>();
       else wait_vm<0>();
       wait_lgkm0();
@@ -960,14 +997,18 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
     // publish the next tile's rows; its first steps ride in this tile's last
     // D steps
     if (has_next) {
-      if (tid < kQBM) put_rows(nxt, raw, buf ^ 1);
+      if (tid < kQBM) put_rows(nxt, raw, wraw, buf ^ 1);
       wait_lgkm0();
       bare_barrier();
       if (cross) setup(nxt, buf ^ 1);
     }
     for (; kb < nkb; ++kb) {
-      if (cross) issue(kb + D - nkb, (g0 + kb + D) % S);
-      compute((g0 + kb) % S);
+      if constexpr (kSpread) {
+        compute((g0 + kb) % S, cross ? kb + D - nkb : -1, (g0 + kb + D) % S);
+      } else {
+        if (cross) issue(kb + D - nkb, (g0 + kb + D) % S);
+        compute((g0 + kb) % S, -1, 0);
+      }
       if (kb + 1 < nkb) {
         if (D == 2 && cross) wait_vm<L::kDmaPerStep>();
         else wait_vm<0>();
