@@ -497,11 +497,6 @@ int experts_decode_impl(const void* x, int M, int top_k, const float* topk_w, co
   }
   // ids the later kernels see: slot ids when the lookup ran here
   const int32_t* route_ids = slots ? slots->slot_ids : topk_ids;
-  g_timer.start_call(stream);
-  rc = route ? check_hip(ftmoe::launch_route_align(*route, al, stream), "experts_decode route + align")
-             : check_hip(ftmoe::launch_align(al, stream), "experts_decode align");
-  if (rc) return rc;
-  g_timer.mark();
 
   ftmoe::DecodeArgs d{};
   d.x = static_cast<const uint16_t*>(x);
@@ -530,8 +525,25 @@ int experts_decode_impl(const void* x, int M, int top_k, const float* topk_w, co
   d.sh_out = L.sh_out;
   d.act_kind = activation;
   d.weight_on_input = apply_router_weight_on_input;
-  rc = check_hip(ftmoe::launch_decode_stage(0, bank->format, shared ? shared->format : FTMOE_FMT_NONE, d, stream),
-                 "experts_decode gate_up");
+  const int fmt_s = shared ? shared->format : FTMOE_FMT_NONE;
+
+  g_timer.start_call(stream);
+  // small grouped-router calls with a shared expert: the shared expert's
+  // gate_up runs in the router's launch
+  bool shared_ran = false;
+  if (route && shared) {
+    const hipError_t e = ftmoe::launch_route_shared(*route, al, fmt_s, d, stream);
+    if (e == hipSuccess) shared_ran = true;
+    else if (e != hipErrorNotSupported) return check_hip(e, "experts_decode route + align + shared gate_up");
+  }
+  if (!shared_ran) {
+    rc = route ? check_hip(ftmoe::launch_route_align(*route, al, stream), "experts_decode route + align")
+               : check_hip(ftmoe::launch_align(al, stream), "experts_decode align");
+    if (rc) return rc;
+  }
+  g_timer.mark();
+
+  rc = check_hip(ftmoe::launch_decode_stage(0, bank->format, fmt_s, d, stream, !shared_ran), "experts_decode gate_up");
   if (rc) return rc;
   g_timer.mark();
   rc = check_hip(ftmoe::launch_decode_stage(1, bank->format, shared ? shared->format : FTMOE_FMT_NONE, d, stream),

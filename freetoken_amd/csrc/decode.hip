@@ -32,7 +32,9 @@
 // Stage 1 (down): rows h0..h0+15, routed: ic3[route] = bf16(acc * w[route]),
 //   shared: sh_out[token] = bf16(acc).
 // A third kernel sums the routes of every token (and the shared expert).
+#include "align_wave.h"
 #include "kernels.h"
+#include "route_token.h"
 
 namespace ftmoe {
 
@@ -869,25 +871,31 @@ constexpr int kRedFloats4 = kDecWaves * 8 * kWave;  // NMAT * chunks_per_pass <=
 // times heavier than the routed ones (a bf16 shared expert beside MXFP4 routed
 // experts reads 4x the bytes per row) and would otherwise start last and trail.
 template <int FMT_R, int FMT_S, int STAGE, int RT, int KS>
-__global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) decode_stage_kernel(DecodeArgs a) {
-  constexpr int kNmat = STAGE == 0 ? 2 * RT : RT;
-  constexpr int kRingF8 = (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? dma_ring_bytes<FMT_FP8, kNmat>() : 0;
-  constexpr int kRingF4 = (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4) ? dma_ring_bytes<FMT_MXFP4, kNmat>() : 0;
-  constexpr int kRing = kDecWaves * (kRingF8 > kRingF4 ? kRingF8 : kRingF4);
+struct StageSmem {
+  static constexpr int kNmat = STAGE == 0 ? 2 * RT : RT;
+  static constexpr int kRingF8 = (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? dma_ring_bytes<FMT_FP8, kNmat>() : 0;
+  static constexpr int kRingF4 =
+      (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4) ? dma_ring_bytes<FMT_MXFP4, kNmat>() : 0;
+  static constexpr int kRing = kDecWaves * (kRingF8 > kRingF4 ? kRingF8 : kRingF4);
   // without a K split the activation ring shared by the waves follows the waves' weight rings
-  constexpr bool kShAct = KS == 1;
-  constexpr int kActF8 = kShAct && (FMT_R == FMT_FP8 || FMT_S == FMT_FP8)
-                             ? sh_act_ring_bytes<FMT_FP8, kNmat, chunks_per_pass<FMT_FP8, STAGE, RT, KS>()>()
-                             : 0;
-  constexpr int kActF4 = kShAct && (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4)
-                             ? sh_act_ring_bytes<FMT_MXFP4, kNmat, chunks_per_pass<FMT_MXFP4, STAGE, RT, KS>()>()
-                             : 0;
-  constexpr int kAct = kActF8 > kActF4 ? kActF8 : kActF4;
-  constexpr int kRed = KS > 1 ? kRedFloats4 * 16 : 0;
-  constexpr int kSmem = kRing + kAct > kRed ? kRing + kAct : kRed > 16 ? kRed : 16;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kSmem];
-  const int n_sh = static_cast<int>(gridDim.y) - a.max_seg;  // shared pieces (0 without a shared expert)
-  int seg = blockIdx.y;
+  static constexpr bool kShAct = KS == 1;
+  static constexpr int kActF8 = kShAct && (FMT_R == FMT_FP8 || FMT_S == FMT_FP8)
+                                    ? sh_act_ring_bytes<FMT_FP8, kNmat, chunks_per_pass<FMT_FP8, STAGE, RT, KS>()>()
+                                    : 0;
+  static constexpr int kActF4 =
+      kShAct && (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4)
+          ? sh_act_ring_bytes<FMT_MXFP4, kNmat, chunks_per_pass<FMT_MXFP4, STAGE, RT, KS>()>()
+          : 0;
+  static constexpr int kAct = kActF8 > kActF4 ? kActF8 : kActF4;
+  static constexpr int kRed = KS > 1 ? kRedFloats4 * 16 : 0;
+  static constexpr int kSmem = kRing + kAct > kRed ? kRing + kAct : kRed > 16 ? kRed : 16;
+};
+
+// One workgroup of the stage grid: row block bx of segment seg, the first n_sh
+// segments being the shared expert's token pieces.
+template <int FMT_R, int FMT_S, int STAGE, int RT, int KS>
+__device__ __forceinline__ void decode_stage_block(const DecodeArgs& a, int bx, int seg, int n_sh, uint8_t* smem) {
+  constexpr int kRing = StageSmem<FMT_R, FMT_S, STAGE, RT, KS>::kRing;
   SegView sv;
   sv.shared = seg < n_sh;
   if (sv.shared) {
@@ -902,7 +910,7 @@ __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves
     sv.count = a.seg_count[seg];
   }
   const int inter = sv.shared ? a.Is : a.I;
-  const int row0 = blockIdx.x * (kDecWaves / KS) * RT * 16;
+  const int row0 = bx * (kDecWaves / KS) * RT * 16;
   if (STAGE == 0 && row0 >= inter) return;
   // field-wise selects keep the kernel argument block out of private memory
   BankView bank;
@@ -924,6 +932,82 @@ __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves
     if constexpr (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4)
       decode_segment<FMT_MXFP4, STAGE, RT, KS>(a, bank, sv, row0, inter, smem, smem + kRing);
   }
+}
+
+template <int FMT_R, int FMT_S, int STAGE, int RT, int KS>
+__global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) decode_stage_kernel(DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[StageSmem<FMT_R, FMT_S, STAGE, RT, KS>::kSmem];
+  // shared pieces (0 without a shared expert, or when the router's launch ran them)
+  const int n_sh = static_cast<int>(gridDim.y) - a.max_seg;
+  decode_stage_block<FMT_R, FMT_S, STAGE, RT, KS>(a, blockIdx.x, blockIdx.y, n_sh, smem);
+}
+
+// ---- Router + permutation beside the shared expert's gate_up --------------
+// For decode calls of at most kRouteSharedTokens tokens with a grouped-sigmoid
+// router and a shared expert: workgroup 0 routes (wave t takes token t, then
+// wave 0 aligns, as route_align_kernel does) while workgroups 1.. run the
+// shared expert's gate_up piece -- the same K split, code and arithmetic as
+// the shared piece of the stage-0 grid, which then leaves it out.  The shared
+// expert does not depend on the routing, so its weights stream while the
+// router's dependent chains keep one CU busy.  One 16-row tile per wave gives
+// the piece enough workgroups to finish under the router (two tiles per wave
+// outlasted it).  Measured: C3 (bf16 shared beside MXFP4) b=1 60.6 -> 53.8 us,
+// b=2 69.3 -> 67.3 us; C4 b=1 -1%; from 4 tokens no gain, so those keep the
+// separate launches.
+constexpr int kSharedRT = 1, kSharedKS = 4;
+constexpr int kRouteSharedTokens = 2;
+
+template <int PER, int FS>
+__global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves_per_eu(2)))
+route_shared_kernel(RouteArgs r, AlignArgs al, DecodeArgs a) {
+  using SM = StageSmem<FS, FS, 0, kSharedRT, kSharedKS>;
+  static_assert(SM::kSmem >= (kDecWaves * PER + 1) * kWave * 4, "router scratch must fit the stage's LDS");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SM::kSmem];
+  if (blockIdx.x == 0) {
+    float* s_c = reinterpret_cast<float*>(smem);
+    int* s_ids = reinterpret_cast<int*>(smem + kDecWaves * PER * kWave * 4);
+    const int lane = lane_id();
+    const int wave = threadIdx.x / kWave;
+    if (wave < r.M) {
+      const int id = grouped_token<PER>(static_cast<const float*>(r.logits) + static_cast<size_t>(wave) * r.E, r.bias,
+                                        r.E, r.n_group, r.topk_group, r.k, r.renorm, r.scale, s_c + wave * PER * kWave,
+                                        r.out_w + static_cast<size_t>(wave) * r.k,
+                                        r.out_ids + static_cast<size_t>(wave) * r.k);
+      if (lane < r.k) s_ids[wave * r.k + lane] = id;
+    }
+    __syncthreads();
+    if (wave == 0) align_wave(al, s_ids);
+    return;
+  }
+  decode_stage_block<FS, FS, 0, kSharedRT, kSharedKS>(a, blockIdx.x - 1, 0, 1, smem);
+}
+
+template <int PER>
+static hipError_t launch_route_shared_per(int fmt_s, const RouteArgs& r, const AlignArgs& al, const DecodeArgs& a,
+                                          hipStream_t stream) {
+  const dim3 grid(1 + (a.Is + kSharedRT * 16 * (kDecWaves / kSharedKS) - 1) / (kSharedRT * 16 * (kDecWaves / kSharedKS)));
+  if (fmt_s == FMT_BF16)
+    hipLaunchKernelGGL((route_shared_kernel<PER, FMT_BF16>), grid, dim3(kDecWaves * kWave), 0, stream, r, al, a);
+  else if (fmt_s == FMT_FP8)
+    hipLaunchKernelGGL((route_shared_kernel<PER, FMT_FP8>), grid, dim3(kDecWaves * kWave), 0, stream, r, al, a);
+  else
+    hipLaunchKernelGGL((route_shared_kernel<PER, FMT_MXFP4>), grid, dim3(kDecWaves * kWave), 0, stream, r, al, a);
+  return hipGetLastError();
+}
+
+bool route_shared_fits(const RouteArgs& r, const AlignArgs& al, int fmt_s, const DecodeArgs& a) {
+  const int per = (r.E + kWave - 1) / kWave;
+  return r.grouped && fmt_s != FMT_NONE && a.Is > 0 && r.M <= kRouteSharedTokens && r.M * r.k <= kWave &&
+         align_fits_wave(al) && per <= 4 && al.ids == r.out_ids;
+}
+
+hipError_t launch_route_shared(const RouteArgs& r, const AlignArgs& al, int fmt_s, const DecodeArgs& a,
+                               hipStream_t stream) {
+  if (!route_shared_fits(r, al, fmt_s, a)) return hipErrorNotSupported;
+  const int per = (r.E + kWave - 1) / kWave;
+  if (per <= 1) return launch_route_shared_per<1>(fmt_s, r, al, a, stream);
+  if (per <= 2) return launch_route_shared_per<2>(fmt_s, r, al, a, stream);
+  return launch_route_shared_per<4>(fmt_s, r, al, a, stream);
 }
 
 // y[t] = bf16( bf16(sum_r ic3[t,r]) + sh_out[t] ), routes with ids outside
@@ -1080,9 +1164,10 @@ static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared
   return launch_one<k1>(g1, a, stream);
 }
 
-hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream) {
-  const bool sh = fmt_s != FMT_NONE;
-  const int fs = sh ? fmt_s : fmt_r;  // FMT_S is unused without a shared expert
+hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream,
+                               bool shared_pieces) {
+  const bool sh = fmt_s != FMT_NONE && shared_pieces;
+  const int fs = fmt_s != FMT_NONE ? fmt_s : fmt_r;  // FMT_S is unused without a shared expert
 #define FTMOE_CASE(R, S) \
   if (fmt_r == R && fs == S) return launch_stage_t<R, S>(stage, a, sh, stream);
   FTMOE_CASE(FMT_BF16, FMT_BF16)

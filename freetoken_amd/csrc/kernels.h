@@ -100,7 +100,16 @@ size_t align_gcount_ints(int numel, int num_experts);
 hipError_t launch_align_large(const AlignArgs& a, int32_t* gcount, hipStream_t stream);
 hipError_t launch_slot_map(const int32_t* ids, int numel, const int32_t* slot_for_id, int table_size,
                            int32_t* slot_ids, uint8_t* miss_mask, long long* stats, hipStream_t stream);
-hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream);
+// shared_pieces false: the shared expert's pieces are left out of the grid
+// (its gate_up already ran beside the router, launch_route_shared)
+hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream,
+                               bool shared_pieces = true);
+// Router + permutation (as launch_route_align) and, in the same launch, the
+// shared expert's gate_up; hipErrorNotSupported when the call does not
+// qualify (grouped router, shared expert, at most 2 tokens, the one-wave
+// align, at most 256 experts).
+hipError_t launch_route_shared(const RouteArgs& r, const AlignArgs& al, int fmt_s, const DecodeArgs& a,
+                               hipStream_t stream);
 struct PrefillGemmArgs {
   // rows of the activation operand
   const uint8_t* xq;        // fp8 [rows, K] (FP8 / MXFP4) or bf16 [rows, K] (BF16)

@@ -45,14 +45,21 @@ def test_softmax_routed_matches_separate_calls(dev, M, logit_dtype):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M", [1, 4, 8, 16, 33])
-def test_grouped_routed_cached_matches_separate_calls(dev, M):
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16, 33])
+@pytest.mark.parametrize("fmts", [("fp8", "fp8"), ("mxfp4", "bf16")])
+def test_grouped_routed_cached_matches_separate_calls(dev, M, fmts):
     """C4-shaped router (256 experts, 8 groups, top-4 groups, k 8) over a
-    64-slot table with misses, with an FP8 shared expert."""
+    64-slot table with misses, with a shared expert (FP8 beside FP8, bf16 beside
+    MXFP4 as in C3).  Up to 2 tokens the shared expert's gate_up runs in the
+    router's launch; the outputs must still equal the separate calls bit for
+    bit."""
     rng = np.random.default_rng(100 + M)
     E, S, H, I, k = 256, 64, 512, 256, 8
-    bank = to_device_bank(code_bank("fp8", S, H, I, rng), dev)
-    shared = to_device_bank(code_bank("fp8", 1, H, I, rng), dev)
+    bank = to_device_bank(code_bank(fmts[0], S, H, I, rng), dev)
+    if fmts[1] == "bf16":
+        shared = to_device_bank(synth.make_bank("bf16", 1, H, 384, rng), dev)  # its own intermediate size
+    else:
+        shared = to_device_bank(code_bank(fmts[1], 1, H, I, rng), dev)
     table = np.full(E, -1, dtype=np.int32)
     table[np.sort(rng.choice(E, S, replace=False))] = np.arange(S, dtype=np.int32)
     t_dev = torch.from_numpy(table).to(dev)
