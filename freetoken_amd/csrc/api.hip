@@ -487,7 +487,9 @@ int experts_decode_impl(const void* x, int M, int top_k, const float* topk_w, co
   al.seg_start = L.seg_start;
   al.seg_count = L.seg_count;
   al.n_seg = L.n_seg;
-  al.seg_cap = ftmoe::kDecodeSegCap;
+  // segment cap (the workspace is sized for the smaller one, which gives more segments)
+  const int seg_cap = ftmoe::decode_seg_cap(M, bank->format == FTMOE_FMT_FP8_B128);
+  al.seg_cap = seg_cap;
   if (slots) {
     al.slot_for_id = slots->slot_for_id;
     al.table_size = slots->num_experts;
@@ -511,8 +513,8 @@ int experts_decode_impl(const void* x, int M, int top_k, const float* topk_w, co
   d.H = bank->hidden;
   d.I = bank->inter;
   d.Is = shared ? shared->inter : 0;
-  d.max_seg = ftmoe::decode_max_segments(numel, bank->num_rows);
-  d.seg_cap = ftmoe::kDecodeSegCap;
+  d.max_seg = ftmoe::decode_max_segments(numel, bank->num_rows, seg_cap);
+  d.seg_cap = seg_cap;
   d.gate_up = {static_cast<const uint8_t*>(bank->gate_up), bank->gate_up_scale};
   d.down = {static_cast<const uint8_t*>(bank->down), bank->down_scale};
   if (shared) {

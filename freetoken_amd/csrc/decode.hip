@@ -426,12 +426,15 @@ __device__ __forceinline__ void dma_tail(int left, const uint8_t* ring, uint32_t
 // workgroup, two resident per CU) or 3 stages of 2 (FP8 measured against 2
 // and 4: 3 is the fastest at b = 1 and no slower at b = 8 and 64; MXFP4 keeps
 // 2 when two route chunks make a stage's registers large).
+// Passes of four route chunks (the wide kernels of large FP8 calls) keep 2
+// stages as well, so that their LDS stays at 80 KB.
 template <int FMT, int NMAT, int NCH>
 constexpr int dma_depth() {
-  return NMAT >= 4 ? 2 : (FMT == FMT_MXFP4 && NCH > 1) ? 2 : 3;
+  return (NMAT >= 4 || NCH >= 4) ? 2 : (FMT == FMT_MXFP4 && NCH > 1) ? 2 : 3;
 }
-template <int FMT, int NMAT>
-constexpr int dma_ring_bytes() {  // per wave, the larger of the NCH variants
+template <int FMT, int NMAT, int WIDE = 0>
+constexpr int dma_ring_bytes() {  // per wave, the larger of the NCH variants (WIDE: four-chunk passes only)
+  if constexpr (WIDE) return dma_depth<FMT, NMAT, 4>() * NMAT * kTileBytes;
   return (dma_depth<FMT, NMAT, 1>() > dma_depth<FMT, NMAT, 2>() ? dma_depth<FMT, NMAT, 1>()
                                                                   : dma_depth<FMT, NMAT, 2>()) *
          NMAT * kTileBytes;
@@ -510,7 +513,8 @@ constexpr int sh_per_step() {  // vector memory instructions of one sh_issue
   return 3 * NMAT + NCH * act_copies<FMT>();
 }
 template <int FMT, int NMAT, int CMAX>
-constexpr int sh_act_ring_bytes() {  // the larger of the NCH variants up to CMAX chunks per pass
+constexpr int sh_act_ring_bytes() {  // the larger of the NCH variants up to CMAX chunks per pass (4: four only)
+  if constexpr (CMAX == 4) return (dma_depth<FMT, NMAT, 4>() + 1) * act_slot_bytes<FMT, 4>();
   constexpr int one = (dma_depth<FMT, NMAT, 1>() + 1) * act_slot_bytes<FMT, 1>();
   constexpr int two = (dma_depth<FMT, NMAT, 2>() + 1) * act_slot_bytes<FMT, 2>();
   return CMAX == 1 || one > two ? one : two;
@@ -694,7 +698,7 @@ __device__ __forceinline__ void tile_epilogue(const DecodeArgs& a, const SegView
 // 16-row tiles per matrix (gate and up tiles in stage 0) and its KS waves split
 // K.  With KS > 1 the partial sums meet in LDS (red[4][NMAT][NCH][64] float4)
 // and are added in fixed wave order, so results do not depend on timing.
-template <int FMT, int STAGE, int RT, int KS, int NCH>
+template <int FMT, int STAGE, int RT, int KS, int NCH, int WIDE = 0>
 __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView& bank, const SegView& sv, int base,
                                             int row0, int inter, uint8_t* smem, uint8_t* aring) {
   f32x4* red = reinterpret_cast<f32x4*>(smem);
@@ -770,7 +774,7 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
         for (int h = 0; h < 2; ++h) dt.voff[m][h] = static_cast<uint32_t>(tile_row + 8 * h + dr) * rb + dc * 16;
         dt.soff[m] = FMT == FMT_FP8 ? wt.soff[m] : static_cast<uint32_t>(tile_row + r16) * (K / 32);
       }
-      uint8_t* ring = smem + wave * dma_ring_bytes<FMT, NMAT>();
+      uint8_t* ring = smem + wave * dma_ring_bytes<FMT, NMAT, WIDE>();
       if constexpr (KS == 1) {
         // activation copies: copy v of chunk c of this wave covers columns
         // q * (1024 / CB) + lane / (CB / 16), q = wave * act_copies + v
@@ -841,20 +845,26 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
 // Route chunks (of 16) per pass, sized so that two K stages of weights and
 // activations plus the accumulators fit 256 registers per lane (occupancy 2).
 // With the activations shared through LDS (KS = 1) MXFP4 takes one chunk per
-// pass, which keeps LDS at 80 KB (two workgroups per CU).
-template <int FMT, int STAGE, int RT, int KS>
+// pass, which keeps LDS at 80 KB (two workgroups per CU).  WIDE kernels (FP8
+// calls of at least kWideMinTokens tokens, segments of up to 64 routes) run
+// every FP8 pass over four chunks, so an expert's weights are read once for
+// its 64 routes.
+template <int FMT, int STAGE, int RT, int KS, int WIDE = 0>
 constexpr int chunks_per_pass() {
+  if constexpr (WIDE && KS == 1 && FMT == FMT_FP8) return 4;
   if constexpr (KS == 1 && FMT == FMT_MXFP4) return 1;
   if constexpr (STAGE == 0) return RT == 1 ? 2 : (FMT == FMT_BF16 ? 1 : 2);
   return 2;
 }
 
-template <int FMT, int STAGE, int RT, int KS>
+template <int FMT, int STAGE, int RT, int KS, int WIDE = 0>
 __device__ __forceinline__ void decode_segment(const DecodeArgs& a, const BankView& bank, const SegView& sv, int row0,
                                                int inter, uint8_t* smem, uint8_t* aring) {
-  constexpr int CMAX = chunks_per_pass<FMT, STAGE, RT, KS>();
+  constexpr int CMAX = chunks_per_pass<FMT, STAGE, RT, KS, WIDE>();
   for (int base = 0; base < sv.count; base += 16 * CMAX) {
-    if constexpr (CMAX == 1) {
+    if constexpr (CMAX == 4) {
+      decode_pass<FMT, STAGE, RT, KS, 4, WIDE>(a, bank, sv, base, row0, inter, smem, aring);
+    } else if constexpr (CMAX == 1) {
       decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, smem, aring);
     } else {
       if (sv.count - base <= 16) decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, smem, aring);
@@ -863,24 +873,25 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, const BankVi
   }
 }
 
-constexpr int kRedFloats4 = kDecWaves * 8 * kWave;  // NMAT * chunks_per_pass <= 8
+constexpr int kRedFloats4 = kDecWaves * 8 * kWave;  // NMAT * chunks_per_pass <= 8 (K-split kernels)
 
 // Grid: x = row blocks of (4/KS) * RT * 16 rows, y = the shared expert's token
 // pieces of seg_cap tokens, then the routed segments (max_seg, the tail beyond
 // n_seg exits).  The shared pieces come first: their workgroups can be several
 // times heavier than the routed ones (a bf16 shared expert beside MXFP4 routed
 // experts reads 4x the bytes per row) and would otherwise start last and trail.
-template <int FMT_R, int FMT_S, int STAGE, int RT, int KS>
+template <int FMT_R, int FMT_S, int STAGE, int RT, int KS, int WIDE = 0>
 struct StageSmem {
   static constexpr int kNmat = STAGE == 0 ? 2 * RT : RT;
-  static constexpr int kRingF8 = (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? dma_ring_bytes<FMT_FP8, kNmat>() : 0;
+  static constexpr int kRingF8 =
+      (FMT_R == FMT_FP8 || FMT_S == FMT_FP8) ? dma_ring_bytes<FMT_FP8, kNmat, WIDE && KS == 1>() : 0;
   static constexpr int kRingF4 =
       (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4) ? dma_ring_bytes<FMT_MXFP4, kNmat>() : 0;
   static constexpr int kRing = kDecWaves * (kRingF8 > kRingF4 ? kRingF8 : kRingF4);
   // without a K split the activation ring shared by the waves follows the waves' weight rings
   static constexpr bool kShAct = KS == 1;
   static constexpr int kActF8 = kShAct && (FMT_R == FMT_FP8 || FMT_S == FMT_FP8)
-                                    ? sh_act_ring_bytes<FMT_FP8, kNmat, chunks_per_pass<FMT_FP8, STAGE, RT, KS>()>()
+                                    ? sh_act_ring_bytes<FMT_FP8, kNmat, chunks_per_pass<FMT_FP8, STAGE, RT, KS, WIDE>()>()
                                     : 0;
   static constexpr int kActF4 =
       kShAct && (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4)
@@ -893,9 +904,9 @@ struct StageSmem {
 
 // One workgroup of the stage grid: row block bx of segment seg, the first n_sh
 // segments being the shared expert's token pieces.
-template <int FMT_R, int FMT_S, int STAGE, int RT, int KS>
+template <int FMT_R, int FMT_S, int STAGE, int RT, int KS, int WIDE = 0>
 __device__ __forceinline__ void decode_stage_block(const DecodeArgs& a, int bx, int seg, int n_sh, uint8_t* smem) {
-  constexpr int kRing = StageSmem<FMT_R, FMT_S, STAGE, RT, KS>::kRing;
+  constexpr int kRing = StageSmem<FMT_R, FMT_S, STAGE, RT, KS, WIDE>::kRing;
   SegView sv;
   sv.shared = seg < n_sh;
   if (sv.shared) {
@@ -927,19 +938,19 @@ __device__ __forceinline__ void decode_stage_block(const DecodeArgs& a, int bx, 
       decode_segment<FMT_BF16, STAGE, RT, KS>(a, bank, sv, row0, inter, smem, smem + kRing);
   } else if (fmt == FMT_FP8) {
     if constexpr (FMT_R == FMT_FP8 || FMT_S == FMT_FP8)
-      decode_segment<FMT_FP8, STAGE, RT, KS>(a, bank, sv, row0, inter, smem, smem + kRing);
+      decode_segment<FMT_FP8, STAGE, RT, KS, WIDE>(a, bank, sv, row0, inter, smem, smem + kRing);
   } else {
     if constexpr (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4)
       decode_segment<FMT_MXFP4, STAGE, RT, KS>(a, bank, sv, row0, inter, smem, smem + kRing);
   }
 }
 
-template <int FMT_R, int FMT_S, int STAGE, int RT, int KS>
+template <int FMT_R, int FMT_S, int STAGE, int RT, int KS, int WIDE = 0>
 __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) decode_stage_kernel(DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[StageSmem<FMT_R, FMT_S, STAGE, RT, KS>::kSmem];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[StageSmem<FMT_R, FMT_S, STAGE, RT, KS, WIDE>::kSmem];
   // shared pieces (0 without a shared expert, or when the router's launch ran them)
   const int n_sh = static_cast<int>(gridDim.y) - a.max_seg;
-  decode_stage_block<FMT_R, FMT_S, STAGE, RT, KS>(a, blockIdx.x, blockIdx.y, n_sh, smem);
+  decode_stage_block<FMT_R, FMT_S, STAGE, RT, KS, WIDE>(a, blockIdx.x, blockIdx.y, n_sh, smem);
 }
 
 // ---- Router + permutation beside the shared expert's gate_up --------------
@@ -1135,15 +1146,31 @@ static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared
   const int gy = a.max_seg + (has_shared ? (a.M + a.seg_cap - 1) / a.seg_cap : 0);
   const int imax = has_shared ? max(a.I, a.Is) : a.I;
   constexpr double kSlack = 0.15;
+  if constexpr (FR == FMT_FP8) {
+    if (a.seg_cap > kDecodeSegCap) {
+      // wide segments (FP8 calls from kWideMinTokens tokens): no K split (as
+      // below) and four-chunk passes, so an expert with up to 64 routes is
+      // read once (with 32-route segments about half of C4 b=256's experts
+      // were read twice): C4 b=256 637 -> 594-597 us; at b=128-192, where
+      // most experts have fewer than 32 routes, the wide passes were equal or
+      // slower (b=128 498 -> 549 us)
+      if (stage == 0) {
+        constexpr auto kw = decode_stage_kernel<FR, FS, 0, 1, 1, 1>;
+        return launch_one<kw>(dim3((imax + 63) / 64, gy), a, stream);
+      }
+      constexpr auto kw = decode_stage_kernel<FR, FS, 1, 2, 1, 1>;
+      return launch_one<kw>(dim3(a.H / 128, gy), a, stream);
+    }
+  }
   if (stage == 0) {
     constexpr auto k1 = decode_stage_kernel<FR, FS, 0, 1, 4>;
     constexpr auto k2 = decode_stage_kernel<FR, FS, 0, 2, 4>;
     if (FR == FMT_FP8 && a.M >= kGateUpSharedMinM) {
-      // large FP8 calls: no K split, the 4 waves own 64 + 64 rows and share
-      // the activation chunks through LDS (half the activation reads per
-      // weight byte of the RT = 2 K-split grid); measured C4 b=128 326 ->
-      // 302 us, b=256 457 -> 386 us, b=16-64 unchanged, b=8 slower (its grid
-      // no longer fills the GPU); MXFP4 (one chunk per pass) slower at b=8-64
+      // large FP8 calls: no K split, the 4 waves own 16 + 16 rows each and
+      // share the activation chunks through LDS (half the activation reads
+      // per weight byte of the RT = 2 K-split grid); measured C4 b=128 326 ->
+      // 302 us, b=16-64 unchanged, b=8 slower (its grid no longer fills the
+      // GPU); MXFP4 (one chunk per pass) slower at b=8-64
       constexpr auto ks = decode_stage_kernel<FR, FS, 0, 1, 1>;
       return launch_one<ks>(dim3((imax + 63) / 64, gy), a, stream);
     }
