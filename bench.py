@@ -362,6 +362,71 @@ def run_miss_fetch(gen, dev, n_fetch: int = 8, steps: int = 10):
                 fetch_gbs=gbs, pcie_frac=gbs / PCIE_PEAK_GBS)
 
 
+def run_ep_share(gen, dev, ep: int = 8, per_gpu_batch: int = 64, steps: int = 20, warmup: int = 3, graphs: int = 4):
+    """One GPU's share of an expert-parallel C4 layer, the per-GPU kernel work
+    at its real shape: `ep` GPUs hold 256/ep experts each; every GPU routes its
+    own `per_gpu_batch` tokens and sends each route to the owner of its expert,
+    so GPU 0's experts see the routes of the whole global batch
+    (ep * per_gpu_batch tokens) that fall on experts [0, 256/ep).  The dispatch
+    sends each token with at least one route here once (its activations, its
+    k expert ids with -1 for the other GPUs' experts, its weights), and the
+    same decode entry point runs the received tokens over the local bank; the
+    return all-to-all and the home GPU's sum of the GPUs' partial outputs are
+    the combine.  Timed: the share's routed-expert call, replayed
+    from graphs (routing precomputed; the all-to-alls and the shared expert,
+    which runs on each token's home GPU, are not part of it)."""
+    c = C4
+    H, I, E, k = c["H"], c["I"], c["E"], c["k"]
+    e_loc = E // ep
+    B = ep * per_gpu_batch
+    bank = make_bank("fp8_block", e_loc, H, I, gen, dev)
+    bias = torch.randn((E,), generator=gen, device=dev) * 0.1
+    G = max(1, min(graphs, steps))
+    ws, ids_loc, xs, outs = [], [], [], []
+    for _ in range(G):
+        w, ids = ops.route_grouped_sigmoid(torch.randn((B, E), generator=gen, device=dev), bias, c["n_group"],
+                                           c["topk_group"], k, True, c["scale"])
+        x = torch.randn((B, H), generator=gen, device=dev).to(torch.bfloat16)
+        local = ids < e_loc  # this GPU's routes
+        tok = torch.nonzero(local.any(1))[:, 0]  # received tokens, in token order
+        ws.append(w[tok].contiguous())
+        ids_loc.append(torch.where(local[tok], ids[tok], torch.full_like(ids[tok], -1)).contiguous())
+        xs.append(x[tok].contiguous())
+        outs.append(torch.empty((int(tok.numel()), H), dtype=torch.bfloat16, device=dev))
+    for g in range(G):  # eager calls size the workspace
+        ops.experts_decode(xs[g], ws[g], ids_loc[g], bank, out=outs[g])
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=dev)
+    grs = []
+    with torch.cuda.stream(stream):
+        for g in range(G):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=stream):
+                ops.experts_decode(xs[g], ws[g], ids_loc[g], bank, out=outs[g])
+            grs.append(gr)
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        grs[i % G].replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        grs[i % G].replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    eb = expert_bytes("fp8_block", H, I)
+    us = [int(torch.unique(t[t >= 0]).numel()) for t in ids_loc]
+    routes = [int((t >= 0).sum()) for t in ids_loc]
+    tokens = [int(t.shape[0]) for t in ids_loc]
+    step_bytes = statistics.mean(us) * eb + 2 * statistics.mean(tokens) * H * 2
+    return dict(ep=ep, experts_per_gpu=e_loc, global_batch=B, per_gpu_batch=per_gpu_batch,
+                received_tokens_per_step=statistics.mean(tokens),
+                local_routes_per_step=statistics.mean(routes), local_experts_per_step=statistics.mean(us),
+                ms_per_step=ms, gbs=step_bytes / (ms * 1e-3) / 1e9, hbm_frac=step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                global_tok_s_bound=B / (ms * 1e-3))
+
+
 def run_hybrid(gen, dev, M: int = 1, n_sets: int = 4, slots: int = 8, max_fetch: int = 1, steps: int = 8,
                warmup: int = 8, fetch_fraction: float | None = None):
     """Hybrid decode at C4 shape (FP8 experts, one layer): each step routes the
@@ -870,6 +935,8 @@ def main() -> int:
         sweep["c4_prefill_offload_3x32_experts"] = run_prefill_offload(gen, dev)
         log("[bench] sweep C4 hybrid decode (1 expert fetched per step, the other misses on the CPU)")
         sweep["c4_hybrid_b1"] = run_hybrid(gen, dev, M=1)
+        log("[bench] sweep C4 expert-parallel share (EP-8: 32 experts on this GPU, 64 tokens per GPU)")
+        sweep["c4_ep8_share_b64_per_gpu"] = run_ep_share(gen, dev)
         # the reference's benched rules (moe/bench_profile.py:156-191): the fetch share from the measured
         # PCIe and CPU rates, pcie / cpu for rates taken under DRAM contention, pcie / (pcie + cpu) for
         # rates of transfers that overlap without contending; both from this run's standalone rates

@@ -426,15 +426,15 @@ __device__ __forceinline__ void dma_tail(int left, const uint8_t* ring, uint32_t
 // workgroup, two resident per CU) or 3 stages of 2 (FP8 measured against 2
 // and 4: 3 is the fastest at b = 1 and no slower at b = 8 and 64; MXFP4 keeps
 // 2 when two route chunks make a stage's registers large).
-// Passes of four route chunks (the wide kernels of large FP8 calls) keep 2
-// stages as well, so that their LDS stays at 80 KB.
-template <int FMT, int NMAT, int NCH>
+// The wide kernels of large FP8 calls (passes of up to four route chunks)
+// keep 2 stages for every pass, so that their LDS stays at 80 KB.
+template <int FMT, int NMAT, int NCH, int WIDE = 0>
 constexpr int dma_depth() {
-  return (NMAT >= 4 || NCH >= 4) ? 2 : (FMT == FMT_MXFP4 && NCH > 1) ? 2 : 3;
+  return (WIDE || NMAT >= 4 || NCH >= 4) ? 2 : (FMT == FMT_MXFP4 && NCH > 1) ? 2 : 3;
 }
 template <int FMT, int NMAT, int WIDE = 0>
-constexpr int dma_ring_bytes() {  // per wave, the larger of the NCH variants (WIDE: four-chunk passes only)
-  if constexpr (WIDE) return dma_depth<FMT, NMAT, 4>() * NMAT * kTileBytes;
+constexpr int dma_ring_bytes() {  // per wave, the larger of the NCH variants (WIDE: 2 stages for all)
+  if constexpr (WIDE) return dma_depth<FMT, NMAT, 4, 1>() * NMAT * kTileBytes;
   return (dma_depth<FMT, NMAT, 1>() > dma_depth<FMT, NMAT, 2>() ? dma_depth<FMT, NMAT, 1>()
                                                                   : dma_depth<FMT, NMAT, 2>()) *
          NMAT * kTileBytes;
@@ -513,8 +513,8 @@ constexpr int sh_per_step() {  // vector memory instructions of one sh_issue
   return 3 * NMAT + NCH * act_copies<FMT>();
 }
 template <int FMT, int NMAT, int CMAX>
-constexpr int sh_act_ring_bytes() {  // the larger of the NCH variants up to CMAX chunks per pass (4: four only)
-  if constexpr (CMAX == 4) return (dma_depth<FMT, NMAT, 4>() + 1) * act_slot_bytes<FMT, 4>();
+constexpr int sh_act_ring_bytes() {  // the larger of the NCH variants up to CMAX chunks per pass (4: wide kernels)
+  if constexpr (CMAX == 4) return (dma_depth<FMT, NMAT, 4, 1>() + 1) * act_slot_bytes<FMT, 4>();
   constexpr int one = (dma_depth<FMT, NMAT, 1>() + 1) * act_slot_bytes<FMT, 1>();
   constexpr int two = (dma_depth<FMT, NMAT, 2>() + 1) * act_slot_bytes<FMT, 2>();
   return CMAX == 1 || one > two ? one : two;
@@ -586,12 +586,12 @@ __device__ __forceinline__ void sh_tail(int left, int i, const uint8_t* ring, co
 // gemv_tile_dma for the down stage with the activations in the shared ring
 // (aring); route column col of chunk c reads activation row arow[c][...]
 // through the per-lane copy offsets avoff (kOutOfRange past the segment).
-template <int FMT, int NMAT, int NCH>
+template <int FMT, int NMAT, int NCH, int WIDE = 0>
 __device__ __forceinline__ void gemv_tile_dma_sh(const DmaTiles<NMAT>& dt, int K, int wave,
                                                  __amdgpu_buffer_rsrc_t br,
                                                  const uint32_t (&avoff)[NCH][act_copies<FMT>()], uint8_t* ring,
                                                  uint8_t* aring, f32x4 (&acc)[NMAT][NCH]) {
-  constexpr int S = dma_depth<FMT, NMAT, NCH>();
+  constexpr int S = dma_depth<FMT, NMAT, NCH, WIDE>();
   constexpr int SA = S + 1;
   constexpr int kStage = NMAT * kTileBytes;
   constexpr int kSlot = act_slot_bytes<FMT, NCH>();
@@ -796,7 +796,7 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
               avoff[c][v] = kOutOfRange;
             }
           }
-        gemv_tile_dma_sh<FMT, NMAT, NCH>(dt, K, wave, br, avoff, ring, aring, acc);
+        gemv_tile_dma_sh<FMT, NMAT, NCH, WIDE>(dt, K, wave, br, avoff, ring, aring, acc);
       } else {
         gemv_tile_dma<FMT, NMAT, NCH, KS>(dt, K, kw, br, bvoff, ring, acc);
       }
@@ -847,8 +847,8 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
 // With the activations shared through LDS (KS = 1) MXFP4 takes one chunk per
 // pass, which keeps LDS at 80 KB (two workgroups per CU).  WIDE kernels (FP8
 // calls of at least kWideMinTokens tokens, segments of up to 64 routes) run
-// every FP8 pass over four chunks, so an expert's weights are read once for
-// its 64 routes.
+// FP8 passes of up to four chunks, as many as the segment's routes need, so
+// an expert's weights are read once for its 64 routes.
 template <int FMT, int STAGE, int RT, int KS, int WIDE = 0>
 constexpr int chunks_per_pass() {
   if constexpr (WIDE && KS == 1 && FMT == FMT_FP8) return 4;
@@ -863,7 +863,11 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, const BankVi
   constexpr int CMAX = chunks_per_pass<FMT, STAGE, RT, KS, WIDE>();
   for (int base = 0; base < sv.count; base += 16 * CMAX) {
     if constexpr (CMAX == 4) {
-      decode_pass<FMT, STAGE, RT, KS, 4, WIDE>(a, bank, sv, base, row0, inter, smem, aring);
+      // as many chunks as the segment has routes left (all on the 2-stage ring)
+      const int left = sv.count - base;
+      if (left <= 16) decode_pass<FMT, STAGE, RT, KS, 1, WIDE>(a, bank, sv, base, row0, inter, smem, aring);
+      else if (left <= 32) decode_pass<FMT, STAGE, RT, KS, 2, WIDE>(a, bank, sv, base, row0, inter, smem, aring);
+      else decode_pass<FMT, STAGE, RT, KS, 4, WIDE>(a, bank, sv, base, row0, inter, smem, aring);
     } else if constexpr (CMAX == 1) {
       decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, smem, aring);
     } else {
@@ -1037,9 +1041,11 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
   const int t = idx / per_tok;
   const int h = (idx - t * per_tok) * 8;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  // routes in groups of 8: all loads of a group, ids and ic3 rows alike, are
-  // issued before the adds (the ic3 row of route r is t*k + r whatever its id;
-  // rows of skipped routes hold stale data and are dropped by the id test)
+  // routes in groups of 8: the group's ids are read, then the ic3 rows of its
+  // valid routes, all before the adds (the ic3 row of route r is t*k + r
+  // whatever its id; rows of skipped routes hold stale data and are not read,
+  // which matters where most routes are skipped: an expert-parallel share, the
+  // misses of an offload cache)
   for (int r0 = 0; r0 < k; r0 += 8) {
     u32x4 v[8];
     bool ok[8];
@@ -1048,8 +1054,11 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
       const int r = r0 + q;
       const int e = r < k ? ids[t * k + r] : -1;
       ok[q] = e >= 0 && e < num_rows;
-      const u32x4* src = reinterpret_cast<const u32x4*>(ic3 + static_cast<size_t>(t * k + r) * H + h);
-      v[q] = r >= k ? u32x4{0, 0, 0, 0} : STREAM ? __builtin_nontemporal_load(src) : *src;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(ic3 + static_cast<size_t>(t * k + r0 + q) * H + h);
+      v[q] = !ok[q] ? u32x4{0, 0, 0, 0} : STREAM ? __builtin_nontemporal_load(src) : *src;
     }
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
