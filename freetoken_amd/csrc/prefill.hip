@@ -29,8 +29,10 @@
 // and read it from HBM about once; the expert's activation rows stay hot in the
 // memory-side cache across its N tiles.  Shared-expert blocks come last.
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.h"
+#include "quant.h"
 
 namespace ftmoe {
 
@@ -39,35 +41,9 @@ constexpr int kPBN = 128;   // weight rows per tile
 constexpr int kPThreads = 256;
 
 // ----------------------------------------------------------------------------
-// Activation quantisation: one wave per row, 2 values per lane per 128-group.
-//   MODE 0: float scale s = max(amax, 1e-10) / 448, q = e4m3(clamp(x / s))
-//   MODE 1: e8m0 scale 2^ceil(log2(max(amax, 1e-4) * (1/448))), q = e4m3(x / 2^e),
-//           codes stored as uint8; MODE 2: the same with codes stored as uint32
-//           (the grouped GEMM copies them to LDS in 4-byte units)
+// Activation quantisation: one wave per row, 2 values per lane per 128-group
+// (group_scale / quant_value of quant.h).
 // ----------------------------------------------------------------------------
-// Scale of one 128-value group with absolute maximum amax, shared by the
-// quantisation kernel and the gate/up epilogue so both give identical bytes.
-// MODE 0: returns s and sets mul = 0 (values are divided by s);
-// MODE 1/2: returns the e8m0 code e+127 as a float and sets mul = 2^-e.
-template <int MODE>
-__device__ __forceinline__ float group_scale(float amax, float& mul) {
-  if (MODE == 0) {
-    mul = 0.f;
-    return fmaxf(amax, 1e-10f) / 448.0f;
-  }
-  const float t = fmaxf(amax, 1e-4f) * 0x1.24924ap-9f;  // * (1/448) rounded to float
-  const uint32_t bits = __float_as_uint(t);
-  const int e = static_cast<int>((bits >> 23) & 0xff) - 127 + ((bits & 0x7fffff) ? 1 : 0);
-  mul = ldexpf(1.0f, -e);
-  return static_cast<float>(e + 127);
-}
-
-template <int MODE>
-__device__ __forceinline__ float quant_value(float x, float s, float mul) {
-  const float y = MODE == 0 ? __fdiv_rn(x, s) : x * mul;
-  return fminf(fmaxf(y, -448.0f), 448.0f);
-}
-
 // Maximum over each 16-lane row of the wave (DPP inside the row), in every lane.
 __device__ __forceinline__ float row16_max_f32(float v) {
   v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
@@ -862,29 +838,39 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
       constexpr int QMODE = FMT == FMT_FP8 ? 0 : 2;
       uint32_t pk[8][2][2];  // bf16 pairs (v0,v1), (v2,v3) of each column tile and gate/up tile pair
       float amax[8];
+      // SiLU (every configuration here) runs as straight-line code with its
+      // kind fixed at compile time; the other kinds keep the runtime choice
+      auto swiglu = [&](auto kind) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float m = 0.f;
+        for (int i = 0; i < 8; ++i) {
+          float m = 0.f;
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          float o[4];
+          for (int s2 = 0; s2 < 2; ++s2) {
+            float o[4];
 #pragma unroll
-          for (int v4 = 0; v4 < 4; ++v4) {
-            // gate and up of one feature rounded to bf16 by one packed conversion
-            const uint32_t gu = pack_bf16x2(acc[s2][i][v4], acc[2 + s2][i][v4]);
-            o[v4] = act_apply(a.act_kind, __uint_as_float(gu << 16)) * __uint_as_float(gu & 0xffff0000u);
+            for (int v4 = 0; v4 < 4; ++v4) {
+              // gate and up of one feature rounded to bf16 by one packed conversion
+              const uint32_t gu = pack_bf16x2(acc[s2][i][v4], acc[2 + s2][i][v4]);
+              const float gg = __uint_as_float(gu << 16);
+              float act;
+              if constexpr (decltype(kind)::value == ACT_SILU) act = act_fixed<ACT_SILU>(gg);
+              else act = act_apply(a.act_kind, gg);
+              o[v4] = act * __uint_as_float(gu & 0xffff0000u);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const uint32_t p2 = pack_bf16x2(o[2 * h], o[2 * h + 1]);
+              pk[i][s2][h] = p2;
+              m = fmaxf(m, fmaxf(fabsf(__uint_as_float(p2 << 16)), fabsf(__uint_as_float(p2 & 0xffff0000u))));
+            }
           }
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const uint32_t p2 = pack_bf16x2(o[2 * h], o[2 * h + 1]);
-            pk[i][s2][h] = p2;
-            m = fmaxf(m, fmaxf(fabsf(__uint_as_float(p2 << 16)), fabsf(__uint_as_float(p2 & 0xffff0000u))));
-          }
+          m = fmaxf(m, __shfl_xor(m, 16));
+          m = fmaxf(m, __shfl_xor(m, 32));
+          amax[i] = m;
         }
-        m = fmaxf(m, __shfl_xor(m, 16));
-        m = fmaxf(m, __shfl_xor(m, 32));
-        amax[i] = m;
-      }
+      };
+      if (a.act_kind == ACT_SILU) swiglu(std::integral_constant<int, ACT_SILU>{});
+      else swiglu(std::integral_constant<int, -1>{});
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         if (g == 0) s_amax[rg * kQBM + 128 * ch + 16 * i + r16] = amax[i];
