@@ -829,7 +829,8 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
   };
 
   // ---- epilogue: lane holds rows trow + g*4 + v of route column 128ch + 16i + r16
-  auto epilogue = [&](const QTile& t, int b) {
+  // (stg: an LDS stage that no copy targets before the next tile's K loop)
+  auto epilogue = [&](const QTile& t, int b, uint8_t* stg) {
     const int n0 = n0_of(t);
     if constexpr (GATE_UP) {
       // SwiGLU, then the down GEMM's activation quantisation of this 128-feature
@@ -908,22 +909,49 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
         }
       }
     } else {
+      // A lane holds 4 consecutive output rows of a route, so direct stores
+      // write 32-byte pieces of 16 routes per instruction.  The outputs are
+      // staged in LDS instead (CT column tiles per pass, each wave in its own
+      // 128-byte-per-route area, 16-byte chunks swizzled by route so that
+      // writes and reads are conflict-free) and stored as whole 128-byte rows
+      // of this wave's 64 output rows, 8 routes per instruction: half the
+      // store instructions and a quarter of the memory requests.  N is a
+      // multiple of 128, so a wave's rows are all inside N or all past it.
+      constexpr int CT = FMT == FMT_FP8 ? 4 : 2;
+      static_assert(8 * 16 * CT * 128 <= L::kStage, "a pass's staging areas fit one stage");
+      uint8_t* const mine = stg + wave * (16 * CT * 128);
+      const int nrow0 = n0 + 64 * rg;
+      const bool rows_in = nrow0 < a.N;
+      uint16_t* const base = t.shared ? a.sh_out : a.out;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int col = 128 * ch + 16 * i + r16;
-        const int route = s_route[b][col];
-        if (route < 0) continue;
-        const float wt = s_wt[b][col];
-        uint16_t* dst = t.shared ? a.sh_out + static_cast<size_t>(route) * a.N : a.out + static_cast<size_t>(route) * a.N;
+      for (int p = 0; p < 8 / CT; ++p) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int n = n0 + trow_rel(rg, j) + g * 4;
-          if (n >= a.N) continue;
-          uint2 pk2;
-          pk2.x = pack_bf16x2(acc[j][i][0] * wt, acc[j][i][1] * wt);
-          pk2.y = pack_bf16x2(acc[j][i][2] * wt, acc[j][i][3] * wt);
-          *reinterpret_cast<uint2*>(dst + n) = pk2;
+        for (int ii = 0; ii < CT; ++ii) {
+          const int i = p * CT + ii;
+          const int c = 16 * ii + r16;  // staging row of this lane's route
+          const float wt = s_wt[b][128 * ch + 16 * i + r16];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            uint2 pk2;
+            pk2.x = pack_bf16x2(acc[j][i][0] * wt, acc[j][i][1] * wt);
+            pk2.y = pack_bf16x2(acc[j][i][2] * wt, acc[j][i][3] * wt);
+            // rows 16j + 4g .. +3 are bytes 32j + 8g of the route's 128
+            const int chunk = (2 * j + (g >> 1)) ^ (c & 7);
+            *reinterpret_cast<uint2*>(mine + c * 128 + chunk * 16 + (g & 1) * 8) = pk2;
+          }
         }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+        for (int kk = 0; kk < 2 * CT; ++kk) {
+          const int c = 8 * kk + (lane >> 3), chunk = lane & 7;
+          const u32x4 v = *reinterpret_cast<const u32x4*>(mine + c * 128 + ((chunk ^ (c & 7)) * 16));
+          const int route = s_route[b][128 * ch + 16 * (p * CT + (c >> 4)) + (c & 15)];
+          if (route >= 0 && rows_in)
+            *reinterpret_cast<u32x4*>(base + static_cast<size_t>(route) * a.N + nrow0 + 8 * chunk) = v;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       }
     }
   };
@@ -1002,7 +1030,10 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
       wait_lgkm0();
       bare_barrier();
     }
-    epilogue(cur, buf);
+    // the stage of this tile's last step: the next tile's first D steps ride
+    // in the other stages, and its step D is issued after the barrier that
+    // starts its K loop
+    epilogue(cur, buf, q_lds + ((g0 + nkb + D) % S) * L::kStage);
     if (!has_next) break;
     ahead = cross;
     cur = nxt;
