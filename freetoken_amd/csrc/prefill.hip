@@ -775,30 +775,34 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
         wcode[j] = st[L::kOffAS + R * 4 + g];
       }
     }
+    // Column tile i reads route column 128ch + 16i + r16.  The chunk swizzle
+    // depends on the column's low 3 bits (those of r16) only, so every tile's
+    // reads are one per-lane base of the step plus a compile-time offset
+    // (2048 B per tile for the codes, 64 B for the scales): no address
+    // arithmetic per tile.  The f8f6f4 MFMA reads an fp8 lane group g as
+    // K = 16g+[0,16) and 64+16g+[0,16), an fp4 lane group as the block
+    // [32g, 32g+32).
+    const int c0 = 128 * ch + r16;
+    const int q_lo = FMT == FMT_FP8 ? (2 * g) ^ swz_b<FMT>(r16) : g ^ swz_b<FMT>(r16);
+    const int q_hi = FMT == FMT_FP8 ? (2 * g + 1) ^ swz_b<FMT>(r16) : (4 + g) ^ swz_b<FMT>(r16);
+    const uint8_t* const x_lo = st + L::kOffB + c0 * 128 + q_lo * 16;
+    const uint8_t* const x_hi = st + L::kOffB + c0 * 128 + q_hi * 16;
+    const uint8_t* const x_sc = st + L::kOffBS + c0 * 4;
     auto read_x = [&](int i, i32x8& xf, uint32_t& xs) {
-      const int col = 128 * ch + 16 * i + r16;
-      const uint8_t* p = st + L::kOffB + col * 128;
-      u32x4 lo, hi;
-      if constexpr (FMT == FMT_FP8) {
-        lo = *reinterpret_cast<const u32x4*>(p + (((2 * g) ^ swz_b<FMT>(col)) * 16));
-        hi = *reinterpret_cast<const u32x4*>(p + (((2 * g + 1) ^ swz_b<FMT>(col)) * 16));
-      } else {
-        // the f8f6f4 MFMA reads an fp8 lane group g as K = 16g+[0,16) and
-        // 64+16g+[0,16), an fp4 lane group as the block [32g, 32g+32)
-        lo = *reinterpret_cast<const u32x4*>(p + ((g ^ swz_b<FMT>(col)) * 16));
-        hi = *reinterpret_cast<const u32x4*>(p + (((4 + g) ^ swz_b<FMT>(col)) * 16));
-      }
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(x_lo + 2048 * i);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(x_hi + 2048 * i);
       xf = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-      xs = *reinterpret_cast<const uint32_t*>(st + L::kOffBS + col * 4);
+      xs = *reinterpret_cast<const uint32_t*>(x_sc + 64 * i);
     };
     // The next column tile's LDS reads are issued before this tile's MFMAs.
-    // FP8: every MFMA is followed by the scale fold of the previous one; pin()
-    // keeps each fold there, so the VALU work runs while the matrix core is busy.
+    // FP8: pin() keeps each scale fold after the MFMA two places later in the
+    // stream, so the VALU work runs while the matrix core is busy.
     i32x8 xf[2];
     uint32_t xs[2];
     read_x(0, xf[0], xs[0]);
-    f32x4 tp = zero;
-    float fp = 0.f;
+    // FP8: two MFMA results in flight (tq, with their fold factors fq)
+    f32x4 tq[2] = {zero, zero};
+    float fq[2] = {0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       if (ikb >= 0) {
@@ -807,25 +811,36 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
           if (q < kPieces) issue_piece(q, ikb, istg);
       }
       if (i + 1 < 8) read_x(i + 1, xf[(i + 1) & 1], xs[(i + 1) & 1]);
+      // FP8 fold factors of this column tile: a weight scale covers 128 rows,
+      // so tiles j = 0, 1 (gate rows) share one and tiles 2, 3 (up rows)
+      // another, and the down GEMM's 64 rows of a wave share one
+      float fi[2] = {0.f, 0.f};
+      if constexpr (FMT == FMT_FP8) {
+        fi[0] = __uint_as_float(xs[i & 1]) * sw[0];
+        fi[1] = GATE_UP ? __uint_as_float(xs[i & 1]) * sw[2] : fi[0];
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         if constexpr (FMT == FMT_FP8) {
           const f32x4 t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[j], xf[i & 1], zero, 0, 0, 0, 0, 0, 0);
           const int k = 4 * i + j;
-          if (k > 0) {
-            const int pi = (k - 1) >> 2, pj = (k - 1) & 3;
-            acc[pj][pi] += tp * fp;
+          if (k >= 2) {
+            const int pi = (k - 2) >> 2, pj = (k - 2) & 3;
+            acc[pj][pi] += tq[k & 1] * fq[k & 1];
             pin(acc[pj][pi]);
           }
-          tp = t;
-          fp = __uint_as_float(xs[i & 1]) * sw[j];
+          tq[k & 1] = t;
+          fq[k & 1] = fi[j >> 1];
         } else {
           acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[j], xf[i & 1], acc[j][i], 4, 0, 0, wcode[j], 0,
                                                                        static_cast<int>(xs[i & 1]));
         }
       }
     }
-    if constexpr (FMT == FMT_FP8) acc[3][7] += tp * fp;
+    if constexpr (FMT == FMT_FP8) {
+      acc[2][7] += tq[0] * fq[0];
+      acc[3][7] += tq[1] * fq[1];
+    }
   };
 
   // ---- epilogue: lane holds rows trow + g*4 + v of route column 128ch + 16i + r16
