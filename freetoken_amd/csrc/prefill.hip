@@ -15,7 +15,11 @@
 //             scales in hardware and accumulates directly.
 //   FMT_BF16  bf16 activations and weights, v_mfma_f32_16x16x32_bf16.
 //
-// Tiling: a workgroup computes a 128 (weight rows) x 128 (routes) tile with 4 waves
+// The quantised formats (FP8, MXFP4) run prefill_qgemm_kernel, whose tiling,
+// copies and schedule are described at its section below; the rest of this
+// header describes the bf16 grouped GEMM (prefill_gemm_kernel).
+//
+// Tiling (bf16): a workgroup computes a 128 (weight rows) x 128 (routes) tile with 4 waves
 // (2 x 2), each 64 x 64 = 4 x 4 MFMA blocks.  Weights are the MFMA A operand, so a
 // lane's four accumulators are four consecutive output features of one route and
 // stores are 8-byte vectors.  K advances 128 per step; global->LDS copies of the
@@ -464,7 +468,10 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillGemmArgs
 // Gate/up: row group rg owns gate rows n0+32rg+[0,32) and up rows
 // I+n0+32rg+[0,32), so SwiGLU pairs registers; a workgroup covers 128
 // intermediate features.  Down: rows at or past N (the last tile when
-// N % 256 != 0) are read clamped to row N-1 and never stored.
+// N % 256 != 0) are read clamped to row N-1 and never stored.  The epilogues
+// are VALU work with the matrix cores idle: the gate/up epilogue quantises
+// without a division instruction (quant.h) and the down epilogue stores its
+// outputs as whole 128-byte rows through LDS.
 //
 // Schedule (map_tile_q): the active workgroups are laid out XCD-major
 // (workgroup b runs on XCD b % 8), so each XCD works through a contiguous range
