@@ -56,7 +56,7 @@ from .numerics import (
     e4m3_encode,
     log2_ceil,
     pack_nibbles,
-    silu_f32,
+    act_f32,
     unpack_nibbles,
 )
 
@@ -203,8 +203,10 @@ def _gemm(regime: str, fmt: str, x, w, s):
     return act_roundtrip_ue8m0(x) @ dequant_mxfp4(w, s).T
 
 
-def expert_mlp(regime: str, bank: Bank, e: int, x_rows, route_w=None, weight_on_input: bool = False):
-    """One expert on a set of rows: bf16(down(bf16(silu(g)*u)) * w).
+def expert_mlp(regime: str, bank: Bank, e: int, x_rows, route_w=None, weight_on_input: bool = False,
+               activation: str = "silu"):
+    """One expert on a set of rows: bf16(down(bf16(act(g)*u)) * w), act = silu
+    unless ``activation`` names gelu or gelu_tanh (``kernel/triton/activation.py:68-112``).
 
     With ``weight_on_input`` the router weight scales the gate_up output before
     its bf16 rounding instead of the down output (``MUL_ROUTED_WEIGHT`` on the
@@ -216,7 +218,7 @@ def expert_mlp(regime: str, bank: Bank, e: int, x_rows, route_w=None, weight_on_
         g = (g * np.asarray(route_w, dtype=np.float32)[:, None]).astype(np.float32)
     g = bf16_round(g)
     inter = g.shape[1] // 2
-    act = bf16_round(silu_f32(g[:, :inter]) * g[:, inter:])
+    act = bf16_round(act_f32(activation, g[:, :inter]) * g[:, inter:])
     d = _gemm(regime, bank.fmt, act, w2, s2)
     if route_w is not None and not weight_on_input:
         d = (d * np.asarray(route_w, dtype=np.float32)[:, None]).astype(np.float32)
@@ -224,7 +226,7 @@ def expert_mlp(regime: str, bank: Bank, e: int, x_rows, route_w=None, weight_on_
 
 
 def moe_layer(regime: str, x, topk_w, topk_ids, bank: Bank, shared: Bank | None = None,
-              weight_on_input: bool = False):
+              weight_on_input: bool = False, activation: str = "silu"):
     """Full MoE layer for a precomputed routing (``routed_forward``; ids index
     bank rows, ids < 0 or >= S are skipped and contribute nothing).
 
@@ -237,12 +239,12 @@ def moe_layer(regime: str, x, topk_w, topk_ids, bank: Bank, shared: Bank | None 
     ids = np.asarray(topk_ids, dtype=np.int32)
     for e in np.unique(ids[(ids >= 0) & (ids < s_rows)]):
         t, r = np.nonzero(ids == e)
-        ic3[t, r] = expert_mlp(regime, bank, int(e), x[t], topk_w[t, r], weight_on_input)
+        ic3[t, r] = expert_mlp(regime, bank, int(e), x[t], topk_w[t, r], weight_on_input, activation)
     acc = np.zeros((m, h), dtype=np.float32)
     for r in range(k):
         acc = (acc + ic3[:, r]).astype(np.float32)
     y = bf16_round(acc)
     if shared is not None:
-        sh = expert_mlp(regime, shared, 0, x)
+        sh = expert_mlp(regime, shared, 0, x, activation=activation)
         y = bf16_round(y + sh)
     return y

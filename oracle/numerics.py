@@ -203,6 +203,37 @@ def sigmoid_det(x) -> np.ndarray:
     return (F32(1.0) / (F32(1.0) + e)).astype(np.float32)
 
 
+def gelu_f32(g) -> np.ndarray:
+    """gelu(g) = g/2 (1 + erf(g / sqrt 2)) in float32 (``kernel/triton/activation.py:108-109``,
+    the erf form of gelu_and_mul); erf evaluated in float64 and rounded."""
+    from scipy.special import erf
+
+    g = np.asarray(g, dtype=np.float32)
+    e = erf(g.astype(np.float64) * 0.7071067811865476).astype(np.float32)
+    return (F32(0.5) * g * (F32(1.0) + e)).astype(np.float32)
+
+
+def gelu_tanh_f32(g) -> np.ndarray:
+    """gelu_tanh(g) = g/2 (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))) in float32
+    (``kernel/triton/activation.py:99-101``, gelu_tanh_and_mul); tanh evaluated in
+    float64 and rounded (the reference's tanh.approx is not reproduced)."""
+    g = np.asarray(g, dtype=np.float32)
+    inner = (F32(0.7978845608028654) * (g + F32(0.044715) * g * g * g)).astype(np.float32)
+    t = np.tanh(inner.astype(np.float64)).astype(np.float32)
+    return (F32(0.5) * g * (F32(1.0) + t)).astype(np.float32)
+
+
+def act_f32(kind: str, g) -> np.ndarray:
+    """The activation of an *_and_mul epilogue by name: silu, gelu or gelu_tanh."""
+    if kind == "silu":
+        return silu_f32(g)
+    if kind == "gelu":
+        return gelu_f32(g)
+    if kind == "gelu_tanh":
+        return gelu_tanh_f32(g)
+    raise ValueError(f"Unsupported activation: {kind}")
+
+
 def silu_f32(g) -> np.ndarray:
     """silu(g) = g / (1 + e^-g) in float32 (``kernel/triton/activation.py:96-98``);
     the exponential is not bit-reproducible across implementations, so every

@@ -64,6 +64,9 @@ def test_cpu_experts_activation_variants(executor):
     ys = {a: executor.run(hb, *args, activation=a).float().numpy() for a in ("silu", "gelu", "gelu_tanh")}
     assert cosine(ys["gelu"], ys["gelu_tanh"]) > 0.999  # the tanh form approximates erf
     assert not np.array_equal(ys["silu"], ys["gelu"])
+    for a, y in ys.items():  # each against the oracle's activation of that name
+        y_ref = oracle.experts.moe_layer("decode", x, w, ids, bank, activation=a)
+        assert max_rel(y, y_ref) <= MAX_REL_TOL and cosine(y, y_ref) >= COS_TOL, (a, max_rel(y, y_ref))
 
 
 def test_cpu_experts_validation(executor):

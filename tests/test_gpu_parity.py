@@ -398,3 +398,28 @@ def test_decode_all_routes_skipped(dev, M, with_shared):
     else:
         ref = oracle.experts.moe_layer("decode", x, w, ids, bank, shared)
         assert max_rel(got, ref) <= MAX_REL_TOL and cosine(got, ref) >= COS_TOL
+
+
+# The gelu forms of the *_and_mul epilogue (reference kernel/triton/activation.py:
+# 99-109): the decode epilogue evaluates the activation per value with the
+# runtime kind; bf16, FP8 and MXFP4 (with its bf16 shared expert) at one token
+# and at 33 (several route chunks).
+ACT_DECODE_CASES = [c for c in DECODE_CASES if c[0] in ("c1_bf16", "c2_fp8_reduced", "c3_mxfp4_reduced")]
+
+
+@pytest.mark.parametrize("activation", ["gelu", "gelu_tanh"])
+@pytest.mark.parametrize("case", ACT_DECODE_CASES, ids=[c[0] for c in ACT_DECODE_CASES])
+@pytest.mark.parametrize("M", [1, 33])
+def test_decode_activation_variants(dev, case, M, activation):
+    name, fmt, rows, H, I, k, sfmt, sI = case
+    bank, shared, x, w, ids = _decode_case(*case, M, seed=7)
+    y_ref = oracle.experts.moe_layer("decode", x, w, ids, bank, shared, activation=activation)
+    y = ops.experts_decode(bf16_dev(x, dev), torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev),
+                           to_device_bank(bank, dev), to_device_bank(shared, dev) if shared else None,
+                           activation=activation)
+    got = to_np(y)
+    assert max_rel(got, y_ref) <= MAX_REL_TOL, (name, M, activation, max_rel(got, y_ref))
+    assert cosine(got, y_ref) >= COS_TOL, (name, M, activation, cosine(got, y_ref))
+    # and the activation is really applied: SiLU gives a different layer
+    y_silu = oracle.experts.moe_layer("decode", x, w, ids, bank, shared)
+    assert max_rel(y_silu, y_ref) > 4 * MAX_REL_TOL

@@ -103,3 +103,20 @@ def test_decode_and_prefill_agree_on_bf16(dev):
     a = to_np(ops.experts_prefill(*args))
     b = to_np(ops.experts_decode(*args))
     assert max_rel(a, b) <= 2e-2 and cosine(a, b) >= COS_TOL
+
+
+@pytest.mark.parametrize("activation", ["gelu", "gelu_tanh"])
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "bf16"])
+def test_prefill_activation_variants(dev, fmt, activation):
+    """The gelu forms of the gate/up epilogue (reference kernel/triton/
+    activation.py:99-109), which takes the runtime-kind branch of the
+    quantised GEMMs' epilogue (SiLU has its own straight-line code)."""
+    bank, sh, x, w, ids = _prefill_case(fmt, 16, 512, 256, 300, 4, fmt != "bf16", seed=11, grouped=False)
+    y_ref = oracle.experts.moe_layer("prefill", x, w, ids, bank, sh, activation=activation)
+    y = ops.experts_prefill(bf16_dev(x, dev), torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev),
+                            to_device_bank(bank, dev), to_device_bank(sh, dev) if sh else None, activation=activation)
+    got = to_np(y)
+    assert max_rel(got, y_ref) <= MAX_REL_TOL, (fmt, activation, max_rel(got, y_ref))
+    assert cosine(got, y_ref) >= COS_TOL, (fmt, activation, cosine(got, y_ref))
+    y_silu = oracle.experts.moe_layer("prefill", x, w, ids, bank, sh)
+    assert max_rel(y_silu, y_ref) > 4 * MAX_REL_TOL

@@ -95,3 +95,46 @@ def test_sigmoid_det_accuracy_and_monotone():
     e = N.exp_det(np.linspace(-80, 80, 10001).astype(np.float32))
     er = np.exp(np.linspace(-80, 80, 10001).astype(np.float32).astype(np.float64))
     assert np.max(np.abs(e - er) / er) < 5e-7
+
+
+def test_gelu_pins():
+    """The erf gelu of the oracle (reference kernel/triton/activation.py:108-109)
+    against closed forms: gelu(x) = x Phi(x), so gelu(1) = Phi(1) and
+    gelu(-1) = Phi(1) - 1 (math.erf in float64); gelu(x) - gelu(-x) = x; the
+    saturated tails.  A 1/sqrt(2) written as sqrt(2), or a dropped 1/2, fails
+    the first two."""
+    phi1 = 0.5 * (1.0 + math.erf(1.0 / math.sqrt(2.0)))
+    g = N.gelu_f32(np.array([1.0, -1.0, 10.0, -10.0, 0.0], np.float32)).astype(np.float64)
+    assert abs(g[0] - phi1) <= 1e-7 and abs(g[1] - (phi1 - 1.0)) <= 1e-7
+    assert g[2] == 10.0 and abs(g[3]) < 1e-20 and g[4] == 0.0
+    x = np.linspace(-6, 6, 4001, dtype=np.float32)
+    d = N.gelu_f32(x).astype(np.float64) - N.gelu_f32(-x).astype(np.float64)
+    assert np.abs(d - x).max() <= 4 * np.spacing(np.float32(6.0))
+
+
+def test_gelu_tanh_pins():
+    """The tanh form (reference kernel/triton/activation.py:99-101): odd part
+    gelu_tanh(x) - gelu_tanh(-x) = x, its value at 1 from the float64 closed
+    form, and its known distance to the erf form (at most 4.8e-4 absolute on
+    [-6, 6]; a 0.044715 coefficient left out moves it to 3.4e-2)."""
+    u = math.sqrt(2.0 / math.pi) * (1.0 + 0.044715)
+    t1 = 0.5 * (1.0 + math.tanh(u))
+    assert abs(float(N.gelu_tanh_f32(np.array([1.0], np.float32))[0]) - t1) <= 1e-7
+    x = np.linspace(-6, 6, 4001, dtype=np.float32)
+    d = N.gelu_tanh_f32(x).astype(np.float64) - N.gelu_tanh_f32(-x).astype(np.float64)
+    assert np.abs(d - x).max() <= 4 * np.spacing(np.float32(6.0))
+    gap = np.abs(N.gelu_tanh_f32(x).astype(np.float64) - N.gelu_f32(x).astype(np.float64)).max()
+    assert 1e-4 < gap <= 4.8e-4, gap
+
+
+def test_act_f32_dispatch():
+    x = np.linspace(-3, 3, 13, dtype=np.float32)
+    np.testing.assert_array_equal(N.act_f32("silu", x), N.silu_f32(x))
+    np.testing.assert_array_equal(N.act_f32("gelu", x), N.gelu_f32(x))
+    np.testing.assert_array_equal(N.act_f32("gelu_tanh", x), N.gelu_tanh_f32(x))
+    try:
+        N.act_f32("swigluoai", x)
+    except ValueError:
+        pass
+    else:
+        raise AssertionError("unknown activation accepted")
