@@ -198,10 +198,11 @@ int ftmoe_version(void) { return 1; }
 
 int ftmoe_route_softmax_topk(const void* logits, int logits_dtype, int M, int E, int k, int renormalize,
                              float* topk_w, int32_t* topk_ids, ftmoe_stream_t stream) {
-  if (!logits || !topk_w || !topk_ids) return fail(FTMOE_ERR_INVALID, "route_softmax_topk: NULL pointer");
+  if (M < 0) return fail(FTMOE_ERR_INVALID, "route_softmax_topk: M=%d", M);
+  if ((!logits || !topk_w || !topk_ids) && M) return fail(FTMOE_ERR_INVALID, "route_softmax_topk: NULL pointer");
   if (logits_dtype != FTMOE_DTYPE_F32 && logits_dtype != FTMOE_DTYPE_BF16)
     return fail(FTMOE_ERR_UNSUPPORTED, "route_softmax_topk: logits dtype %d", logits_dtype);
-  if (M < 0 || E <= 0 || E > 1024 || k <= 0 || k > E || k > 64)
+  if (E <= 0 || E > 1024 || k <= 0 || k > E || k > 64)
     return fail(FTMOE_ERR_UNSUPPORTED, "route_softmax_topk: M=%d E=%d k=%d (need E<=1024, 0<k<=min(E,64))", M, E, k);
   if (M == 0) return FTMOE_OK;
   return check_hip(ftmoe::launch_softmax_topk(logits, logits_dtype == FTMOE_DTYPE_BF16, M, E, k, renormalize,
@@ -212,8 +213,10 @@ int ftmoe_route_softmax_topk(const void* logits, int logits_dtype, int M, int E,
 int ftmoe_route_grouped_sigmoid(const float* logits, const float* bias, int M, int E, int n_group, int topk_group,
                                 int k, int renormalize, float routed_scaling_factor, float* topk_w,
                                 int32_t* topk_ids, ftmoe_stream_t stream) {
-  if (!logits || !topk_w || !topk_ids) return fail(FTMOE_ERR_INVALID, "route_grouped_sigmoid: NULL pointer");
-  if (M < 0 || E <= 0 || E > 1024 || n_group <= 0 || n_group > 64 || E % n_group || topk_group <= 0 ||
+  if (M < 0) return fail(FTMOE_ERR_INVALID, "route_grouped_sigmoid: M=%d", M);
+  if ((!logits || !topk_w || !topk_ids) && M)
+    return fail(FTMOE_ERR_INVALID, "route_grouped_sigmoid: NULL pointer");
+  if (E <= 0 || E > 1024 || n_group <= 0 || n_group > 64 || E % n_group || topk_group <= 0 ||
       topk_group > n_group || k <= 0 || k > 64 || k > E / n_group * topk_group)
     return fail(FTMOE_ERR_UNSUPPORTED, "route_grouped_sigmoid: M=%d E=%d n_group=%d topk_group=%d k=%d", M, E,
                 n_group, topk_group, k);
@@ -442,8 +445,9 @@ int experts_decode_impl(const void* x, int M, int top_k, const float* topk_w, co
     if (rc) return rc;
     if (shared->hidden != bank->hidden) return fail(FTMOE_ERR_INVALID, "shared hidden %d != %d", shared->hidden, bank->hidden);
   }
+  if (M < 0 || top_k <= 0) return fail(FTMOE_ERR_INVALID, "experts_decode: M=%d top_k=%d", M, top_k);
+  if (M == 0) return FTMOE_OK;  // an empty batch: nothing to compute, no pointer is read
   if (!x || !topk_w || !topk_ids || !y) return fail(FTMOE_ERR_INVALID, "experts_decode: NULL pointer");
-  if (M <= 0 || top_k <= 0) return fail(FTMOE_ERR_INVALID, "experts_decode: M=%d top_k=%d", M, top_k);
   if (bank->num_rows > ftmoe::kSortMaxRows ||
       (bank->num_rows > ftmoe::kCountMaxRows && M * top_k > ftmoe::kSortMaxRoutes))
     return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode: num_rows %d with %d routes (rows <= %d, and routes <= %d "
@@ -575,7 +579,8 @@ int ftmoe_experts_decode_cached(const void* x, int M, int top_k, const float* to
                                 int64_t* stats, const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
                                 int apply_router_weight_on_input, void* y, void* workspace, size_t workspace_bytes,
                                 ftmoe_stream_t stream) {
-  if (!slot_for_id || !slot_ids) return fail(FTMOE_ERR_INVALID, "experts_decode_cached: NULL slot table or slot ids");
+  if (M != 0 && (!slot_for_id || !slot_ids))
+    return fail(FTMOE_ERR_INVALID, "experts_decode_cached: NULL slot table or slot ids");
   if (num_experts <= 0 || num_experts > 16384)
     return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode_cached: num_experts=%d", num_experts);
   const SlotLookup sl{slot_for_id, num_experts, slot_ids, miss_mask, stats};
@@ -588,8 +593,7 @@ int ftmoe_experts_decode_routed(const void* x, int M, int top_k, const ftmoe_rou
                                 uint8_t* miss_mask, int64_t* stats, const ftmoe_bank* bank, const ftmoe_bank* shared,
                                 int activation, int apply_router_weight_on_input, void* y, void* workspace,
                                 size_t workspace_bytes, ftmoe_stream_t stream) {
-  if (!router || !router->logits || !topk_w || !topk_ids)
-    return fail(FTMOE_ERR_INVALID, "experts_decode_routed: NULL router, logits or router outputs");
+  if (!router) return fail(FTMOE_ERR_INVALID, "experts_decode_routed: NULL router");
   const int E = router->num_experts, k = top_k;
   ftmoe::RouteArgs r{};
   r.logits = router->logits;
@@ -621,6 +625,10 @@ int ftmoe_experts_decode_routed(const void* x, int M, int top_k, const ftmoe_rou
   } else {
     return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode_routed: router kind %d", router->kind);
   }
+  if (M < 0) return fail(FTMOE_ERR_INVALID, "experts_decode_routed: M=%d", M);
+  if (M == 0) return FTMOE_OK;  // an empty batch: nothing to route or compute
+  if (!router->logits || !topk_w || !topk_ids)
+    return fail(FTMOE_ERR_INVALID, "experts_decode_routed: NULL logits or router outputs");
   if (!slot_for_id)
     return experts_decode_impl(x, M, top_k, topk_w, topk_ids, nullptr, bank, shared, activation,
                                apply_router_weight_on_input, y, workspace, workspace_bytes, stream, &r);
@@ -648,8 +656,9 @@ int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, 
     if (shared->hidden != bank->hidden || shared->inter != bank->inter || shared->format != bank->format)
       return fail(FTMOE_ERR_UNSUPPORTED, "experts_prefill: the shared expert must match the routed format and shape");
   }
+  if (M < 0 || top_k <= 0) return fail(FTMOE_ERR_INVALID, "experts_prefill: M=%d top_k=%d", M, top_k);
+  if (M == 0) return FTMOE_OK;  // an empty batch: nothing to compute, no pointer is read
   if (!x || !topk_w || !topk_ids || !y) return fail(FTMOE_ERR_INVALID, "experts_prefill: NULL pointer");
-  if (M <= 0 || top_k <= 0) return fail(FTMOE_ERR_INVALID, "experts_prefill: M=%d top_k=%d", M, top_k);
   if (bank->num_rows > 1023) return fail(FTMOE_ERR_UNSUPPORTED, "experts_prefill: num_rows %d > 1023", bank->num_rows);
   if (activation < FTMOE_ACT_SILU || activation > FTMOE_ACT_GELU_TANH)
     return fail(FTMOE_ERR_UNSUPPORTED, "experts_prefill: activation %d", activation);
@@ -796,9 +805,10 @@ size_t ftmoe_experts_decode_noalloc_capacity(void) { return kNoallocScratchBytes
 int ftmoe_experts_decode_noalloc(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
                                  const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
                                  int apply_router_weight_on_input, void* y, ftmoe_stream_t stream) {
-  if (!bank || M <= 0 || top_k <= 0)
+  if (!bank || M < 0 || top_k <= 0)
     return fail(FTMOE_ERR_INVALID, "experts_decode_noalloc: bank %p, M=%d top_k=%d", static_cast<const void*>(bank),
                 M, top_k);
+  if (M == 0) return FTMOE_OK;  // an empty batch: nothing to compute
   const size_t need = decode_layout(nullptr, M, top_k, bank, shared).bytes;
   if (need > kNoallocScratchBytes)
     return fail(FTMOE_ERR_WORKSPACE, "experts_decode_noalloc: batch %d x top-%d needs %zu bytes of scratch, beyond the "

@@ -10,7 +10,10 @@
  *   - returns FTMOE_OK (0) or a negative ftmoe_status; the message of the last
  *     failure on the calling thread is available from ftmoe_last_error();
  *   - uses fixed shapes and no host reads of device data, so it can be captured
- *     in a HIP graph.
+ *     in a HIP graph;
+ *   - takes M = 0 tokens (an empty batch, whose tensors may have NULL data
+ *     pointers) as a no-op that returns FTMOE_OK without reading any pointer
+ *     (routers and expert calls); M < 0 is FTMOE_ERR_INVALID.
  *
  * Number formats: bf16 is passed as uint16 bit patterns; fp8 is OCP e4m3fn;
  * fp4 is OCP e2m1 packed two per byte, low nibble = even k; e8m0 scale codes

@@ -400,6 +400,35 @@ def test_decode_all_routes_skipped(dev, M, with_shared):
         assert max_rel(got, ref) <= MAX_REL_TOL and cosine(got, ref) >= COS_TOL
 
 
+def test_empty_batch_through_ops(dev):
+    """Zero tokens (as a serving step with no requests hands over): every
+    router and expert call returns empty outputs without an error, and the
+    next non-empty call is unaffected."""
+    rng = np.random.default_rng(17)
+    E, H, I, k = 8, 512, 256, 4
+    bank = to_device_bank(synth.make_bank("fp8", E, H, I, rng), dev)
+    shared = to_device_bank(synth.make_bank("fp8", 1, H, I, rng), dev)
+    x0 = torch.empty((0, H), dtype=torch.bfloat16, device=dev)
+    logits0 = torch.empty((0, E), dtype=torch.float32, device=dev)
+    w0, ids0 = ops.route_softmax_topk(logits0, k, True)
+    assert w0.shape == (0, k) and ids0.shape == (0, k)
+    w1, ids1 = ops.route_grouped_sigmoid(logits0, None, 2, 1, k, True, 2.5)
+    assert w1.shape == (0, k) and ids1.shape == (0, k)
+    assert ops.experts_decode(x0, w0, ids0, bank, shared).shape == (0, H)
+    assert ops.experts_prefill(x0, w0, ids0, bank, shared).shape == (0, H)
+    slots = torch.arange(E, dtype=torch.int32, device=dev)
+    assert ops.experts_decode(x0, w0, ids0, bank, None, slot_for_id=slots).shape == (0, H)
+    for router in (ops.Router("softmax", k), ops.Router("grouped_sigmoid", k, n_group=2, topk_group=1, scale=2.5)):
+        y, w, ids = ops.experts_decode_routed(x0, logits0, router, bank, shared)
+        assert y.shape == (0, H) and w.shape == (0, k) and ids.shape == (0, k)
+    torch.cuda.synchronize(dev)
+    b, s, x, w, ids = _decode_case("empty_then", "fp8", E, H, I, k, "fp8", I, 3, seed=17)
+    y_ref = oracle.experts.moe_layer("decode", x, w, ids, b, s)
+    got = to_np(ops.experts_decode(bf16_dev(x, dev), torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev),
+                                   to_device_bank(b, dev), to_device_bank(s, dev)))
+    assert max_rel(got, y_ref) <= MAX_REL_TOL and cosine(got, y_ref) >= COS_TOL
+
+
 # The gelu forms of the *_and_mul epilogue (reference kernel/triton/activation.py:
 # 99-109): the decode epilogue evaluates the activation per value with the
 # runtime kind; bf16, FP8 and MXFP4 (with its bf16 shared expert) at one token

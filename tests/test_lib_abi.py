@@ -85,3 +85,41 @@ def test_ops_reject_cpu_tensors():
 
     with pytest.raises(ValueError):
         ops.route_softmax_topk(torch.zeros(2, 8), 2, True)
+
+
+def test_empty_batch_is_a_noop():
+    """M = 0 (empty tensors, NULL data pointers) returns OK from every router
+    and expert entry point without reading a pointer or launching; M < 0 is an
+    error.  Runs without a GPU: a launch or a dereference would fail here."""
+    L = _lib.lib()
+    w = ctypes.c_void_p(16)
+    bank = _lib.FtmoeBank(_lib.FMT_FP8_B128, 8, 256, 256, 16, 16, 16, 16)
+    bp = ctypes.byref(bank)
+    shared = _lib.FtmoeBank(_lib.FMT_FP8_B128, 1, 256, 256, 16, 16, 16, 16)
+    sp = ctypes.byref(shared)
+    assert L.ftmoe_route_softmax_topk(None, _lib.DTYPE_F32, 0, 64, 8, 1, None, None, None) == 0
+    assert L.ftmoe_route_grouped_sigmoid(None, None, 0, 256, 8, 4, 8, 1, 2.5, None, None, None) == 0
+    assert L.ftmoe_experts_decode(None, 0, 8, None, None, bp, sp, 0, 0, None, None, 0, None) == 0
+    assert L.ftmoe_experts_decode_noalloc(None, 0, 8, None, None, bp, None, 0, 0, None, None) == 0
+    assert L.ftmoe_experts_prefill(None, 0, 8, None, None, bp, sp, 0, None, None, 0, None) == 0
+    assert L.ftmoe_experts_decode_cached(None, 0, 8, None, None, None, 64, None, None, None, bp, None, 0, 0, None,
+                                         None, 0, None) == 0
+    for kind in (_lib.ROUTER_SOFTMAX_TOPK, _lib.ROUTER_GROUPED_SIGMOID):
+        r = _lib.FtmoeRouter(kind, None, _lib.DTYPE_F32, 8, 1, None, 1, 1, 1.0)
+        assert L.ftmoe_experts_decode_routed(None, 0, 8, ctypes.byref(r), None, None, None, 0, None, None, None, bp,
+                                             None, 0, 0, None, None, 0, None) == 0
+    assert L.ftmoe_experts_decode_workspace(0, 8, bp, None) == 0
+    assert L.ftmoe_experts_prefill_workspace(0, 8, bp, None) == 0
+    # negative sizes and invalid configurations still fail with M = 0
+    assert L.ftmoe_route_softmax_topk(w, _lib.DTYPE_F32, -1, 64, 8, 1, w, w, None) == _lib.FTMOE_ERR_INVALID
+    assert L.ftmoe_route_softmax_topk(None, _lib.DTYPE_F32, 0, 64, 80, 1, None, None, None) == _lib.FTMOE_ERR_UNSUPPORTED
+    assert L.ftmoe_experts_decode(w, -1, 8, w, w, bp, None, 0, 0, w, w, 1 << 20, None) == _lib.FTMOE_ERR_INVALID
+    assert L.ftmoe_experts_prefill(w, -1, 8, w, w, bp, None, 0, w, w, 1 << 20, None) == _lib.FTMOE_ERR_INVALID
+    assert L.ftmoe_experts_decode_noalloc(w, -1, 8, w, w, bp, None, 0, 0, w, None) == _lib.FTMOE_ERR_INVALID
+    assert L.ftmoe_experts_decode(None, 0, 0, None, None, bp, None, 0, 0, None, None, 0, None) == _lib.FTMOE_ERR_INVALID
+    bad = _lib.FtmoeBank(_lib.FMT_FP8_B128, 8, 1000, 256, 16, None, 16, None)
+    assert L.ftmoe_experts_decode(None, 0, 8, None, None, ctypes.byref(bad), None, 0, 0, None, None, 0,
+                                  None) == _lib.FTMOE_ERR_UNSUPPORTED
+    r = _lib.FtmoeRouter(7, None, _lib.DTYPE_F32, 8, 1, None, 1, 1, 1.0)
+    assert L.ftmoe_experts_decode_routed(None, 0, 8, ctypes.byref(r), None, None, None, 0, None, None, None, bp, None,
+                                         0, 0, None, None, 0, None) == _lib.FTMOE_ERR_UNSUPPORTED
