@@ -291,9 +291,9 @@ template <int FMT>
 constexpr int dma_pieces() {  // activation loads (16 bytes) per chunk and step
   return FMT == FMT_FP8 ? 4 : 8;
 }
-template <int FMT, int NMAT, int NCH>
-constexpr int dma_per_step() {  // vector memory instructions of one dma_issue
-  return 3 * NMAT + dma_pieces<FMT>() * NCH;
+template <int FMT, int NMAT, int NCH, bool CT = false>
+constexpr int dma_per_step() {  // vector memory instructions of one dma_issue (CT: codes from the LDS table)
+  return (CT ? 2 : 3) * NMAT + dma_pieces<FMT>() * NCH;
 }
 
 // Per-step side data of a tile: FP8 the 128x128 block scale (wave-uniform);
@@ -322,7 +322,11 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds
                                            kNtPolicy);
 }
 
-template <int FMT, int NMAT, int NCH>
+__device__ __forceinline__ void lds_dma16_cached(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+template <int FMT, int NMAT, int NCH, bool CT = false>
 __device__ __forceinline__ void dma_issue(const DmaTiles<NMAT>& dt, __amdgpu_buffer_rsrc_t br,
                                           const uint32_t (&bvoff)[NCH], uint8_t* stage, int step, uint32_t dead,
                                           u32x4 (&b)[NCH][dma_pieces<FMT>()], DmaSide<FMT> (&side)[NMAT]) {
@@ -331,12 +335,14 @@ __device__ __forceinline__ void dma_issue(const DmaTiles<NMAT>& dt, __amdgpu_buf
   for (int m = 0; m < NMAT; ++m)
 #pragma unroll
     for (int h = 0; h < 2; ++h) lds_dma16(dt.wr, stage + m * kTileBytes + h * 1024, dt.voff[m][h] | dead, so);
+  if constexpr (!CT) {
 #pragma unroll
-  for (int m = 0; m < NMAT; ++m) {
-    if constexpr (FMT == FMT_FP8)
-      side[m].s = buf_f32(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(step) * 4);
-    else
-      side[m].codes = buf_x2(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(step) * 8);
+    for (int m = 0; m < NMAT; ++m) {
+      if constexpr (FMT == FMT_FP8)
+        side[m].s = buf_f32(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(step) * 4);
+      else
+        side[m].codes = buf_x2(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(step) * 8);
+    }
   }
   const uint32_t sb = static_cast<uint32_t>(step) * dma_kstep<FMT>() * 2;
 #pragma unroll
@@ -407,17 +413,69 @@ __device__ __forceinline__ void dma_compute(const uint8_t* stage, uint32_t rd0, 
   }
 }
 
+// MXFP4 with a K split (the gate_up stage): the e8m0 codes of the workgroup's
+// NMAT tiles (16 rows each, K/32 bytes per row) are copied into LDS once per
+// pass, a few 1 KB DMA instructions per wave, instead of one 8-byte load per
+// tile and step whose 64 lanes gather from 16 rows.  Measured on C3 and C4
+// shapes: those per-step loads cost 18% of the MXFP4 gate_up stage.  Each
+// wave reads its codes for step st from LDS: row r of tile m at
+// (16 m + r) * K/32 + 8 st, the same two words the per-step load returned.
+constexpr int kCodeTableBytes = 16384;
+template <int NMAT>
+__device__ __forceinline__ bool code_table_fits(int K) {
+  return K % 512 == 0 && NMAT * 16 * (K / 32) <= kCodeTableBytes;
+}
+
+// Copies the table (NMAT * 16 rows of K/32 bytes) into ctab.  The tiles are
+// the gate_up stage's: table rows [0, 16 RT) are weight rows wrow0.. (gate),
+// the next 16 RT rows are inter + wrow0.. (up).  Instruction q of the
+// workgroup covers table bytes [1024 q, 1024 q + 1024) and is issued by wave
+// q % kDecWaves; lanes past the table read zeros (the region is
+// kCodeTableBytes long).  The row is computed, not looked up, so that no
+// per-lane index reaches memory.
+template <int RT>
+__device__ __forceinline__ void code_table_fill(__amdgpu_buffer_rsrc_t sr, int K, int wrow0, int inter, int wave,
+                                                uint8_t* ctab) {
+  const int rb = K / 32, bytes = 2 * RT * 16 * rb, lane = lane_id();
+  for (int q = wave; q * 1024 < bytes; q += kDecWaves) {
+    const int b = q * 1024 + lane * 16;
+    uint32_t src = kOutOfRange;
+    if (b < bytes) {
+      const int row = b / rb, off = b - row * rb;
+      const int grow = row < 16 * RT ? wrow0 + row : inter + wrow0 + row - 16 * RT;
+      src = static_cast<uint32_t>(grow) * rb + off;
+    }
+    lds_dma16_cached(sr, ctab + q * 1024, src, 0);
+  }
+}
+
+// The codes of step st for the lane's row of each tile (ctl: the lane's row
+// r16 of tile 0; ctile: bytes per tile, 16 * K/32).
+template <int NMAT>
+__device__ __forceinline__ void code_table_side(const uint8_t* __restrict__ ctl, uint32_t ctile, int st,
+                                                DmaSide<FMT_MXFP4> (&sd)[NMAT]) {
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m) sd[m].codes = *reinterpret_cast<const uint2*>(ctl + m * ctile + 8 * st);
+}
+
 // Computes the stages T.. of the last `left` steps of a ring of S stages,
 // waiting for each stage alone (the S-2-T stages behind it stay in flight).
-template <int FMT, int S, int T, int NMAT, int NCH>
+template <int FMT, int S, int T, int NMAT, int NCH, bool CT = false>
 __device__ __forceinline__ void dma_tail(int left, const uint8_t* ring, uint32_t rd0, uint32_t rd1, int gsh,
                                          const u32x4 (&b)[S][NCH][dma_pieces<FMT>()],
-                                         const DmaSide<FMT> (&side)[S][NMAT], f32x4 (&acc)[NMAT][NCH]) {
+                                         const DmaSide<FMT> (&side)[S][NMAT], f32x4 (&acc)[NMAT][NCH],
+                                         const uint8_t* ctl = nullptr, uint32_t ctile = 0, int st0 = 0) {
   if constexpr (T < S - 1) {
     if (left > T) {
-      wait_vmcnt<(S - 2 - T) * dma_per_step<FMT, NMAT, NCH>()>();
-      dma_compute<FMT, NMAT, NCH>(ring + T * NMAT * kTileBytes, rd0, rd1, gsh, b[T], side[T], acc);
-      dma_tail<FMT, S, T + 1, NMAT, NCH>(left, ring, rd0, rd1, gsh, b, side, acc);
+      wait_vmcnt<(S - 2 - T) * dma_per_step<FMT, NMAT, NCH, CT>()>();
+      if constexpr (CT) {
+        DmaSide<FMT> sd[NMAT];
+        code_table_side<NMAT>(ctl, ctile, st0 + T, sd);
+        dma_compute<FMT, NMAT, NCH>(ring + T * NMAT * kTileBytes, rd0, rd1, gsh, b[T], sd, acc);
+      } else {
+        dma_compute<FMT, NMAT, NCH>(ring + T * NMAT * kTileBytes, rd0, rd1, gsh, b[T], side[T], acc);
+      }
+      dma_tail<FMT, S, T + 1, NMAT, NCH, CT>(left, ring, rd0, rd1, gsh, b, side, acc, ctl, ctile, st0);
     }
   }
 }
@@ -444,10 +502,13 @@ constexpr int dma_ring_bytes() {  // per wave, the larger of the NCH variants (W
 // accumulation order, the weights through the wave's LDS ring of S stages (the
 // DMA of the next S-1 steps is in flight while one is computed; a dead step
 // still issues, reading zeros, so every step's wait count is exact).
-template <int FMT, int NMAT, int NCH, int KS>
+template <int FMT, int NMAT, int NCH, int KS, bool CT = false>
 __device__ __forceinline__ void gemv_tile_dma(const DmaTiles<NMAT>& dt, int K, int kw, __amdgpu_buffer_rsrc_t br,
                                               const uint32_t (&bvoff)[NCH], uint8_t* ring,
-                                              f32x4 (&acc)[NMAT][NCH]) {
+                                              f32x4 (&acc)[NMAT][NCH], uint8_t* ctab = nullptr, int wrow0 = 0,
+                                              int inter = 0) {
+  static_assert(!CT || (FMT == FMT_MXFP4 && KS == kDecWaves && NMAT % 2 == 0),
+                "the code table serves the MXFP4 gate_up stage with one row group");
   constexpr int S = dma_depth<FMT, NMAT, NCH>();
   constexpr int P = dma_pieces<FMT>();
   constexpr int kStage = NMAT * kTileBytes;
@@ -464,25 +525,47 @@ __device__ __forceinline__ void gemv_tile_dma(const DmaTiles<NMAT>& dt, int K, i
 #pragma unroll
     for (int c = 0; c < NCH; ++c) acc[m][c] = zero;
   u32x4 b[S][NCH][P];
-  DmaSide<FMT> side[S][NMAT];
+  DmaSide<FMT> side[S][NMAT];  // unused with the code table
+  const uint32_t ctile = 16 * static_cast<uint32_t>(K / 32);
+  const uint8_t* ctl = ctab + r16 * (K / 32);
+  if constexpr (CT) code_table_fill<NMAT / 2>(dt.sr, K, wrow0, inter, kw, ctab);
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
-    dma_issue<FMT, NMAT, NCH>(dt, br, bvoff, ring + s * kStage, st_lo + s, s < n ? 0u : kOutOfRange, b[s], side[s]);
+    dma_issue<FMT, NMAT, NCH, CT>(dt, br, bvoff, ring + s * kStage, st_lo + s, s < n ? 0u : kOutOfRange, b[s],
+                                  side[s]);
+  DmaSide<FMT> nx[NMAT];  // the code table: codes of the next step
+  if constexpr (CT) {
+    // the table copies were issued first: wait for them alone, then make
+    // every wave's copies visible
+    wait_vmcnt<(S - 1) * dma_per_step<FMT, NMAT, NCH, CT>()>();
+    bare_barrier_dec();
+    code_table_side<NMAT>(ctl, ctile, st_lo, nx);
+  }
   int i = 0;
   for (; i + S <= n; i += S) {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       const int ahead = i + s + S - 1;
-      dma_issue<FMT, NMAT, NCH>(dt, br, bvoff, ring + ((s + S - 1) % S) * kStage, st_lo + ahead,
-                                ahead < n ? 0u : kOutOfRange, b[(s + S - 1) % S], side[(s + S - 1) % S]);
-      wait_vmcnt<(S - 1) * dma_per_step<FMT, NMAT, NCH>()>();
+      dma_issue<FMT, NMAT, NCH, CT>(dt, br, bvoff, ring + ((s + S - 1) % S) * kStage, st_lo + ahead,
+                                    ahead < n ? 0u : kOutOfRange, b[(s + S - 1) % S], side[(s + S - 1) % S]);
+      wait_vmcnt<(S - 1) * dma_per_step<FMT, NMAT, NCH, CT>()>();
       __builtin_amdgcn_sched_barrier(0);
-      dma_compute<FMT, NMAT, NCH>(ring + s * kStage, rd0, rd1, gsh, b[s], side[s], acc);
+      if constexpr (CT) {
+        // this step's codes were read during the previous one; read the next
+        // step's now (the scheduling barriers keep them in this step)
+        DmaSide<FMT> sd[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) sd[m] = nx[m];
+        code_table_side<NMAT>(ctl, ctile, min(st_lo + i + s + 1, st_hi - 1), nx);
+        dma_compute<FMT, NMAT, NCH>(ring + s * kStage, rd0, rd1, gsh, b[s], sd, acc);
+      } else {
+        dma_compute<FMT, NMAT, NCH>(ring + s * kStage, rd0, rd1, gsh, b[s], side[s], acc);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
   // the last n - i < S steps sit in stages 0.. (loaded above)
-  dma_tail<FMT, S, 0, NMAT, NCH>(n - i, ring, rd0, rd1, gsh, b, side, acc);
+  dma_tail<FMT, S, 0, NMAT, NCH, CT>(n - i, ring, rd0, rd1, gsh, b, side, acc, ctl, ctile, st_lo + i);
 }
 
 // ---- Down stage: activations shared through LDS ----------------------------
@@ -520,9 +603,6 @@ constexpr int sh_act_ring_bytes() {  // the larger of the NCH variants up to CMA
   return CMAX == 1 || one > two ? one : two;
 }
 
-__device__ __forceinline__ void lds_dma16_cached(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
-}
 
 template <int FMT, int NMAT, int NCH>
 __device__ __forceinline__ void sh_issue(const DmaTiles<NMAT>& dt, __amdgpu_buffer_rsrc_t br,
@@ -798,7 +878,13 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
           }
         gemv_tile_dma_sh<FMT, NMAT, NCH, WIDE>(dt, K, wave, br, avoff, ring, aring, acc);
       } else {
-        gemv_tile_dma<FMT, NMAT, NCH, KS>(dt, K, kw, br, bvoff, ring, acc);
+        if constexpr (FMT == FMT_MXFP4 && KS == kDecWaves && STAGE == 0) {
+          // aring: the code table's LDS, behind the waves' rings
+          if (code_table_fits<NMAT>(K)) gemv_tile_dma<FMT, NMAT, NCH, KS, true>(dt, K, kw, br, bvoff, ring, acc, aring, wrow0, inter);
+          else gemv_tile_dma<FMT, NMAT, NCH, KS>(dt, K, kw, br, bvoff, ring, acc);
+        } else {
+          gemv_tile_dma<FMT, NMAT, NCH, KS>(dt, K, kw, br, bvoff, ring, acc);
+        }
       }
     }
   } else {
@@ -902,8 +988,11 @@ struct StageSmem {
           ? sh_act_ring_bytes<FMT_MXFP4, kNmat, chunks_per_pass<FMT_MXFP4, STAGE, RT, KS>()>()
           : 0;
   static constexpr int kAct = kActF8 > kActF4 ? kActF8 : kActF4;
+  // MXFP4 with a K split: the e8m0 code table of the workgroup's tiles
+  static constexpr int kCodes = (KS == kDecWaves && (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4)) ? kCodeTableBytes : 0;
   static constexpr int kRed = KS > 1 ? kRedFloats4 * 16 : 0;
-  static constexpr int kSmem = kRing + kAct > kRed ? kRing + kAct : kRed > 16 ? kRed : 16;
+  static constexpr int kSmem =
+      kRing + kAct + kCodes > kRed ? kRing + kAct + kCodes : kRed > 16 ? kRed : 16;
 };
 
 // One workgroup of the stage grid: row block bx of segment seg, the first n_sh
