@@ -591,9 +591,9 @@ template <int FMT, int NCH>
 constexpr int act_slot_bytes() {
   return NCH * 16 * act_col_bytes<FMT>();
 }
-template <int FMT, int NMAT, int NCH>
-constexpr int sh_per_step() {  // vector memory instructions of one sh_issue
-  return 3 * NMAT + NCH * act_copies<FMT>();
+template <int FMT, int NMAT, int NCH, bool CR = false>
+constexpr int sh_per_step() {  // vector memory instructions of one sh_issue (CR: codes in registers)
+  return (CR ? 2 : 3) * NMAT + NCH * act_copies<FMT>();
 }
 template <int FMT, int NMAT, int CMAX>
 constexpr int sh_act_ring_bytes() {  // the larger of the NCH variants up to CMAX chunks per pass (4: wide kernels)
@@ -604,7 +604,7 @@ constexpr int sh_act_ring_bytes() {  // the larger of the NCH variants up to CMA
 }
 
 
-template <int FMT, int NMAT, int NCH>
+template <int FMT, int NMAT, int NCH, bool CR = false>
 __device__ __forceinline__ void sh_issue(const DmaTiles<NMAT>& dt, __amdgpu_buffer_rsrc_t br,
                                          const uint32_t (&avoff)[NCH][act_copies<FMT>()], uint8_t* wstage,
                                          uint8_t* aslot, int wave, int step, uint32_t dead,
@@ -615,12 +615,14 @@ __device__ __forceinline__ void sh_issue(const DmaTiles<NMAT>& dt, __amdgpu_buff
   for (int m = 0; m < NMAT; ++m)
 #pragma unroll
     for (int h = 0; h < 2; ++h) lds_dma16(dt.wr, wstage + m * kTileBytes + h * 1024, dt.voff[m][h] | dead, so);
+  if constexpr (!CR) {
 #pragma unroll
-  for (int m = 0; m < NMAT; ++m) {
-    if constexpr (FMT == FMT_FP8)
-      side[m].s = buf_f32(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(step) * 4);
-    else
-      side[m].codes = buf_x2(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(step) * 8);
+    for (int m = 0; m < NMAT; ++m) {
+      if constexpr (FMT == FMT_FP8)
+        side[m].s = buf_f32(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(step) * 4);
+      else
+        side[m].codes = buf_x2(dt.sr, dt.soff[m] | dead, static_cast<uint32_t>(step) * 8);
+    }
   }
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
@@ -648,17 +650,42 @@ __device__ __forceinline__ void sh_compute(const uint8_t* wstage, const uint8_t*
   dma_compute<FMT, NMAT, NCH>(wstage, rd0, rd1, 8 * g, b, side, acc);
 }
 
-template <int FMT, int S, int SA, int T, int NMAT, int NCH>
+// MXFP4 down stage (no K split) of at most 8 K steps: the lane's row of e8m0
+// codes lives in registers, 16 bytes per lane group (those of steps 2g and
+// 2g + 1), loaded once per pass instead of one gathered 8-byte load per tile
+// and step; step st takes its two words from lane group st / 2 by a lane
+// permutation (no memory access).
+constexpr int kCodeRegSteps = 8;
+template <int NMAT>
+__device__ __forceinline__ void code_regs_side(const u32x4 (&cr)[NMAT], int r16, int st,
+                                               DmaSide<FMT_MXFP4> (&sd)[NMAT]) {
+  const int src = (r16 + 16 * (st >> 1)) * 4;
+  const bool hi = (st & 1) != 0;
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m) {
+    sd[m].codes.x = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(hi ? cr[m][2] : cr[m][0])));
+    sd[m].codes.y = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(hi ? cr[m][3] : cr[m][1])));
+  }
+}
+
+template <int FMT, int S, int SA, int T, int NMAT, int NCH, bool CR = false>
 __device__ __forceinline__ void sh_tail(int left, int i, const uint8_t* ring, const uint8_t* aring, uint32_t rd0,
                                         uint32_t rd1, int r16, int g, const DmaSide<FMT> (&side)[S][NMAT],
-                                        f32x4 (&acc)[NMAT][NCH]) {
+                                        f32x4 (&acc)[NMAT][NCH], const u32x4 (&cr)[NMAT]) {
   if constexpr (T < S - 1) {
     if (left > T) {
-      wait_vmcnt<(S - 2 - T) * sh_per_step<FMT, NMAT, NCH>()>();
+      wait_vmcnt<(S - 2 - T) * sh_per_step<FMT, NMAT, NCH, CR>()>();
       bare_barrier_dec();
-      sh_compute<FMT, NMAT, NCH>(ring + T * NMAT * kTileBytes, aring + ((i + T) % SA) * act_slot_bytes<FMT, NCH>(),
-                                 rd0, rd1, r16, g, side[T], acc);
-      sh_tail<FMT, S, SA, T + 1, NMAT, NCH>(left, i, ring, aring, rd0, rd1, r16, g, side, acc);
+      if constexpr (CR) {
+        DmaSide<FMT> sd[NMAT];
+        code_regs_side<NMAT>(cr, r16, i + T, sd);
+        sh_compute<FMT, NMAT, NCH>(ring + T * NMAT * kTileBytes, aring + ((i + T) % SA) * act_slot_bytes<FMT, NCH>(),
+                                   rd0, rd1, r16, g, sd, acc);
+      } else {
+        sh_compute<FMT, NMAT, NCH>(ring + T * NMAT * kTileBytes, aring + ((i + T) % SA) * act_slot_bytes<FMT, NCH>(),
+                                   rd0, rd1, r16, g, side[T], acc);
+      }
+      sh_tail<FMT, S, SA, T + 1, NMAT, NCH, CR>(left, i, ring, aring, rd0, rd1, r16, g, side, acc, cr);
     }
   }
 }
@@ -666,11 +693,12 @@ __device__ __forceinline__ void sh_tail(int left, int i, const uint8_t* ring, co
 // gemv_tile_dma for the down stage with the activations in the shared ring
 // (aring); route column col of chunk c reads activation row arow[c][...]
 // through the per-lane copy offsets avoff (kOutOfRange past the segment).
-template <int FMT, int NMAT, int NCH, int WIDE = 0>
+template <int FMT, int NMAT, int NCH, int WIDE = 0, bool CR = false>
 __device__ __forceinline__ void gemv_tile_dma_sh(const DmaTiles<NMAT>& dt, int K, int wave,
                                                  __amdgpu_buffer_rsrc_t br,
                                                  const uint32_t (&avoff)[NCH][act_copies<FMT>()], uint8_t* ring,
                                                  uint8_t* aring, f32x4 (&acc)[NMAT][NCH]) {
+  static_assert(!CR || FMT == FMT_MXFP4, "codes in registers: MXFP4 only");
   constexpr int S = dma_depth<FMT, NMAT, NCH, WIDE>();
   constexpr int SA = S + 1;
   constexpr int kStage = NMAT * kTileBytes;
@@ -684,27 +712,47 @@ __device__ __forceinline__ void gemv_tile_dma_sh(const DmaTiles<NMAT>& dt, int K
   for (int m = 0; m < NMAT; ++m)
 #pragma unroll
     for (int c = 0; c < NCH; ++c) acc[m][c] = zero;
-  DmaSide<FMT> side[S][NMAT];
+  DmaSide<FMT> side[S][NMAT];  // unused with the codes in registers
+  u32x4 cr[NMAT];
+  DmaSide<FMT> nx[NMAT];  // codes in registers: those of the next step
+  if constexpr (CR) {
+    // issued before the first step's copies: its wait covers them
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) cr[m] = buf_x4(dt.sr, dt.soff[m] + 16 * g, 0);
+  }
   bare_barrier_dec();  // the previous pass's last slots have been read by every wave
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
-    sh_issue<FMT, NMAT, NCH>(dt, br, avoff, ring + s * kStage, aring + s * kSlot, wave, s, s < n ? 0u : kOutOfRange,
-                             side[s]);
+    sh_issue<FMT, NMAT, NCH, CR>(dt, br, avoff, ring + s * kStage, aring + s * kSlot, wave, s,
+                                 s < n ? 0u : kOutOfRange, side[s]);
   int i = 0;
   for (; i + S <= n; i += S) {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       const int t = i + s, ahead = t + S - 1;
-      sh_issue<FMT, NMAT, NCH>(dt, br, avoff, ring + ((s + S - 1) % S) * kStage, aring + (ahead % SA) * kSlot, wave,
-                               ahead, ahead < n ? 0u : kOutOfRange, side[(s + S - 1) % S]);
-      wait_vmcnt<(S - 1) * sh_per_step<FMT, NMAT, NCH>()>();
+      sh_issue<FMT, NMAT, NCH, CR>(dt, br, avoff, ring + ((s + S - 1) % S) * kStage, aring + (ahead % SA) * kSlot,
+                                   wave, ahead, ahead < n ? 0u : kOutOfRange, side[(s + S - 1) % S]);
+      wait_vmcnt<(S - 1) * sh_per_step<FMT, NMAT, NCH, CR>()>();
       bare_barrier_dec();  // every wave's copies of step t have landed
       __builtin_amdgcn_sched_barrier(0);
-      sh_compute<FMT, NMAT, NCH>(ring + s * kStage, aring + (t % SA) * kSlot, rd0, rd1, r16, g, side[s], acc);
+      if constexpr (CR) {
+        DmaSide<FMT> sd[NMAT];
+        if (t == 0) {
+          code_regs_side<NMAT>(cr, r16, 0, sd);
+        } else {
+#pragma unroll
+          for (int m = 0; m < NMAT; ++m) sd[m] = nx[m];
+        }
+        // the next step's codes, permuted while this step computes
+        code_regs_side<NMAT>(cr, r16, t + 1, nx);
+        sh_compute<FMT, NMAT, NCH>(ring + s * kStage, aring + (t % SA) * kSlot, rd0, rd1, r16, g, sd, acc);
+      } else {
+        sh_compute<FMT, NMAT, NCH>(ring + s * kStage, aring + (t % SA) * kSlot, rd0, rd1, r16, g, side[s], acc);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  sh_tail<FMT, S, SA, 0, NMAT, NCH>(n - i, i, ring, aring, rd0, rd1, r16, g, side, acc);
+  sh_tail<FMT, S, SA, 0, NMAT, NCH, CR>(n - i, i, ring, aring, rd0, rd1, r16, g, side, acc, cr);
 }
 
 // Where a segment's column lives.  Routed segments: column col is route
@@ -876,7 +924,14 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
               avoff[c][v] = kOutOfRange;
             }
           }
-        gemv_tile_dma_sh<FMT, NMAT, NCH, WIDE>(dt, K, wave, br, avoff, ring, aring, acc);
+        if constexpr (FMT == FMT_MXFP4) {
+          if (K <= kCodeRegSteps * dma_kstep<FMT>())
+            gemv_tile_dma_sh<FMT, NMAT, NCH, WIDE, true>(dt, K, wave, br, avoff, ring, aring, acc);
+          else
+            gemv_tile_dma_sh<FMT, NMAT, NCH, WIDE>(dt, K, wave, br, avoff, ring, aring, acc);
+        } else {
+          gemv_tile_dma_sh<FMT, NMAT, NCH, WIDE>(dt, K, wave, br, avoff, ring, aring, acc);
+        }
       } else {
         if constexpr (FMT == FMT_MXFP4 && KS == kDecWaves && STAGE == 0) {
           // aring: the code table's LDS, behind the waves' rings
