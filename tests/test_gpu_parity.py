@@ -208,6 +208,27 @@ def test_decode_parity_full_shapes(dev, case, M):
     assert cosine(got, y_ref) >= COS_TOL, (name, M, cosine(got, y_ref))
 
 
+# MXFP4 decode by shape: the gate_up stage's LDS code table (H a multiple of
+# 512: 2, 4, 6 or 8 K steps of 256 split over the 4 waves, so at H = 512 two
+# waves have no step and at H = 1536 the waves have 1 or 2) and the down
+# stage's codes in registers (I a multiple of 256 up to 2048: 1, 2, 3 and 8 K
+# steps), with one or two route chunks per pass and several passes or
+# segments per expert (M = 200: 67 routes per expert).
+MX_SHAPE_CASES = [(512, 256), (1024, 768), (1536, 512), (2048, 2048)]
+
+
+@pytest.mark.parametrize("H,I", MX_SHAPE_CASES, ids=[f"H{h}_I{i}" for h, i in MX_SHAPE_CASES])
+@pytest.mark.parametrize("M", [1, 24, 90, 200])
+def test_decode_mxfp4_code_paths(dev, H, I, M):
+    bank, shared, x, w, ids = _decode_case("mx", "mxfp4", 12, H, I, 4, "bf16", I, M, seed=3)
+    y_ref = oracle.experts.moe_layer("decode", x, w, ids, bank, shared)
+    y = ops.experts_decode(bf16_dev(x, dev), torch.from_numpy(w).to(dev), torch.from_numpy(ids).to(dev),
+                           to_device_bank(bank, dev), to_device_bank(shared, dev))
+    got = to_np(y)
+    assert max_rel(got, y_ref) <= MAX_REL_TOL, (H, I, M, max_rel(got, y_ref))
+    assert cosine(got, y_ref) >= COS_TOL, (H, I, M, cosine(got, y_ref))
+
+
 def test_decode_skips_and_weight_on_input(dev):
     bank, shared, x, w, ids = _decode_case(*DECODE_CASES[0], 8, seed=5)
     ids[0, 1] = -1
