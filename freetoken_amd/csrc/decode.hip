@@ -450,7 +450,10 @@ __device__ __forceinline__ void code_table_fill(__amdgpu_buffer_rsrc_t sr, int K
 }
 
 // The codes of step st for the lane's row of each tile (ctl: the lane's row
-// r16 of tile 0; ctile: bytes per tile, 16 * K/32).
+// r16 of tile 0; ctile: bytes per tile, 16 * K/32).  ctl is __restrict__: with
+// that alias information the compiler does not make these reads wait for the
+// weight copies (LDS DMA) in flight, which without it it must assume may
+// write the same LDS.
 template <int NMAT>
 __device__ __forceinline__ void code_table_side(const uint8_t* __restrict__ ctl, uint32_t ctile, int st,
                                                 DmaSide<FMT_MXFP4> (&sd)[NMAT]) {
