@@ -317,16 +317,20 @@ struct DmaTiles {
   uint32_t soff[NMAT];     // FP8: tile's scale row (wave-uniform); MXFP4: lane's code row
 };
 
+// CW: the weights are read more than once by nearby workgroups (the shared
+// expert's token pieces): the default policy instead of the nontemporal one,
+// so that the later readers find the lines in L2.
+template <bool CW = false>
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0,
-                                           kNtPolicy);
+                                           CW ? 0 : kNtPolicy);
 }
 
 __device__ __forceinline__ void lds_dma16_cached(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
 
-template <int FMT, int NMAT, int NCH, bool CT = false>
+template <int FMT, int NMAT, int NCH, bool CT = false, bool CW = false>
 __device__ __forceinline__ void dma_issue(const DmaTiles<NMAT>& dt, __amdgpu_buffer_rsrc_t br,
                                           const uint32_t (&bvoff)[NCH], uint8_t* stage, int step, uint32_t dead,
                                           u32x4 (&b)[NCH][dma_pieces<FMT>()], DmaSide<FMT> (&side)[NMAT]) {
@@ -334,7 +338,7 @@ __device__ __forceinline__ void dma_issue(const DmaTiles<NMAT>& dt, __amdgpu_buf
 #pragma unroll
   for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) lds_dma16(dt.wr, stage + m * kTileBytes + h * 1024, dt.voff[m][h] | dead, so);
+    for (int h = 0; h < 2; ++h) lds_dma16<CW>(dt.wr, stage + m * kTileBytes + h * 1024, dt.voff[m][h] | dead, so);
   if constexpr (!CT) {
 #pragma unroll
     for (int m = 0; m < NMAT; ++m) {
@@ -505,7 +509,7 @@ constexpr int dma_ring_bytes() {  // per wave, the larger of the NCH variants (W
 // accumulation order, the weights through the wave's LDS ring of S stages (the
 // DMA of the next S-1 steps is in flight while one is computed; a dead step
 // still issues, reading zeros, so every step's wait count is exact).
-template <int FMT, int NMAT, int NCH, int KS, bool CT = false>
+template <int FMT, int NMAT, int NCH, int KS, bool CT = false, bool CW = false>
 __device__ __forceinline__ void gemv_tile_dma(const DmaTiles<NMAT>& dt, int K, int kw, __amdgpu_buffer_rsrc_t br,
                                               const uint32_t (&bvoff)[NCH], uint8_t* ring,
                                               f32x4 (&acc)[NMAT][NCH], uint8_t* ctab = nullptr, int wrow0 = 0,
@@ -534,7 +538,7 @@ __device__ __forceinline__ void gemv_tile_dma(const DmaTiles<NMAT>& dt, int K, i
   if constexpr (CT) code_table_fill<NMAT / 2>(dt.sr, K, wrow0, inter, kw, ctab);
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
-    dma_issue<FMT, NMAT, NCH, CT>(dt, br, bvoff, ring + s * kStage, st_lo + s, s < n ? 0u : kOutOfRange, b[s],
+    dma_issue<FMT, NMAT, NCH, CT, CW>(dt, br, bvoff, ring + s * kStage, st_lo + s, s < n ? 0u : kOutOfRange, b[s],
                                   side[s]);
   DmaSide<FMT> nx[NMAT];  // the code table: codes of the next step
   if constexpr (CT) {
@@ -549,7 +553,7 @@ __device__ __forceinline__ void gemv_tile_dma(const DmaTiles<NMAT>& dt, int K, i
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       const int ahead = i + s + S - 1;
-      dma_issue<FMT, NMAT, NCH, CT>(dt, br, bvoff, ring + ((s + S - 1) % S) * kStage, st_lo + ahead,
+      dma_issue<FMT, NMAT, NCH, CT, CW>(dt, br, bvoff, ring + ((s + S - 1) % S) * kStage, st_lo + ahead,
                                     ahead < n ? 0u : kOutOfRange, b[(s + S - 1) % S], side[(s + S - 1) % S]);
       wait_vmcnt<(S - 1) * dma_per_step<FMT, NMAT, NCH, CT>()>();
       __builtin_amdgcn_sched_barrier(0);
@@ -607,7 +611,7 @@ constexpr int sh_act_ring_bytes() {  // the larger of the NCH variants up to CMA
 }
 
 
-template <int FMT, int NMAT, int NCH, bool CR = false>
+template <int FMT, int NMAT, int NCH, bool CR = false, bool CW = false>
 __device__ __forceinline__ void sh_issue(const DmaTiles<NMAT>& dt, __amdgpu_buffer_rsrc_t br,
                                          const uint32_t (&avoff)[NCH][act_copies<FMT>()], uint8_t* wstage,
                                          uint8_t* aslot, int wave, int step, uint32_t dead,
@@ -617,7 +621,7 @@ __device__ __forceinline__ void sh_issue(const DmaTiles<NMAT>& dt, __amdgpu_buff
 #pragma unroll
   for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) lds_dma16(dt.wr, wstage + m * kTileBytes + h * 1024, dt.voff[m][h] | dead, so);
+    for (int h = 0; h < 2; ++h) lds_dma16<CW>(dt.wr, wstage + m * kTileBytes + h * 1024, dt.voff[m][h] | dead, so);
   if constexpr (!CR) {
 #pragma unroll
     for (int m = 0; m < NMAT; ++m) {
@@ -696,7 +700,7 @@ __device__ __forceinline__ void sh_tail(int left, int i, const uint8_t* ring, co
 // gemv_tile_dma for the down stage with the activations in the shared ring
 // (aring); route column col of chunk c reads activation row arow[c][...]
 // through the per-lane copy offsets avoff (kOutOfRange past the segment).
-template <int FMT, int NMAT, int NCH, int WIDE = 0, bool CR = false>
+template <int FMT, int NMAT, int NCH, int WIDE = 0, bool CR = false, bool CW = false>
 __device__ __forceinline__ void gemv_tile_dma_sh(const DmaTiles<NMAT>& dt, int K, int wave,
                                                  __amdgpu_buffer_rsrc_t br,
                                                  const uint32_t (&avoff)[NCH][act_copies<FMT>()], uint8_t* ring,
@@ -726,14 +730,14 @@ __device__ __forceinline__ void gemv_tile_dma_sh(const DmaTiles<NMAT>& dt, int K
   bare_barrier_dec();  // the previous pass's last slots have been read by every wave
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
-    sh_issue<FMT, NMAT, NCH, CR>(dt, br, avoff, ring + s * kStage, aring + s * kSlot, wave, s,
+    sh_issue<FMT, NMAT, NCH, CR, CW>(dt, br, avoff, ring + s * kStage, aring + s * kSlot, wave, s,
                                  s < n ? 0u : kOutOfRange, side[s]);
   int i = 0;
   for (; i + S <= n; i += S) {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       const int t = i + s, ahead = t + S - 1;
-      sh_issue<FMT, NMAT, NCH, CR>(dt, br, avoff, ring + ((s + S - 1) % S) * kStage, aring + (ahead % SA) * kSlot,
+      sh_issue<FMT, NMAT, NCH, CR, CW>(dt, br, avoff, ring + ((s + S - 1) % S) * kStage, aring + (ahead % SA) * kSlot,
                                    wave, ahead, ahead < n ? 0u : kOutOfRange, side[(s + S - 1) % S]);
       wait_vmcnt<(S - 1) * sh_per_step<FMT, NMAT, NCH, CR>()>();
       bare_barrier_dec();  // every wave's copies of step t have landed
@@ -829,7 +833,7 @@ __device__ __forceinline__ void tile_epilogue(const DecodeArgs& a, const SegView
 // 16-row tiles per matrix (gate and up tiles in stage 0) and its KS waves split
 // K.  With KS > 1 the partial sums meet in LDS (red[4][NMAT][NCH][64] float4)
 // and are added in fixed wave order, so results do not depend on timing.
-template <int FMT, int STAGE, int RT, int KS, int NCH, int WIDE = 0>
+template <int FMT, int STAGE, int RT, int KS, int NCH, int WIDE = 0, bool CW = false>
 __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView& bank, const SegView& sv, int base,
                                             int row0, int inter, uint8_t* smem, uint8_t* aring) {
   f32x4* red = reinterpret_cast<f32x4*>(smem);
@@ -933,7 +937,7 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
           else
             gemv_tile_dma_sh<FMT, NMAT, NCH, WIDE>(dt, K, wave, br, avoff, ring, aring, acc);
         } else {
-          gemv_tile_dma_sh<FMT, NMAT, NCH, WIDE>(dt, K, wave, br, avoff, ring, aring, acc);
+          gemv_tile_dma_sh<FMT, NMAT, NCH, WIDE, false, CW>(dt, K, wave, br, avoff, ring, aring, acc);
         }
       } else {
         if constexpr (FMT == FMT_MXFP4 && KS == kDecWaves && STAGE == 0) {
@@ -941,7 +945,7 @@ __device__ __forceinline__ void decode_pass(const DecodeArgs& a, const BankView&
           if (code_table_fits<NMAT>(K)) gemv_tile_dma<FMT, NMAT, NCH, KS, true>(dt, K, kw, br, bvoff, ring, acc, aring, wrow0, inter);
           else gemv_tile_dma<FMT, NMAT, NCH, KS>(dt, K, kw, br, bvoff, ring, acc);
         } else {
-          gemv_tile_dma<FMT, NMAT, NCH, KS>(dt, K, kw, br, bvoff, ring, acc);
+          gemv_tile_dma<FMT, NMAT, NCH, KS, false, CW>(dt, K, kw, br, bvoff, ring, acc);
         }
       }
     }
@@ -1001,7 +1005,7 @@ constexpr int chunks_per_pass() {
   return 2;
 }
 
-template <int FMT, int STAGE, int RT, int KS, int WIDE = 0>
+template <int FMT, int STAGE, int RT, int KS, int WIDE = 0, bool CW = false>
 __device__ __forceinline__ void decode_segment(const DecodeArgs& a, const BankView& bank, const SegView& sv, int row0,
                                                int inter, uint8_t* smem, uint8_t* aring) {
   constexpr int CMAX = chunks_per_pass<FMT, STAGE, RT, KS, WIDE>();
@@ -1009,14 +1013,14 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, const BankVi
     if constexpr (CMAX == 4) {
       // as many chunks as the segment has routes left (all on the 2-stage ring)
       const int left = sv.count - base;
-      if (left <= 16) decode_pass<FMT, STAGE, RT, KS, 1, WIDE>(a, bank, sv, base, row0, inter, smem, aring);
-      else if (left <= 32) decode_pass<FMT, STAGE, RT, KS, 2, WIDE>(a, bank, sv, base, row0, inter, smem, aring);
-      else decode_pass<FMT, STAGE, RT, KS, 4, WIDE>(a, bank, sv, base, row0, inter, smem, aring);
+      if (left <= 16) decode_pass<FMT, STAGE, RT, KS, 1, WIDE, CW>(a, bank, sv, base, row0, inter, smem, aring);
+      else if (left <= 32) decode_pass<FMT, STAGE, RT, KS, 2, WIDE, CW>(a, bank, sv, base, row0, inter, smem, aring);
+      else decode_pass<FMT, STAGE, RT, KS, 4, WIDE, CW>(a, bank, sv, base, row0, inter, smem, aring);
     } else if constexpr (CMAX == 1) {
       decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, smem, aring);
     } else {
-      if (sv.count - base <= 16) decode_pass<FMT, STAGE, RT, KS, 1>(a, bank, sv, base, row0, inter, smem, aring);
-      else decode_pass<FMT, STAGE, RT, KS, 2>(a, bank, sv, base, row0, inter, smem, aring);
+      if (sv.count - base <= 16) decode_pass<FMT, STAGE, RT, KS, 1, 0, CW>(a, bank, sv, base, row0, inter, smem, aring);
+      else decode_pass<FMT, STAGE, RT, KS, 2, 0, CW>(a, bank, sv, base, row0, inter, smem, aring);
     }
   }
 }
@@ -1089,7 +1093,15 @@ __device__ __forceinline__ void decode_stage_block(const DecodeArgs& a, int bx, 
       decode_segment<FMT_BF16, STAGE, RT, KS>(a, bank, sv, row0, inter, smem, smem + kRing);
   } else if (fmt == FMT_FP8) {
     if constexpr (FMT_R == FMT_FP8 || FMT_S == FMT_FP8)
-      decode_segment<FMT_FP8, STAGE, RT, KS, WIDE>(a, bank, sv, row0, inter, smem, smem + kRing);
+    {
+      // the shared expert's token pieces read the same weights at about the
+      // same time (the grid's first rows: each row block's pieces are
+      // gridDim.x apart, a multiple of 8, so on the same XCD)
+      if (sv.shared && a.M > a.seg_cap)
+        decode_segment<FMT_FP8, STAGE, RT, KS, WIDE, true>(a, bank, sv, row0, inter, smem, smem + kRing);
+      else
+        decode_segment<FMT_FP8, STAGE, RT, KS, WIDE>(a, bank, sv, row0, inter, smem, smem + kRing);
+    }
   } else {
     if constexpr (FMT_R == FMT_MXFP4 || FMT_S == FMT_MXFP4)
       decode_segment<FMT_MXFP4, STAGE, RT, KS>(a, bank, sv, row0, inter, smem, smem + kRing);
