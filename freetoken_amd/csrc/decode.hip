@@ -1075,7 +1075,11 @@ __device__ __forceinline__ void decode_stage_block(const DecodeArgs& a, int bx, 
     sv.start = a.seg_start[seg];
     sv.count = a.seg_count[seg];
   }
-  const int inter = sv.shared ? a.Is : a.I;
+  // both fields read, then chosen: a select between the two (adjacent)
+  // argument fields was compiled into a load from a private copy of the
+  // arguments, i.e. scratch memory, in some instantiations
+  const int ia = a.I, is = a.Is;
+  const int inter = sv.shared ? is : ia;
   const int row0 = bx * (kDecWaves / KS) * RT * 16;
   if (STAGE == 0 && row0 >= inter) return;
   // field-wise selects keep the kernel argument block out of private memory
