@@ -673,7 +673,13 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
   const int xrows = a.x_token_rows ? a.M : a.numel + a.M;
   const __amdgpu_buffer_rsrc_t rsrc_x = make_rsrc(a.xq, static_cast<uint32_t>(xrows) * K);
   __amdgpu_buffer_rsrc_t rsrc_w;
-  __amdgpu_buffer_rsrc_t rsrc_s = make_rsrc(a.xs, static_cast<uint32_t>(xrows) * nkb * 4);
+  // scales: the activation scales' descriptor is the kernel's; the weight
+  // scales' is set per tile for every wave (waves 4-7 never use it), so that
+  // both stay wave-uniform values in scalar registers (a descriptor assigned
+  // under a per-wave condition was kept in vector registers and every copy
+  // became a loop over its distinct values)
+  const __amdgpu_buffer_rsrc_t rsrc_xs = make_rsrc(a.xs, static_cast<uint32_t>(xrows) * nkb * 4);
+  __amdgpu_buffer_rsrc_t rsrc_ws = rsrc_xs;
   // weights: copy c of wave w fills LDS rows of 1 KB block i = w*kACopies + c
   uint32_t avoff[L::kACopies];
 #pragma unroll
@@ -705,15 +711,13 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
     const BankView bank = t.shared ? a.ws : a.w;
     const int n0 = n0_of(t);
     rsrc_w = make_rsrc(bank.w + (static_cast<size_t>(t.expert) * a.N + n0) * rb, static_cast<uint32_t>(a.N - n0) * rb);
-    if (wave < 4) {
-      if constexpr (FMT == FMT_FP8)
-        rsrc_s = make_rsrc(static_cast<const uint8_t*>(bank.s) +
-                               (static_cast<size_t>(t.expert) * (a.N / 128) + n0 / 128) * nkb * 4,
-                           static_cast<uint32_t>((a.N - n0) / 128) * nkb * 4);
-      else
-        rsrc_s = make_rsrc(static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(t.expert) * a.N + n0) * (K / 32),
-                           static_cast<uint32_t>(a.N - n0) * (K / 32));
-    }
+    if constexpr (FMT == FMT_FP8)
+      rsrc_ws = make_rsrc(static_cast<const uint8_t*>(bank.s) +
+                              (static_cast<size_t>(t.expert) * (a.N / 128) + n0 / 128) * nkb * 4,
+                          static_cast<uint32_t>((a.N - n0) / 128) * nkb * 4);
+    else
+      rsrc_ws = make_rsrc(static_cast<const uint8_t*>(bank.s) + (static_cast<size_t>(t.expert) * a.N + n0) * (K / 32),
+                          static_cast<uint32_t>(a.N - n0) * (K / 32));
     const int ln = fresh_lane();
     if (wave >= 4) {
       const int row = s_row[b][64 * (wave - 4) + ln];
@@ -737,8 +741,10 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
     } else if (q < L::kACopies + L::kBCopies) {
       const int c = q - L::kACopies;
       lds_buf16(rsrc_x, st + L::kOffB + (wave * L::kBCopies + c) * 1024, xvoff[c], static_cast<uint32_t>(kb) * 128);
-    } else if (scopy) {
-      lds_buf4(rsrc_s, sdst_base + stg * L::kStage, svoff, static_cast<uint32_t>(kb) * 4);
+    } else if (wave < 4) {
+      if (scopy) lds_buf4(rsrc_ws, sdst_base + stg * L::kStage, svoff, static_cast<uint32_t>(kb) * 4);
+    } else {
+      lds_buf4(rsrc_xs, sdst_base + stg * L::kStage, svoff, static_cast<uint32_t>(kb) * 4);
     }
   };
   auto issue = [&](int kb, int stg) {
@@ -749,7 +755,11 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
 #pragma unroll
     for (int c = 0; c < L::kBCopies; ++c)
       lds_buf16(rsrc_x, st + L::kOffB + (wave * L::kBCopies + c) * 1024, xvoff[c], static_cast<uint32_t>(kb) * 128);
-    if (scopy) lds_buf4(rsrc_s, sdst_base + stg * L::kStage, svoff, static_cast<uint32_t>(kb) * 4);
+    if (wave < 4) {
+      if (scopy) lds_buf4(rsrc_ws, sdst_base + stg * L::kStage, svoff, static_cast<uint32_t>(kb) * 4);
+    } else {
+      lds_buf4(rsrc_xs, sdst_base + stg * L::kStage, svoff, static_cast<uint32_t>(kb) * 4);
+    }
   };
 
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
