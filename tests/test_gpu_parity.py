@@ -212,9 +212,10 @@ def test_decode_parity_full_shapes(dev, case, M):
 # 512: 2, 4, 6 or 8 K steps of 256 split over the 4 waves, so at H = 512 two
 # waves have no step and at H = 1536 the waves have 1 or 2) and the down
 # stage's codes in registers (I a multiple of 256 up to 2048: 1, 2, 3 and 8 K
-# steps), with one or two route chunks per pass and several passes or
-# segments per expert (M = 200: 67 routes per expert).
-MX_SHAPE_CASES = [(512, 256), (1024, 768), (1536, 512), (2048, 2048)]
+# steps; I = 2304, 9 steps, takes the per-step code loads), with one or two
+# route chunks per pass and several passes or segments per expert (M = 200:
+# 67 routes per expert).
+MX_SHAPE_CASES = [(512, 256), (1024, 768), (1536, 512), (2048, 2048), (512, 2304)]
 
 
 @pytest.mark.parametrize("H,I", MX_SHAPE_CASES, ids=[f"H{h}_I{i}" for h, i in MX_SHAPE_CASES])
