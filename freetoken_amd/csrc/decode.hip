@@ -1357,6 +1357,9 @@ static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared
         (a.M <= 2 ||
          static_cast<long long>(g2.x) * g2.y <= static_cast<long long>(cu_count()) * resident_per_cu<k2>()))
       return launch_one<k1>(g1, a, stream);
+    // MXFP4 up to 8 tokens keeps two row tiles per wave (C3 b=2 66.0-66.5 ->
+    // 65.1 us; one tile per wave 0.6-10 us slower at b=1-8)
+    if (FR == FMT_MXFP4 && a.M <= 8) return launch_one<k2>(g2, a, stream);
     if (fill_of<k2>(g2) >= fill_of<k1>(g1) - kSlack) return launch_one<k2>(g2, a, stream);
     return launch_one<k1>(g1, a, stream);
   }
