@@ -6,11 +6,19 @@ Reference: ``setup_offload_expert_banks`` / ``_build_fp8_expert_banks`` /
 ``convert_checkpoint`` (``checkpoint/convert.py:163-330``).
 
 Tensor names follow the HF layout the reference matches
-(``models/qwen3_5_moe/weight.py:720-723``), with any prefix before
-``layers`` (``model.language_model.layers`` for Qwen3.5, ``model.layers`` for
-DeepSeek-V3)::
+(``models/qwen3_5_moe/weight.py:720-723``), under one of the two decoder
+stems, ``model.language_model.layers`` (Qwen3.5) or ``model.layers``
+(DeepSeek-V3)::
 
-    <prefix>.layers.<L>.mlp.experts.<e>.{gate,up,down}_proj.{weight,weight_scale_inv}
+    <stem>.<L>.mlp.experts.<e>.{gate,up,down}_proj.{weight,weight_scale_inv}
+
+Multi-token-prediction heads are not decoder layers and are dropped, as the
+reference drops them: Qwen3.5's ``mtp.layers.N.mlp.experts.*`` do not match the
+anchored stems (``weight.py:36-38,718-723``), and DeepSeek-V3's MTP layer,
+stored as ``model.layers.<num_hidden_layers>`` after the decoder layers, is
+cut by the ``num_hidden_layers`` of ``config.json`` (or of its
+``text_config``), as the reference's model config counts only those
+(``models/glm4_moe/config.py:28-30``).
 
 ``weight`` is e4m3 ``[N, K]``; ``weight_scale_inv`` the 128x128 block scale
 ``[N/128, K/128]`` (bf16 in the reference's checkpoints, float32 in some).
@@ -53,7 +61,7 @@ from .ftw import DEFAULT_SHARD_LIMIT, _host_buffer, save_ftw_banks
 BLOCK = 128
 INDEX_FILE = "model.safetensors.index.json"
 _EXPERT_RE = re.compile(
-    r"^(?P<stem>.+\.)?layers\.(?P<layer>\d+)\.mlp\.experts\.(?P<expert>\d+)\."
+    r"^(?P<stem>model\.(?:language_model\.)?)layers\.(?P<layer>\d+)\.mlp\.experts\.(?P<expert>\d+)\."
     r"(?P<proj>gate|up|down)_proj\.(?P<kind>weight|weight_scale_inv)$"
 )
 _WEIGHT_SUFFIXES = (".safetensors", ".gguf", ".ftw")
@@ -88,24 +96,44 @@ def _weight_map(model_path: str) -> dict[str, str]:
         return {k: "model.safetensors" for k in f.keys()}
 
 
+def _num_hidden_layers(model_path: str) -> int | None:
+    """Decoder layers of the checkpoint's ``config.json`` (``num_hidden_layers``,
+    or that of ``text_config`` for multimodal configs); None when not stated."""
+    path = os.path.join(model_path, "config.json")
+    if not os.path.isfile(path):
+        return None
+    with open(path) as f:
+        cfg = json.load(f)
+    n = cfg.get("num_hidden_layers")
+    if n is None and isinstance(cfg.get("text_config"), dict):
+        n = cfg["text_config"].get("num_hidden_layers")
+    return int(n) if n is not None else None
+
+
 def scan_experts(model_path: str) -> tuple[ExpertLayout, dict[str, list[tuple[str, tuple]]]]:
     """The checkpoint's expert layout and, per shard file, its expert tensors as
     (name, (layer, expert, proj, kind)); raises on a missing or misshapen tensor."""
     from safetensors import safe_open
 
     wmap = _weight_map(model_path)
+    n_layers = _num_hidden_layers(model_path)
     per_file: dict[str, list[tuple[str, tuple]]] = {}
-    layers, experts = set(), set()
+    layers, experts, stems = set(), set(), set()
     for name, file in wmap.items():
         m = _EXPERT_RE.match(name)
         if m is None:
             continue
+        if n_layers is not None and int(m["layer"]) >= n_layers:
+            continue  # an MTP layer stored after the decoder layers
+        stems.add(m["stem"])
         key = (int(m["layer"]), int(m["expert"]), m["proj"], m["kind"])
         per_file.setdefault(file, []).append((name, key))
         layers.add(key[0])
         experts.add(key[1])
     if not per_file:
-        raise ValueError(f"{model_path}: no routed-expert tensors (<prefix>.layers.L.mlp.experts.e.*_proj.*)")
+        raise ValueError(f"{model_path}: no routed-expert tensors (model[.language_model].layers.L.mlp.experts.e.*_proj.*)")
+    if len(stems) > 1:
+        raise ValueError(f"{model_path}: routed experts under two decoder stems {sorted(stems)}")
     first, L, E = min(layers), len(layers), len(experts)
     if sorted(layers) != list(range(first, first + L)) or sorted(experts) != list(range(E)):
         raise ValueError(f"{model_path}: expert layers {sorted(layers)} / experts 0..{E - 1} not contiguous")

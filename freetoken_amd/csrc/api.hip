@@ -785,6 +785,14 @@ int noalloc_scratch(ftmoe_stream_t stream, void** out) {
   }
   std::lock_guard<std::mutex> g(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    // the lookup may load the library's code object on this device: not a
+    // call to make while the stream is being captured
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (stream && hipStreamIsCapturing(stream, &cs) != hipSuccess)
+      return fail(FTMOE_ERR_HIP, "experts_decode_noalloc: stream capture query failed");
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode_noalloc: the first call on device %d must run outside graph "
+                  "capture (it looks up the scratch array's address)", dev);
     void* p = nullptr;
     const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (err != hipSuccess || !p)

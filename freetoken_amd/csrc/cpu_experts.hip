@@ -364,7 +364,9 @@ struct Job {
   bool permanent = false;
   bool done = true;
   bool failed = false;     // poisoned by the watchdog (or refused by an unhealthy executor)
-  bool abandoned = false;  // poisoned while the driver held it: never recycled
+  // poisoned while the driver held it: never recycled, and the pool stops
+  // taking its work units and writes nothing more to its y
+  std::atomic<bool> abandoned{false};
 };
 
 class Executor {
@@ -406,12 +408,21 @@ class Executor {
     return captured_;
   }
   bool healthy() const { return !unhealthy_.load(); }
+  // The watchdog abandoned a job that the driver is still computing (a wedged
+  // pool): the threads cannot be joined, so the executor must not be freed.
+  bool wedged() {
+    std::lock_guard<std::mutex> g(m_);
+    return unhealthy_.load() && busy_;
+  }
   void set_watchdog_ms(int ms) { watchdog_ms_ = ms; }
-  // Holds the driver before its next job (maintenance; tests of the watchdog).
-  void hold(bool on) {
+  // Maintenance and tests of the watchdog: mode 1 holds the driver before its
+  // next job; mode 2 lets the driver take its next job and stall inside it,
+  // before its first work unit, as a wedged pool would (until mode 0).
+  void hold(int mode) {
     {
       std::lock_guard<std::mutex> g(m_);
-      hold_ = on;
+      hold_ = mode == 1;
+      stall_.store(mode == 2);
     }
     cv_job_.notify_all();
   }
@@ -634,6 +645,10 @@ class Executor {
     } else {
       act16_.resize(static_cast<size_t>(R) * I);
     }
+    while (stall_.load(std::memory_order_relaxed)) std::this_thread::sleep_for(std::chrono::milliseconds(1));
+    // an abandoned job's remaining work units return at once, and pass 3, the
+    // only writer of the caller's y, writes no row once the job is abandoned
+    const auto dropped = [&] { return j.abandoned.load(std::memory_order_relaxed); };
     const X* const xin = BF ? reinterpret_cast<const X*>(j.x) : reinterpret_cast<const X*>(xf_.data());
     X* const act = BF ? reinterpret_cast<X*>(act16_.data()) : reinterpret_cast<X*>(act_.data());
     const auto dot = [&](const Mat& m, int n, const X* const* xs, int nv, float* o) {
@@ -645,6 +660,7 @@ class Executor {
     // pass 1: gate and up rows of (group, 32 rows of I) -> bf16 act
     const int tiles1 = I / kTile;
     parallel(G * tiles1, [&](int u) {
+      if (dropped()) return;
       const int g = u / tiles1, i0 = (u % tiles1) * kTile;
       const int* rs = order_.data() + group_[g];
       const int nv = group_[g + 1] - group_[g];
@@ -667,6 +683,7 @@ class Executor {
     // pass 2: down rows of (group, 32 rows of H) -> bf16(down * router weight) per route
     const int tiles2 = H / kTile;
     parallel(G * tiles2, [&](int u) {
+      if (dropped()) return;
       const int g = u / tiles2, h0 = (u % tiles2) * kTile;
       const int* rs = order_.data() + group_[g];
       const int nv = group_[g + 1] - group_[g];
@@ -681,6 +698,7 @@ class Executor {
     });
     // pass 3: each token's routes summed in route order
     parallel(j.M, [&](int t) {
+      if (dropped()) return;
       bf16* y = j.y + static_cast<size_t>(t) * H;
       for (int h = 0; h < H; ++h) {
         float s = 0.f;
@@ -707,6 +725,7 @@ class Executor {
   std::atomic<bool> stop_{false};
   bool busy_ = false;  // the driver is computing a job
   bool hold_ = false;  // the driver takes no new job
+  std::atomic<bool> stall_{false};  // the driver stalls inside its job (tests of a wedged pool)
   int captured_ = 0;   // permanent (graph-captured) job records
   int watchdog_ms_ = 10000;
   std::atomic<uint64_t> progress_{0};  // work units and jobs completed
@@ -773,6 +792,9 @@ int ftmoe_cpu_executor_destroy(ftmoe_cpu_executor* ex, int graphs_released) {
                   e->captured_jobs());
     return ftmoe::report_error(FTMOE_ERR_BUSY, msg);
   }
+  if (e->wedged())
+    return ftmoe::report_error(FTMOE_ERR_BUSY, "cpu_executor_destroy: the watchdog abandoned a job the pool is still "
+                               "computing; its threads cannot be joined, so the executor is kept");
   delete e;
   return FTMOE_OK;
 }
@@ -787,7 +809,7 @@ void ftmoe_cpu_executor_set_watchdog(ftmoe_cpu_executor* ex, int ms) {
 }
 
 void ftmoe_cpu_executor_hold(ftmoe_cpu_executor* ex, int hold) {
-  if (ex) reinterpret_cast<ftmoe_cpu::Executor*>(ex)->hold(hold != 0);
+  if (ex) reinterpret_cast<ftmoe_cpu::Executor*>(ex)->hold(hold);
 }
 
 const char* ftmoe_cpu_executor_isa(ftmoe_cpu_executor* ex) {

@@ -591,6 +591,11 @@ class CpuExecutor:
         """Keeps the pool from starting jobs while ``on`` (maintenance; tests of the watchdog)."""
         lib().ftmoe_cpu_executor_hold(self._h, int(bool(on)))
 
+    def stall(self, on: bool) -> None:
+        """While ``on``, the driver takes its next job and stalls inside it, as a
+        wedged pool would (tests of the watchdog and of ``close``)."""
+        lib().ftmoe_cpu_executor_hold(self._h, 2 if on else 0)
+
     @property
     def healthy(self) -> bool:
         return lib().ftmoe_cpu_executor_healthy(self._h) == _lib.FTMOE_OK
@@ -606,7 +611,9 @@ class CpuExecutor:
         """Frees the executor once the host functions queued on streams have run
         (the device is synchronised first).  While jobs captured into graphs
         exist the executor is kept alive instead, unless ``graphs_released``
-        says those graphs are destroyed: a replay would touch a freed executor."""
+        says those graphs are destroyed: a replay would touch a freed executor.
+        A pool wedged inside a job the watchdog abandoned cannot be joined: its
+        executor is kept too, and ``close`` returns at once."""
         if not self._h:
             return
         if torch.cuda.is_available() and torch.cuda.is_initialized():

@@ -252,7 +252,10 @@ int ftmoe_experts_decode(const void* x, int M, int top_k, const float* topk_w, c
  * must belong to the current device.  Every call on a GPU shares that GPU's
  * array (nothing in it needs clearing between calls): calls that overlap on
  * one GPU -- on different streams, or from different host threads -- race and
- * must be serialised by the caller. */
+ * must be serialised by the caller.  The first call on a device looks up the
+ * array's address there and must run outside graph capture (refused with
+ * FTMOE_ERR_UNSUPPORTED under capture); later calls can be captured and
+ * replayed. */
 size_t ftmoe_experts_decode_noalloc_capacity(void);
 int ftmoe_experts_decode_noalloc(const void* x, int M, int top_k, const float* topk_w, const int32_t* topk_ids,
                                  const ftmoe_bank* bank, const ftmoe_bank* shared, int activation,
@@ -328,8 +331,11 @@ ftmoe_cpu_executor* ftmoe_cpu_executor_create(int threads);
 /* Waits for queued jobs and frees the executor.  Refused (FTMOE_ERR_BUSY,
  * nothing freed) while jobs captured into graphs exist, unless
  * graphs_released says that every such graph is destroyed: a replay would
- * run their host functions against the freed executor.  Host functions still
- * queued on a stream must have run (synchronise the stream first). */
+ * run their host functions against the freed executor.  Also refused, at
+ * once, when the watchdog abandoned a job that the pool is still computing
+ * (a wedged pool: its threads cannot be joined); the caller keeps the handle
+ * for the life of the process.  Host functions still queued on a stream must
+ * have run (synchronise the stream first). */
 int ftmoe_cpu_executor_destroy(ftmoe_cpu_executor* ex, int graphs_released);
 const char* ftmoe_cpu_executor_isa(ftmoe_cpu_executor* ex);
 /* Watchdog (replaces the flag watchdog of moe/cpu_executor.py:602-656): a
@@ -341,8 +347,11 @@ const char* ftmoe_cpu_executor_isa(ftmoe_cpu_executor* ex);
  * written; callers check ftmoe_cpu_executor_healthy once per step (0 =
  * healthy, FTMOE_ERR_TIMEOUT after the watchdog fired).  The period is
  * FTMOE_CPU_WATCHDOG_S seconds (default 10; 0 turns the watchdog off) or
- * set_watchdog's milliseconds.  hold != 0 keeps the driver from starting
- * jobs (maintenance; tests force a stalled pool with it). */
+ * set_watchdog's milliseconds.  A job abandoned while the pool computes it
+ * takes no further work units and writes no more rows of its y.  hold 1 keeps
+ * the driver from starting jobs; hold 2 lets the driver take its next job and
+ * stall inside it until hold 0 (maintenance; tests force a stalled or wedged
+ * pool with them). */
 int ftmoe_cpu_executor_healthy(ftmoe_cpu_executor* ex);
 void ftmoe_cpu_executor_set_watchdog(ftmoe_cpu_executor* ex, int ms);
 void ftmoe_cpu_executor_hold(ftmoe_cpu_executor* ex, int hold);

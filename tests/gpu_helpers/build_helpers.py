@@ -8,8 +8,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 ROOT = HERE.parents[1]
-HELPERS = {"libbf16check.so": "bf16_rounding.hip", "libquantcheck.so": "quant_division.hip",
-           "libreadbw.so": "read_bw.hip"}
+HELPERS = {"libbf16check.so": "bf16_rounding.hip", "libquantcheck.so": "quant_division.hip"}
 
 
 def build() -> list[Path]:

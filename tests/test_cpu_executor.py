@@ -197,3 +197,33 @@ def test_destroy_refused_while_captured_jobs_may_replay():
     assert L.ftmoe_cpu_executor_healthy(h) == _lib.FTMOE_OK
     assert L.ftmoe_cpu_executor_destroy(h, 0) == _lib.FTMOE_OK
     assert L.ftmoe_cpu_executor_destroy(None, 0) == _lib.FTMOE_OK
+
+
+def test_close_returns_when_the_pool_is_wedged():
+    """A job stuck inside the pool (the driver stalls in it) is abandoned by the
+    watchdog: ``close`` must not wait for the wedged threads (the executor is
+    kept for the process instead), and when the stuck job moves again it writes
+    nothing more to the caller's output."""
+    import time
+
+    rng = np.random.default_rng(47)
+    ex = ops.CpuExecutor(threads=2, watchdog_s=0.3)
+    args, _ = _small_job(rng)
+    y = torch.full_like(args[1], 7.0)
+    ex.stall(True)
+    with pytest.raises(_lib.FtmoeError, match="watchdog"):
+        ex.run(*args, y=y)
+    assert not ex.healthy
+    h = ex._h
+    t0 = time.monotonic()
+    ex.close()
+    assert time.monotonic() - t0 < 2.0 and ex._h is None
+    assert ops._KEPT_EXECUTORS and ops._KEPT_EXECUTORS[-1] == h
+    L = _lib.lib()
+    L.ftmoe_cpu_executor_hold(h, 0)  # the stuck job resumes and finds itself abandoned
+    deadline = time.monotonic() + 10.0
+    while L.ftmoe_cpu_executor_destroy(h, 0) != _lib.FTMOE_OK:  # refused while the pool is still inside the job
+        assert time.monotonic() < deadline, "the abandoned job never left the pool"
+        time.sleep(0.05)
+    ops._KEPT_EXECUTORS.remove(h)
+    assert (y == 7).all()  # the abandoned job wrote no row of y

@@ -21,13 +21,31 @@ from freetoken_amd.checkpoint.hf import convert_hf_experts_to_ftw, load_hf_exper
 
 
 def write_hf_checkpoint(path, prefix: str, dense: int, L: int, E: int, H: int, I: int, seed: int = 0,
-                        scale_dtype=torch.bfloat16, shards: int = 2):
+                        scale_dtype=torch.bfloat16, shards: int = 2, mtp: bool = True):
     """A block-FP8 checkpoint: ``dense`` dense layers, then ``L`` MoE layers of
-    ``E`` experts; returns the oracle banks per MoE layer (scales as stored)."""
+    ``E`` experts; returns the oracle banks per MoE layer (scales as stored).
+
+    With ``mtp`` the checkpoint also holds a multi-token-prediction head's
+    experts where the two model families store them: ``mtp.layers.0`` (Qwen3.5,
+    ``model.language_model`` stem) or ``model.layers.<num_hidden_layers>``
+    (DeepSeek-V3, ``model.layers`` stem), which the loader must drop."""
     import safetensors.torch as st
 
     rng = np.random.default_rng(seed)
     tensors, banks = {}, []
+    if mtp:
+        mtp_prefix = "mtp.layers.0" if prefix.startswith("model.language_model") else f"{prefix}.{dense + L}"
+        junk = synth.make_bank("fp8", E, H, I, np.random.default_rng(seed + 99))
+        for e in range(E):
+            p = f"{mtp_prefix}.mlp.experts.{e}"
+            gu = torch.from_numpy(junk.gate_up[e]).view(torch.float8_e4m3fn)
+            tensors[f"{p}.gate_proj.weight"] = gu[:I].contiguous()
+            tensors[f"{p}.up_proj.weight"] = gu[I:].contiguous()
+            tensors[f"{p}.down_proj.weight"] = torch.from_numpy(junk.down[e]).view(torch.float8_e4m3fn).contiguous()
+            s_gu = torch.from_numpy(junk.gate_up_scale[e]).to(scale_dtype)
+            tensors[f"{p}.gate_proj.weight_scale_inv"] = s_gu[: I // 128].contiguous()
+            tensors[f"{p}.up_proj.weight_scale_inv"] = s_gu[I // 128:].contiguous()
+            tensors[f"{p}.down_proj.weight_scale_inv"] = torch.from_numpy(junk.down_scale[e]).to(scale_dtype)
     for li in range(L):
         bank = synth.make_bank("fp8", E, H, I, rng)
         sc = torch.from_numpy(bank.gate_up_scale).to(scale_dtype)
@@ -62,7 +80,11 @@ def write_hf_checkpoint(path, prefix: str, dense: int, L: int, E: int, H: int, I
     with open(os.path.join(path, "model.safetensors.index.json"), "w") as f:
         json.dump({"metadata": {}, "weight_map": wmap}, f)
     with open(os.path.join(path, "config.json"), "w") as f:
-        json.dump({"hidden_size": H, "moe_intermediate_size": I, "n_routed_experts": E}, f)
+        cfg = {"hidden_size": H, "moe_intermediate_size": I, "n_routed_experts": E, "num_hidden_layers": dense + L,
+               "num_nextn_predict_layers": int(mtp)}
+        if prefix.startswith("model.language_model"):
+            cfg = {"text_config": cfg}
+        json.dump(cfg, f)
     os.makedirs(os.path.join(path, "tok"), exist_ok=True)
     with open(os.path.join(path, "tok", "tokenizer.json"), "w") as f:
         f.write("{}")
@@ -136,3 +158,30 @@ def test_scan_rejects_incomplete_checkpoints(tmp_path):
         scan_experts(str(tmp_path))
     with pytest.raises(ValueError, match="mode"):
         load_hf_expert_banks(str(tmp_path), mode="int4")
+
+
+@pytest.mark.parametrize("prefix", ["model.layers", "model.language_model.layers"])
+def test_mtp_experts_are_dropped(tmp_path, prefix):
+    """The MTP head's experts (``mtp.layers.0`` for Qwen3.5, ``model.layers.<num_hidden_layers>``
+    for DeepSeek-V3) are not decoder layers: the layer count stays L and the banks hold
+    only the decoder layers' experts."""
+    L, E, H, I = 2, 3, 256, 128
+    banks = write_hf_checkpoint(tmp_path, prefix, 1, L, E, H, I, seed=11, mtp=True)
+    lay, per_file = scan_experts(str(tmp_path))
+    assert (lay.num_layers, lay.first_moe_layer) == (L, 1)
+    assert all(not n.startswith("mtp.") and int(n.split(".layers.")[1].split(".")[0]) < 1 + L
+               for items in per_file.values() for n, _ in items)
+    _, src, _ = load_hf_expert_banks(str(tmp_path), pinned=False)
+    assert len(src["gate_up"]) == L
+    for li, b in enumerate(banks):
+        np.testing.assert_array_equal(src["gate_up"][li].view(torch.uint8).numpy(), b.gate_up)
+
+
+def test_expert_names_outside_the_decoder_stems_are_ignored(tmp_path):
+    """Without a layer count in config.json the anchored stems alone decide: a
+    vision tower's or an MTP head's experts never join the banks."""
+    L, E, H, I = 1, 2, 128, 128
+    write_hf_checkpoint(tmp_path, "model.language_model.layers", 0, L, E, H, I, seed=3, mtp=True)
+    os.remove(tmp_path / "config.json")
+    lay, _ = scan_experts(str(tmp_path))
+    assert lay.num_layers == L
