@@ -38,6 +38,7 @@ class FtmoeBank(ctypes.Structure):
         ("gate_up_scale", ctypes.c_void_p),
         ("down", ctypes.c_void_p),
         ("down_scale", ctypes.c_void_p),
+        ("swiglu_limit", ctypes.c_float),
     ]
 
 
@@ -79,6 +80,7 @@ SIGNATURES = {
     "ftmoe_align_sizes": (None, [_i, _i, _i, _ip, _ip]),
     "ftmoe_align": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "ftmoe_slot_map": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp, _vp]),
+    "ftmoe_route_histogram": (_i, [_vp, _i, _i, _vp, _vp]),
     "ftmoe_lru_ensure": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp,
                               _vp, _vp]),
     "ftmoe_fetch_experts": (_i, [_fbp, _i, _vp, _vp, _vp, _i, _vp]),

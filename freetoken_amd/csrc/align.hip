@@ -18,6 +18,8 @@
 // of (expert << 6 | lane) inside the wave yields, for every route, its rank
 // among the equal-expert routes of the batch, so the final position is
 // region_start[e] + wave_base[w][e] + rank -- no atomics, fully deterministic.
+#include <algorithm>
+
 #include "align_wave.h"
 #include "kernels.h"
 
@@ -614,6 +616,32 @@ hipError_t launch_slot_map(const int32_t* ids, int numel, const int32_t* slot_fo
   const size_t lds = stats ? sizeof(int) * static_cast<size_t>(table_size) : 0;
   hipLaunchKernelGGL(slot_map_kernel, dim3(1), dim3(1024), lds, stream, ids, numel, slot_for_id, table_size,
                      slot_ids, miss_mask, stats);
+  return hipGetLastError();
+}
+
+// Routing histogram: freq[e] += number of routes with id e, ids outside
+// [0, num_experts) skipped.  Each workgroup counts its stride of the routes
+// in LDS, then adds its nonzero bins to freq (integer atomics: the sums do
+// not depend on the order).
+__global__ void __launch_bounds__(256) route_histogram_kernel(const int32_t* ids, int numel, int num_experts,
+                                                              unsigned long long* freq) {
+  extern __shared__ int bins[];
+  for (int e = threadIdx.x; e < num_experts; e += blockDim.x) bins[e] = 0;
+  __syncthreads();
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < numel; i += gridDim.x * blockDim.x) {
+    const int e = ids[i];
+    if (e >= 0 && e < num_experts) atomicAdd(&bins[e], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < num_experts; e += blockDim.x)
+    if (bins[e]) atomicAdd(freq + e, static_cast<unsigned long long>(bins[e]));
+}
+
+hipError_t launch_route_histogram(const int32_t* ids, int numel, int num_experts, long long* freq,
+                                  hipStream_t stream) {
+  const int blocks = std::max(1, std::min((numel + 1023) / 1024, 64));
+  hipLaunchKernelGGL(route_histogram_kernel, dim3(blocks), dim3(256), sizeof(int) * static_cast<size_t>(num_experts),
+                     stream, ids, numel, num_experts, reinterpret_cast<unsigned long long*>(freq));
   return hipGetLastError();
 }
 

@@ -1,6 +1,7 @@
 // C ABI of the MoE-layer hot path (declarations and contracts: include/ftmoe.h).
 // Validates arguments on the host, carves the caller's workspace and launches
 // the kernels of route.hip, align.hip and decode.hip on the caller's stream.
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <algorithm>
@@ -59,6 +60,15 @@ int check_bank(const ftmoe_bank* b, const char* name, bool shared) {
   if (!b->gate_up || !b->down) return fail(FTMOE_ERR_INVALID, "%s bank: NULL weights", name);
   if (b->format != FTMOE_FMT_BF16 && (!b->gate_up_scale || !b->down_scale))
     return fail(FTMOE_ERR_INVALID, "%s bank: NULL scales for a quantized format", name);
+  if (!std::isfinite(b->swiglu_limit) || b->swiglu_limit < 0.f)
+    return fail(FTMOE_ERR_INVALID, "%s bank: swiglu_limit %g (finite, >= 0)", name, b->swiglu_limit);
+  return FTMOE_OK;
+}
+
+// The clamped SwiGLU of a bank (swiglu_limit > 0) is a SiLU form.
+int check_limit(const ftmoe_bank* b, const ftmoe_bank* shared, int activation, const char* what) {
+  if (activation != FTMOE_ACT_SILU && ((b && b->swiglu_limit > 0.f) || (shared && shared->swiglu_limit > 0.f)))
+    return fail(FTMOE_ERR_UNSUPPORTED, "%s: swiglu_limit > 0 needs the silu activation (got %d)", what, activation);
   return FTMOE_OK;
 }
 
@@ -266,6 +276,16 @@ int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_i
                    "slot_map launch");
 }
 
+int ftmoe_route_histogram(const int32_t* topk_ids, int numel, int num_experts, int64_t* freq, ftmoe_stream_t stream) {
+  if ((!topk_ids && numel) || !freq) return fail(FTMOE_ERR_INVALID, "route_histogram: NULL pointer");
+  if (numel < 0 || num_experts <= 0 || num_experts > 16384)
+    return fail(FTMOE_ERR_UNSUPPORTED, "route_histogram: numel=%d num_experts=%d", numel, num_experts);
+  if (numel == 0) return FTMOE_OK;
+  return check_hip(ftmoe::launch_route_histogram(topk_ids, numel, num_experts, reinterpret_cast<long long*>(freq),
+                                                 stream),
+                   "route_histogram launch");
+}
+
 int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layers, int num_experts,
                      int32_t* slot_for_id, int32_t* id_of_slot, int64_t* usage, int64_t* step, int cache_size,
                      int64_t* recency, int max_fetch, int fetch_frac_q16, int32_t* evict_slots,
@@ -455,6 +475,8 @@ int experts_decode_impl(const void* x, int M, int top_k, const float* topk_w, co
                 ftmoe::kCountMaxRows);
   if (activation < FTMOE_ACT_SILU || activation > FTMOE_ACT_GELU_TANH)
     return fail(FTMOE_ERR_UNSUPPORTED, "experts_decode: activation %d", activation);
+  rc = check_limit(bank, shared, activation, "experts_decode");
+  if (rc) return rc;
   const DecodeLayout need = decode_layout(nullptr, M, top_k, bank, shared);
   {
     // the decode kernels address activations and one expert's matrices with
@@ -530,6 +552,8 @@ int experts_decode_impl(const void* x, int M, int top_k, const float* topk_w, co
   d.ic3 = L.ic3;
   d.sh_out = L.sh_out;
   d.act_kind = activation;
+  d.act_limit = bank->swiglu_limit;
+  d.sh_act_limit = shared ? shared->swiglu_limit : 0.f;
   d.weight_on_input = apply_router_weight_on_input;
   const int fmt_s = shared ? shared->format : FTMOE_FMT_NONE;
 
@@ -662,6 +686,8 @@ int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, 
   if (bank->num_rows > 1023) return fail(FTMOE_ERR_UNSUPPORTED, "experts_prefill: num_rows %d > 1023", bank->num_rows);
   if (activation < FTMOE_ACT_SILU || activation > FTMOE_ACT_GELU_TANH)
     return fail(FTMOE_ERR_UNSUPPORTED, "experts_prefill: activation %d", activation);
+  rc = check_limit(bank, shared, activation, "experts_prefill");
+  if (rc) return rc;
   const PrefillLayout need = prefill_layout(nullptr, M, top_k, bank, shared);
   if (!workspace || workspace_bytes < need.bytes)
     return fail(FTMOE_ERR_WORKSPACE, "experts_prefill: workspace %zu < %zu bytes", workspace_bytes, need.bytes);
@@ -712,6 +738,8 @@ int ftmoe_experts_prefill(const void* x, int M, int top_k, const float* topk_w, 
   g.shared_blocks = shared ? (M + bm - 1) / bm : 0;
   g.w = {nullptr, nullptr};
   g.act_kind = activation;
+  g.act_limit = bank->swiglu_limit;
+  g.sh_act_limit = shared ? shared->swiglu_limit : 0.f;
   g.topk_w = topk_w;
 
   // gate_up + SwiGLU -> act

@@ -659,6 +659,7 @@ class Executor {
     constexpr int kTile = 32;
     // pass 1: gate and up rows of (group, 32 rows of I) -> bf16 act
     const int tiles1 = I / kTile;
+    const float lim = j.bank.swiglu_limit;
     parallel(G * tiles1, [&](int u) {
       if (dropped()) return;
       const int g = u / tiles1, i0 = (u % tiles1) * kTile;
@@ -672,7 +673,11 @@ class Executor {
         dot(m, i, xs, nv, gv);
         dot(m, I + i, xs, nv, uv);
         for (int v = 0; v < nv; ++v) {
-          const float g = rb(gv[v]), up = rb(uv[v]);
+          float g = rb(gv[v]), up = rb(uv[v]);
+          if (lim > 0.f) {  // clamped SwiGLU (cpu_moe_ext.cpp:1769-1781)
+            g = std::min(g, lim);
+            up = std::min(std::max(up, -lim), lim);
+          }
           const float a = j.activation == FTMOE_ACT_SILU ? silu(g) : j.activation == FTMOE_ACT_GELU ? gelu(g)
                                                                                                   : gelu_tanh(g);
           if constexpr (BF) act[static_cast<size_t>(rs[v]) * I + i] = f2b(a * up);
@@ -755,6 +760,10 @@ int check_job(const ftmoe_bank* b, const void* x, const float* w, const int32_t*
     return ftmoe::report_error(FTMOE_ERR_UNSUPPORTED, "cpu_experts: bank format/shape");
   if (M <= 0 || k <= 0 || act < FTMOE_ACT_SILU || act > FTMOE_ACT_GELU_TANH)
     return ftmoe::report_error(FTMOE_ERR_UNSUPPORTED, "cpu_experts: M/k/activation");
+  if (!std::isfinite(b->swiglu_limit) || b->swiglu_limit < 0.f)
+    return ftmoe::report_error(FTMOE_ERR_INVALID, "cpu_experts: swiglu_limit (finite, >= 0)");
+  if (b->swiglu_limit > 0.f && act != FTMOE_ACT_SILU)
+    return ftmoe::report_error(FTMOE_ERR_UNSUPPORTED, "cpu_experts: swiglu_limit > 0 needs the silu activation");
   return FTMOE_OK;
 }
 

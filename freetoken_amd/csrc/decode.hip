@@ -810,11 +810,14 @@ __device__ __forceinline__ void tile_epilogue(const DecodeArgs& a, const SegView
   float o[4];
   uint16_t* dst;
   if constexpr (STAGE == 0) {
+    const float lim = sv.shared ? a.sh_act_limit : a.act_limit;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       // gate and up rounded to bf16 by one packed conversion
       const uint32_t gu = pack_bf16x2(g[v] * d.w, u[v] * d.w);
-      o[v] = act_apply(a.act_kind, __uint_as_float(gu << 16)) * __uint_as_float(gu & 0xffff0000u);
+      float gg = __uint_as_float(gu << 16), uu = __uint_as_float(gu & 0xffff0000u);
+      swiglu_clamp(lim, gg, uu);
+      o[v] = act_apply(a.act_kind, gg) * uu;
     }
     dst = a.act + static_cast<size_t>(d.row) * a.act_stride + rows_at;
   } else {

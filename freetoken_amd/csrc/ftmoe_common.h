@@ -78,6 +78,16 @@ __device__ __forceinline__ float act_apply(int act, float g) {
   return 0.5f * g * (1.0f + tanhf(inner));
 }
 
+// Clamped SwiGLU inputs (DeepSeek-V4 ds_fp4, kernel/triton/dsv4/fused_moe.py:121-141):
+// the gate capped at lim and the up value clamped to [-lim, lim]; lim = 0
+// leaves both as they are.
+__device__ __forceinline__ void swiglu_clamp(float lim, float& g, float& u) {
+  if (lim > 0.f) {
+    g = fminf(g, lim);
+    u = fminf(fmaxf(u, -lim), lim);
+  }
+}
+
 // Cross-lane reductions: DPP butterflies inside each 16-lane row (quad_perm
 // xor1 / xor2, row_half_mirror, row_mirror leave every lane of a row with the
 // row's result), then the four row results are combined from readlanes.  This

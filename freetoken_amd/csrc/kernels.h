@@ -67,6 +67,8 @@ struct DecodeArgs {
   uint16_t* ic3;            // [M*k, H] bf16
   uint16_t* sh_out;         // [M, H] bf16
   int act_kind;
+  float act_limit;          // clamped SwiGLU of the routed experts (> 0), else 0
+  float sh_act_limit;       // ... of the shared expert
   int weight_on_input;
 };
 
@@ -105,6 +107,8 @@ size_t align_gcount_ints(int numel, int num_experts);
 hipError_t launch_align_large(const AlignArgs& a, int32_t* gcount, hipStream_t stream);
 hipError_t launch_slot_map(const int32_t* ids, int numel, const int32_t* slot_for_id, int table_size,
                            int32_t* slot_ids, uint8_t* miss_mask, long long* stats, hipStream_t stream);
+hipError_t launch_route_histogram(const int32_t* ids, int numel, int num_experts, long long* freq,
+                                  hipStream_t stream);
 // shared_pieces false: the shared expert's pieces are left out of the grid
 // (its gate_up already ran beside the router, launch_route_shared)
 hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs& a, hipStream_t stream,
@@ -142,6 +146,8 @@ struct PrefillGemmArgs {
   uint16_t* sh_out;         // down: shared out [M, N]
   const float* topk_w;      // [numel] (down)
   int act_kind;
+  float act_limit;          // clamped SwiGLU of the routed experts (> 0), else 0
+  float sh_act_limit;       // ... of the shared expert
 };
 
 // Routes per M block of the prefill GEMMs (the align block size): the

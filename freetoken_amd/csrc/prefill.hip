@@ -416,13 +416,15 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillGemmArgs
     if (route < 0) continue;
     if (GATE_UP) {
       const int arow = shared ? a.numel + route : route;
+      const float lim = shared ? a.sh_act_limit : a.act_limit;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         float o[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float gg = bf16_round(acc[s][i][v]);
-          const float uu = bf16_round(acc[2 + s][i][v]);
+          float gg = bf16_round(acc[s][i][v]);
+          float uu = bf16_round(acc[2 + s][i][v]);
+          swiglu_clamp(lim, gg, uu);
           o[v] = act_apply(a.act_kind, gg) * uu;
         }
         const int n = n0 + 32 * wn + 16 * s + g * 4;
@@ -872,8 +874,10 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
       uint32_t pk[8][2][2];  // bf16 pairs (v0,v1), (v2,v3) of each column tile and gate/up tile pair
       float amax[8];
       // SiLU (every configuration here) runs as straight-line code with its
-      // kind fixed at compile time; the other kinds keep the runtime choice
-      auto swiglu = [&](auto kind) {
+      // kind and the clamp of a clamped SwiGLU fixed at compile time; the other
+      // kinds keep the runtime choice
+      const float lim = t.shared ? a.sh_act_limit : a.act_limit;
+      auto swiglu = [&](auto kind, auto clamp) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           float m = 0.f;
@@ -884,11 +888,15 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
             for (int v4 = 0; v4 < 4; ++v4) {
               // gate and up of one feature rounded to bf16 by one packed conversion
               const uint32_t gu = pack_bf16x2(acc[s2][i][v4], acc[2 + s2][i][v4]);
-              const float gg = __uint_as_float(gu << 16);
+              float gg = __uint_as_float(gu << 16), uu = __uint_as_float(gu & 0xffff0000u);
+              if constexpr (decltype(clamp)::value) {
+                gg = fminf(gg, lim);
+                uu = fminf(fmaxf(uu, -lim), lim);
+              }
               float act;
               if constexpr (decltype(kind)::value == ACT_SILU) act = act_fixed<ACT_SILU>(gg);
               else act = act_apply(a.act_kind, gg);
-              o[v4] = act * __uint_as_float(gu & 0xffff0000u);
+              o[v4] = act * uu;
             }
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -902,8 +910,12 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
           amax[i] = m;
         }
       };
-      if (a.act_kind == ACT_SILU) swiglu(std::integral_constant<int, ACT_SILU>{});
-      else swiglu(std::integral_constant<int, -1>{});
+      if (a.act_kind == ACT_SILU) {
+        if (lim > 0.f) swiglu(std::integral_constant<int, ACT_SILU>{}, std::true_type{});
+        else swiglu(std::integral_constant<int, ACT_SILU>{}, std::false_type{});
+      } else {
+        swiglu(std::integral_constant<int, -1>{}, std::false_type{});
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         if (g == 0) s_amax[rg * kQBM + 128 * ch + 16 * i + r16] = amax[i];

@@ -8,7 +8,10 @@ Differences from the reference, all additive:
     the routed output inside the expert kernels, replacing the model block's
     separate ``out + shared_experts(x)`` (``models/glm4_moe/moe.py:81-82``);
   * FP8 block scales are held as float32 (the reference allocates bf16, which
-    converts exactly).
+    converts exactly);
+  * ``swiglu_limit`` (set through ``make_moe_layer``'s ``extra_attrs``, as the
+    reference's engine does) clamps the SwiGLU of the ds_fp4 experts in both
+    regimes (``layers/moe.py:473,550-573``).
 TP is 1 (one GPU): ``_maybe_all_reduce`` is the identity.
 """
 
@@ -64,6 +67,7 @@ class MoELayer:
         self.apply_router_weight_on_input = apply_router_weight_on_input
         self.weight_format = weight_format
         self.shared_expert: ops.ExpertBank | None = None
+        self.swiglu_limit: float | None = None
         if device is None:
             device = torch.device("cuda", torch.cuda.current_device()) if torch.cuda.is_available() else "cpu"
         self.device = torch.device(device)
@@ -94,7 +98,8 @@ class MoELayer:
             return ops.ExpertBank("fp8_block", self.gate_up_proj, self.down_proj, self.gate_up_scale_inv,
                                   self.down_scale_inv)
         if self.weight_format == "ds_fp4":
-            return ops.ExpertBank("mxfp4", self.gate_up_proj, self.down_proj, self.gate_up_scale, self.down_scale)
+            return ops.ExpertBank("mxfp4", self.gate_up_proj, self.down_proj, self.gate_up_scale, self.down_scale,
+                                  swiglu_limit=float(self.swiglu_limit or 0.0))
         return ops.ExpertBank("bf16", self.gate_up_proj, self.down_proj)
 
     def _maybe_all_reduce(self, hidden_states: torch.Tensor) -> torch.Tensor:
@@ -167,7 +172,7 @@ class OffloadMoELayer(MoELayer):
         self.offload_cache: ExpertSlotCache | None = None
 
     def _views_bank(self, views) -> ops.ExpertBank:
-        return bank_from_views(self.offload_cache.quant_format, views)
+        return bank_from_views(self.offload_cache.quant_format, views, self.swiglu_limit)
 
     def forward(self, hidden_states: torch.Tensor, router_logits: torch.Tensor | None = None):
         topk_weights, topk_ids = fused_topk(hidden_states, router_logits, self.top_k, self.renormalize)
@@ -197,7 +202,7 @@ class OffloadMoELayer(MoELayer):
                                       shared=self.shared_expert, activation=self.activation)
         # ensure_experts without admission (expert ids -> slot ids, in place)
         # fused into the decode call; misses are skipped and counted
-        table, stats = cache.slot_lookup(self.layer_id)
+        table, stats = cache.slot_lookup(self.layer_id, topk_ids)
         return ops.experts_decode(hidden_states, topk_weights, topk_ids, self._views_bank(cache.bank_views()),
                                   shared=self.shared_expert, activation=self.activation, slot_for_id=table,
                                   stats=stats)

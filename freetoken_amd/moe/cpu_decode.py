@@ -33,11 +33,12 @@ def hybrid_fetch_fraction(pcie_gbs: float, cpu_gbs: float, overlapped: bool = Tr
 
 class CpuMoeDecoder:
     def __init__(self, cache: ExpertSlotCache, top_k: int, threads: int = 0, activation: str = "silu",
-                 watchdog_s: float | None = None):
+                 watchdog_s: float | None = None, swiglu_limit: float | None = None):
         assert cache.sources, "the CPU share reads the cache's host sources: set_bank_sources first"
         self.cache = cache
         self.top_k = top_k
         self.activation = activation
+        self.swiglu_limit = swiglu_limit  # the layers' ds_fp4 SwiGLU clamp (cpu_moe_ext.cpp:1769-1781)
         self.executor = ops.CpuExecutor(threads, watchdog_s=watchdog_s)
         self._io: dict[int, dict[str, torch.Tensor]] = {}
         self._banks: dict[int, ops.ExpertBank] = {}
@@ -45,7 +46,7 @@ class CpuMoeDecoder:
     def host_bank(self, layer_id: int) -> ops.ExpertBank:
         bank = self._banks.get(layer_id)
         if bank is None:
-            bank = bank_from_views(self.cache.quant_format, self.cache.host_bank_tensors(layer_id))
+            bank = bank_from_views(self.cache.quant_format, self.cache.host_bank_tensors(layer_id), self.swiglu_limit)
             self._banks[layer_id] = bank
         return bank
 

@@ -6,8 +6,10 @@ Decode keeps bf16 activations (W4A16, the layout's own GEMV numerics,
 activation round trip of the reference's decode (``:119,127``) is not applied.
 Prefill FP8-round-trips both GEMM inputs with per-128 power-of-two scales, as
 ``routed_experts_fp4_prefill`` does (``:181-235``), and runs them on the
-MX-scaled FP8 x FP4 MFMA.  The SwiGLU clamp (``swiglu_limit``) is supported
-only as 0 (no clamp).
+MX-scaled FP8 x FP4 MFMA.  ``swiglu_limit`` > 0 clamps the SwiGLU inputs,
+``silu(min(gate, L)) * clamp(up, -L, L)`` on the bf16 gate and up values
+(``fused_swiglu``, ``kernel/triton/dsv4/fused_moe.py:121-141``), in the gate/up
+epilogue of both regimes; 0 (or None) leaves them unclamped.
 """
 
 from __future__ import annotations
@@ -17,13 +19,11 @@ import torch
 from .. import ops
 
 
-def _bank(gu_p, gu_s, dn_p, dn_s) -> ops.ExpertBank:
-    return ops.ExpertBank("mxfp4", gu_p, dn_p, gu_s.view(torch.uint8), dn_s.view(torch.uint8))
-
-
-def _check_limit(swiglu_limit: float) -> None:
-    if swiglu_limit and swiglu_limit > 0:
-        raise ValueError("swiglu_limit > 0 is not supported by the gfx950 ds_fp4 path")
+def _bank(gu_p, gu_s, dn_p, dn_s, swiglu_limit) -> ops.ExpertBank:
+    lim = float(swiglu_limit or 0.0)
+    if not lim >= 0.0 or lim == float("inf"):
+        raise ValueError(f"swiglu_limit must be finite and >= 0, got {swiglu_limit!r}")
+    return ops.ExpertBank("mxfp4", gu_p, dn_p, gu_s.view(torch.uint8), dn_s.view(torch.uint8), swiglu_limit=lim)
 
 
 def routed_experts_fp4(
@@ -38,9 +38,9 @@ def routed_experts_fp4(
     shared: ops.ExpertBank | None = None,
 ) -> torch.Tensor:
     """Decode: routed output summed over the top-k routes (+ shared expert)."""
-    _check_limit(swiglu_limit)
     return ops.experts_decode(x, topk_weights, slots,
-                              _bank(gate_up_packed, gate_up_scale, down_packed, down_scale), shared=shared)
+                              _bank(gate_up_packed, gate_up_scale, down_packed, down_scale, swiglu_limit),
+                              shared=shared)
 
 
 def routed_experts_fp4_prefill(
@@ -56,8 +56,8 @@ def routed_experts_fp4_prefill(
     shared: ops.ExpertBank | None = None,
 ) -> torch.Tensor:
     """Prefill: grouped MX-scaled MFMA over the first ``num_rows`` bank rows."""
-    _check_limit(swiglu_limit)
-    bank = _bank(gate_up_packed[:num_rows], gate_up_scale[:num_rows], down_packed[:num_rows], down_scale[:num_rows])
+    bank = _bank(gate_up_packed[:num_rows], gate_up_scale[:num_rows], down_packed[:num_rows], down_scale[:num_rows],
+                 swiglu_limit)
     return ops.experts_prefill(x, topk_weights, slots, bank, shared=shared)
 
 

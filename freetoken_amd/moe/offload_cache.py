@@ -22,6 +22,7 @@ from __future__ import annotations
 
 from collections import OrderedDict
 
+import numpy as np
 import torch
 
 from .. import ops
@@ -30,15 +31,19 @@ STAT_ACTIVE, STAT_MISS, STAT_CALLS, STAT_MISSED_ROUTES = range(4)
 N_STATS = 4
 
 
-def bank_from_views(quant_format: str, views) -> ops.ExpertBank:
+def bank_from_views(quant_format: str, views, swiglu_limit: float | None = None) -> ops.ExpertBank:
     """An ``ExpertBank`` over bank tensors in registration order: (gate_up,
-    down) for bf16, (gate_up, gate_up_scale, down, down_scale) otherwise."""
+    down) for bf16, (gate_up, gate_up_scale, down, down_scale) otherwise.
+    ``swiglu_limit`` (the layer's DeepSeek-V4 SwiGLU clamp) applies to the
+    ds_fp4 format, as the reference passes it to ``routed_experts_fp4`` only
+    (``layers/moe.py:556-573``)."""
     if quant_format == "bf16":
         gate_up, down = views
         return ops.ExpertBank("bf16", gate_up, down)
     gate_up, gate_up_scale, down, down_scale = views
-    return ops.ExpertBank("fp8_block" if quant_format == "fp8_block" else "mxfp4", gate_up, down, gate_up_scale,
-                          down_scale)
+    if quant_format == "fp8_block":
+        return ops.ExpertBank("fp8_block", gate_up, down, gate_up_scale, down_scale)
+    return ops.ExpertBank("mxfp4", gate_up, down, gate_up_scale, down_scale, swiglu_limit=float(swiglu_limit or 0.0))
 
 
 class ExpertSlotCache:
@@ -84,6 +89,11 @@ class ExpertSlotCache:
         self.id_of_slot = torch.full((cache_size,), -1, dtype=torch.int32, device=self.device)
         self.collect_stats = True
         self.lru_stats = torch.zeros((num_layers, N_STATS), dtype=torch.int64, device=self.device)
+        # opt-in decode routing histogram per (layer, expert), for cache-skew
+        # analysis (:230-236): counted on the device from the raw expert ids
+        # before their rewrite to slots, so replayed graphs keep counting
+        self.collect_decode_freq = False
+        self.decode_freq = torch.zeros((num_layers, num_experts), dtype=torch.int64, device=self.device)
         # misses left without a slot because every slot held an expert of the same call
         self.unserved = torch.zeros((num_layers,), dtype=torch.int64, device=self.device)
         self.banks: "OrderedDict[str, torch.Tensor]" = OrderedDict()
@@ -171,6 +181,7 @@ class ExpertSlotCache:
         first, into the least recently used slots) and staged for
         ``copy_missing``; without, they map to -1 (``miss_mask`` marks them)."""
         stats = self.lru_stats[layer_id] if self.collect_stats else None
+        self.note_decode_routing(layer_id, expert_ids)
         if not self.sources:
             ops.slot_map(expert_ids, self.slot_for_id[layer_id], out=expert_ids, miss_mask=miss_mask, stats=stats)
             return expert_ids
@@ -188,6 +199,7 @@ class ExpertSlotCache:
         ``cpu_ids``, are listed there by expert id for the CPU."""
         assert self.sources, "set_bank_sources must register the host banks first"
         stats = self.lru_stats[layer_id] if self.collect_stats else None
+        self.note_decode_routing(layer_id, expert_ids)
         rec = self.expert_recency[layer_id] if by_recency else None
         max_fetch = self.hybrid_max_fetch if max_fetch is None else max_fetch
         frac = self.hybrid_fetch_fraction if fetch_fraction is None else fetch_fraction
@@ -338,11 +350,22 @@ class ExpertSlotCache:
         self._pf_has_release[buf] = True
         self._pf_released[buf] = True
 
-    def slot_lookup(self, layer_id: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+    def slot_lookup(self, layer_id: int,
+                    expert_ids: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
         """(slot table, stats counters or None) of a layer, for decode calls that
         do the ``ensure_experts`` rewrite themselves (``ops.experts_decode``
-        with ``slot_for_id``)."""
+        with ``slot_for_id``); ``expert_ids``, the call's raw ids, feed the
+        routing histogram as ``ensure_experts`` would."""
+        if expert_ids is not None:
+            self.note_decode_routing(layer_id, expert_ids)
         return self.slot_for_id[layer_id], (self.lru_stats[layer_id] if self.collect_stats else None)
+
+    def note_decode_routing(self, layer_id: int, expert_ids: torch.Tensor) -> None:
+        """Adds a decode step's raw expert ids to the layer's routing histogram
+        when ``collect_decode_freq`` is on (``:803-807``): one small device
+        launch, no host synchronisation."""
+        if self.collect_decode_freq:
+            ops.route_histogram(expert_ids.reshape(-1), self.decode_freq[layer_id])
 
     # -------------------------------------------------------------- statistics
     def reset_stats(self) -> None:
@@ -362,6 +385,42 @@ class ExpertSlotCache:
         """Share of the layers' experts the hit/miss split gathered device to
         device since construction (the counters of ``:275-276,729``)."""
         return self.prefill_hit_rows / self.prefill_total_rows if self.prefill_total_rows else 0.0
+
+    def decode_routing_stats(self) -> dict:
+        """Per-layer routing concentration of the decode histogram
+        (``decode_routing_stats``, ``:936-966``; same keys and definitions),
+        averaged over the layers that saw routes: the working set (experts
+        routed at least once), the experts covering 90% of the routes, the
+        best hit rate a per-layer cache of ``cache_size / num_layers`` slots
+        holding the most frequent experts could reach on this distribution,
+        and the routing entropy normalised by log(E).  Reads the histogram
+        back to the host once."""
+        freq = self.decode_freq.detach().to("cpu", torch.float64).numpy()
+        total = freq.sum(axis=1)
+        valid = total > 0
+        if not valid.any():
+            return {}
+        f, tot = freq[valid], total[valid]
+        slots_per_layer = self.cache_size / self.num_layers
+        c = max(1, int(round(slots_per_layer)))
+        ranked = -np.sort(-f, axis=1)
+        share = ranked / tot[:, None]
+        cover90 = (np.cumsum(share, axis=1) < 0.9).sum(axis=1) + 1
+        p = f / tot[:, None]
+        with np.errstate(divide="ignore", invalid="ignore"):
+            ent = -np.where(p > 0, p * np.log(p), 0.0).sum(axis=1)
+        working = (f > 0).sum(axis=1)
+        return {
+            "slots_per_layer": slots_per_layer,
+            "working_set_mean": float(working.mean()),
+            "working_set_max": int(working.max()),
+            "experts_for_90pct": float(cover90.mean()),
+            "oracle_hit_at_slots": float((ranked[:, :c].sum(axis=1) / tot).mean()),
+            "norm_entropy": float((ent / np.log(self.num_experts)).mean()),
+        }
+
+    def reset_decode_freq(self) -> None:
+        self.decode_freq.zero_()
 
     def decode_miss_stats(self) -> dict:
         active, missing, calls, missed_routes = (int(x) for x in self.lru_stats.sum(0))

@@ -125,6 +125,17 @@ def slot_map(topk_ids: torch.Tensor, slot_for_id: torch.Tensor, out: torch.Tenso
     return out
 
 
+def route_histogram(topk_ids: torch.Tensor, freq: torch.Tensor) -> torch.Tensor:
+    """freq[e] += count of e in ``topk_ids`` (int32; ids outside [0, len(freq))
+    skipped); ``freq`` int64 [E] accumulates on the device (see ftmoe_route_histogram)."""
+    if topk_ids.dtype != torch.int32 or freq.dtype != torch.int64:
+        raise ValueError("topk_ids must be int32 and freq int64")
+    _require_gpu(topk_ids, freq)
+    check(lib().ftmoe_route_histogram(_ptr(topk_ids), topk_ids.numel(), freq.numel(), _ptr(freq),
+                                      _stream(topk_ids.device)), "route_histogram")
+    return freq
+
+
 def lru_ensure(expert_ids: torch.Tensor, layer_id: int, slot_for_id: torch.Tensor, id_of_slot: torch.Tensor,
                usage: torch.Tensor, step: torch.Tensor, evict_slots: torch.Tensor, src_indices: torch.Tensor,
                num_indices: torch.Tensor, num_missing: torch.Tensor, recency: torch.Tensor | None = None,
@@ -290,6 +301,9 @@ class ExpertBank:
     (or bf16, converted once) 128x128 block scales.
     fmt "mxfp4": uint8 packed [S,2I,H/2] / [S,H,I/2] with uint8 e8m0 scales
     [S,2I,H/32] / [S,H,I/32].
+    ``swiglu_limit`` > 0 makes the activation the clamped SwiGLU
+    ``silu(min(gate, L)) * clamp(up, -L, L)`` (DeepSeek-V4's experts,
+    ``moe/fused_ds_fp4.py:105-124``); 0 leaves it unclamped.
     """
 
     fmt: str
@@ -297,6 +311,7 @@ class ExpertBank:
     down: torch.Tensor
     gate_up_scale: torch.Tensor | None = None
     down_scale: torch.Tensor | None = None
+    swiglu_limit: float = 0.0
 
     def __post_init__(self):
         if self.fmt not in _FORMATS:
@@ -332,6 +347,7 @@ class ExpertBank:
         return _lib.FtmoeBank(
             _FORMATS[self.fmt], self.num_rows, self.hidden, self.inter,
             self.gate_up.data_ptr(), _ptr(self.gate_up_scale), self.down.data_ptr(), _ptr(self.down_scale),
+            float(self.swiglu_limit or 0.0),
         )
 
     def cstruct(self) -> _lib.FtmoeBank:
@@ -339,6 +355,7 @@ class ExpertBank:
         return _lib.FtmoeBank(
             _FORMATS[self.fmt], self.num_rows, self.hidden, self.inter,
             _ptr(self.gate_up), _ptr(self.gate_up_scale), _ptr(self.down), _ptr(self.down_scale),
+            float(self.swiglu_limit or 0.0),
         )
 
 

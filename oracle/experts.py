@@ -146,15 +146,18 @@ def act_roundtrip_ue8m0(x, block: int = BLK):
 
 
 class Bank:
-    """One expert bank (routed experts or the shared expert, S = 1)."""
+    """One expert bank (routed experts or the shared expert, S = 1).
+    ``swiglu_limit`` > 0: the bank's experts use the clamped SwiGLU
+    (``swiglu``)."""
 
-    def __init__(self, fmt: str, gate_up, down, gate_up_scale=None, down_scale=None):
+    def __init__(self, fmt: str, gate_up, down, gate_up_scale=None, down_scale=None, swiglu_limit: float = 0.0):
         assert fmt in ("bf16", "fp8", "mxfp4"), fmt
         self.fmt = fmt
         self.gate_up = gate_up
         self.down = down
         self.gate_up_scale = gate_up_scale
         self.down_scale = down_scale
+        self.swiglu_limit = float(swiglu_limit)
 
     def weights(self, which: str, e: int):
         w = self.gate_up if which == "gate_up" else self.down
@@ -203,10 +206,27 @@ def _gemm(regime: str, fmt: str, x, w, s):
     return act_roundtrip_ue8m0(x) @ dequant_mxfp4(w, s).T
 
 
+def swiglu(activation: str, g, u, limit: float = 0.0):
+    """float32 act(g) * u of the bf16 gate and up values.  With ``limit`` L > 0
+    the DeepSeek-V4 clamped form: act(min(g, L)) * clamp(u, -L, L)
+    (``_swiglu_kernel``, ``kernel/triton/dsv4/fused_moe.py:121-141``, used by
+    ``routed_experts_fp4`` / ``routed_experts_fp4_prefill``,
+    ``moe/fused_ds_fp4.py:124,226``; the CPU pass ``cpu_moe_ext.cpp:1769-1781``).
+    The gate is capped from above only."""
+    g = np.asarray(g, dtype=np.float32)
+    u = np.asarray(u, dtype=np.float32)
+    if limit > 0:
+        lim = F32(limit)
+        g = np.minimum(g, lim)
+        u = np.minimum(np.maximum(u, -lim), lim)
+    return (act_f32(activation, g) * u).astype(np.float32)
+
+
 def expert_mlp(regime: str, bank: Bank, e: int, x_rows, route_w=None, weight_on_input: bool = False,
                activation: str = "silu"):
     """One expert on a set of rows: bf16(down(bf16(act(g)*u)) * w), act = silu
-    unless ``activation`` names gelu or gelu_tanh (``kernel/triton/activation.py:68-112``).
+    unless ``activation`` names gelu or gelu_tanh (``kernel/triton/activation.py:68-112``),
+    clamped as ``swiglu`` when the bank has a ``swiglu_limit``.
 
     With ``weight_on_input`` the router weight scales the gate_up output before
     its bf16 rounding instead of the down output (``MUL_ROUTED_WEIGHT`` on the
@@ -218,7 +238,7 @@ def expert_mlp(regime: str, bank: Bank, e: int, x_rows, route_w=None, weight_on_
         g = (g * np.asarray(route_w, dtype=np.float32)[:, None]).astype(np.float32)
     g = bf16_round(g)
     inter = g.shape[1] // 2
-    act = bf16_round(act_f32(activation, g[:, :inter]) * g[:, inter:])
+    act = bf16_round(swiglu(activation, g[:, :inter], g[:, inter:], bank.swiglu_limit))
     d = _gemm(regime, bank.fmt, act, w2, s2)
     if route_w is not None and not weight_on_input:
         d = (d * np.asarray(route_w, dtype=np.float32)[:, None]).astype(np.float32)

@@ -40,8 +40,9 @@ def to_device_bank(bank: Bank, dev, rows=None) -> ExpertBank:
         x = torch.from_numpy(np.ascontiguousarray(a[sl])).to(dev)
         return x.to(dtype) if dtype is not None else x
 
+    lim = getattr(bank, "swiglu_limit", 0.0)
     if bank.fmt == "bf16":
-        return ExpertBank("bf16", t(bank.gate_up, torch.bfloat16), t(bank.down, torch.bfloat16))
+        return ExpertBank("bf16", t(bank.gate_up, torch.bfloat16), t(bank.down, torch.bfloat16), swiglu_limit=lim)
     if bank.fmt == "fp8":
         return ExpertBank(
             "fp8_block",
@@ -49,8 +50,10 @@ def to_device_bank(bank: Bank, dev, rows=None) -> ExpertBank:
             t(bank.down).view(torch.float8_e4m3fn),
             t(bank.gate_up_scale),
             t(bank.down_scale),
+            swiglu_limit=lim,
         )
-    return ExpertBank("mxfp4", t(bank.gate_up), t(bank.down), t(bank.gate_up_scale), t(bank.down_scale))
+    return ExpertBank("mxfp4", t(bank.gate_up), t(bank.down), t(bank.gate_up_scale), t(bank.down_scale),
+                      swiglu_limit=lim)
 
 
 def bf16_dev(a, dev) -> torch.Tensor:
@@ -66,4 +69,5 @@ def to_np(t: torch.Tensor) -> np.ndarray:
 def sub_bank(bank: Bank, rows) -> Bank:
     """Rows of a bank (e.g. the resident experts of a slot cache)."""
     f = (lambda a: None if a is None else np.ascontiguousarray(a[rows]))
-    return Bank(bank.fmt, f(bank.gate_up), f(bank.down), f(bank.gate_up_scale), f(bank.down_scale))
+    return Bank(bank.fmt, f(bank.gate_up), f(bank.down), f(bank.gate_up_scale), f(bank.down_scale),
+                getattr(bank, "swiglu_limit", 0.0))

@@ -227,3 +227,31 @@ def test_close_returns_when_the_pool_is_wedged():
         time.sleep(0.05)
     ops._KEPT_EXECUTORS.remove(h)
     assert (y == 7).all()  # the abandoned job wrote no row of y
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "fp8"])
+@pytest.mark.parametrize("lim", [0.0, 7.0, 0.75])
+def test_cpu_experts_swiglu_limit(executor, fmt, lim):
+    """The clamped SwiGLU of the CPU pass (reference cpu_moe_ext.cpp:1769-1781)
+    against the oracle: the bank's limit binds at 0.75 and hardly at 7."""
+    rng = np.random.default_rng(91 + int(lim * 4))
+    E, H, I, M, k = 6, 512, 256, 3, 4
+    bank = synth.make_bank(fmt, E, H, I, rng)
+    bank.swiglu_limit = lim
+    x = synth.activations(rng, M, H)
+    w, ids = oracle.routing.softmax_topk(synth.normal(rng, (M, E)), k, True)
+    y_ref = oracle.experts.moe_layer("decode", x, w, ids, bank, None)
+    y = executor.run(to_device_bank(bank, "cpu"), _host(x, np.float32).to(torch.bfloat16), _host(w, np.float32),
+                     _host(ids, np.int32))
+    g = y.float().numpy()
+    assert max_rel(g, y_ref) <= MAX_REL_TOL and cosine(g, y_ref) >= COS_TOL, (fmt, lim, max_rel(g, y_ref))
+    with pytest.raises(ValueError, match="silu"):
+        executor.run(to_device_bank(bank, "cpu") if lim > 0 else _limited(bank, "cpu"),
+                     _host(x, np.float32).to(torch.bfloat16), _host(w, np.float32), _host(ids, np.int32),
+                     activation="gelu")
+
+
+def _limited(bank, dev):
+    b = to_device_bank(bank, dev)
+    b.swiglu_limit = 1.0
+    return b

@@ -160,3 +160,46 @@ def test_cpu_executor_restatement_matches_oracle():
         y = (cpu.run(bf16_bits(x), w, ids).astype(np.uint32) << 16).view(np.float32)
         cpu.close()
         assert max_rel(y, y_ref) < 2e-2 and cosine(y, y_ref) > 0.9995, fmt
+
+
+def test_swiglu_clamp_special_cases():
+    """The clamped SwiGLU (limit L): the gate is capped from above only, the up
+    value clamped on both sides; values inside [-L, L] pass unchanged; L = 0 is
+    the plain SwiGLU.  Expected values from float64 closed forms."""
+    import math
+
+    def silu64(v):
+        return v / (1.0 + math.exp(-v))
+
+    L = 7.0
+    g = np.array([20.0, -20.0, 3.0, 7.0, 6.5, -3.0], np.float32)
+    u = np.array([10.0, -10.0, -2.0, 8.0, -9.0, 7.5], np.float32)
+    want = [silu64(7.0) * 7.0, silu64(-20.0) * -7.0, silu64(3.0) * -2.0, silu64(7.0) * 7.0, silu64(6.5) * -7.0,
+            silu64(-3.0) * 7.0]
+    got = X.swiglu("silu", g, u, L)
+    np.testing.assert_allclose(got, np.array(want), rtol=2e-6, atol=1e-30)
+    plain = X.swiglu("silu", g, u, 0.0)
+    np.testing.assert_allclose(plain, [silu64(float(a)) * float(b) for a, b in zip(g, u)], rtol=2e-6, atol=1e-30)
+    # a limit above every |value| changes nothing, bit for bit
+    np.testing.assert_array_equal(X.swiglu("silu", g, u, 1e30), plain)
+
+
+def test_identity_expert_with_clamped_swiglu():
+    """gate = x, up = 2x through identity weights: the layer reduces to
+    bf16(bf16(silu(min(x, L)) * clamp(2x, -L, L))), which fails if the clamp
+    is applied to the wrong half or before the bf16 rounding of gate and up is
+    lost; the router weight scales the down output after it."""
+    h = 128
+    eye = np.eye(h, dtype=np.float32)
+    rng = np.random.default_rng(61)
+    x = bf16_round(synth.activations(rng, 3, h) * np.float32(4.0))
+    for L in (0.0, 1.5, 7.0):
+        bank = X.Bank("bf16", np.concatenate([eye, 2 * eye])[None], eye[None], swiglu_limit=L)
+        y = X.moe_layer("decode", x, np.ones((3, 1), np.float32), np.zeros((3, 1), np.int32), bank)
+        g, u = x.astype(np.float64), 2.0 * x.astype(np.float64)
+        if L > 0:
+            g, u = np.minimum(g, L), np.clip(u, -L, L)
+        act = bf16_round((g / (1.0 + np.exp(-g)) * u).astype(np.float32))
+        np.testing.assert_allclose(y, bf16_round(act), rtol=2 ** -7, atol=0)
+        if L == 1.5:
+            assert (np.abs(2 * x) > L).mean() > 0.3  # the clamp binds on many values

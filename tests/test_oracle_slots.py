@@ -216,3 +216,26 @@ def test_release_slots_unmaps():
     assert (st.id_of_slot[4:9] == -1).all() and (st.usage[4:9] == 0).all()
     assert st.slot_for_id[0].tolist() == [0, 1, 2, 3, -1, -1, -1, -1]
     assert st.slot_for_id[1, 3] == -1 and st.slot_for_id[1, 4] == 9
+
+
+def test_decode_routing_stats_closed_forms():
+    """ExpertSlotCache.decode_routing_stats (reference moe/offload_cache.py:936-966)
+    on hand-built histograms: a uniform layer (entropy log E, 90% of the routes
+    on 15 of 16 experts, hit rate slots/E), a one-expert layer (entropy 0, one
+    expert covers everything) and an unrouted layer that takes no part."""
+    import torch
+
+    from freetoken_amd.moe.offload_cache import ExpertSlotCache
+
+    cache = ExpertSlotCache(3, 16, 12, "fp8_block", device="cpu")
+    assert cache.decode_routing_stats() == {}
+    cache.decode_freq[0] = 3
+    cache.decode_freq[1, 5] = 40
+    st = cache.decode_routing_stats()
+    assert st["slots_per_layer"] == 4.0
+    assert st["working_set_mean"] == 8.5 and st["working_set_max"] == 16
+    assert st["experts_for_90pct"] == 8.0  # (15 + 1) / 2
+    assert abs(st["oracle_hit_at_slots"] - (4 / 16 + 1.0) / 2) < 1e-12
+    assert abs(st["norm_entropy"] - 0.5) < 1e-12
+    cache.reset_decode_freq()
+    assert int(cache.decode_freq.sum()) == 0 and isinstance(cache.decode_freq, torch.Tensor)
