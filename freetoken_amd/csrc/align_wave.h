@@ -99,6 +99,90 @@ __device__ __forceinline__ void align_wave(const AlignArgs& a, const int32_t* id
 }
 
 
+// ----------------------------------------------------------------------------
+// One-wave align by counting (the outputs of align_wave, at most 64 routes):
+// lane i takes route i; one pass over the call's routes (their keys read
+// with readlane, uniform j) counts, for every route, the valid routes whose
+// (expert, route) key sorts before its own (its position), those of smaller
+// experts (the start of its expert's run) and those of its own expert (the
+// run's length); a second pass numbers the segment heads by position.  The
+// counters' distinct experts come from the same first pass (first occurrence
+// of an id).  No cross-lane sort: the dependent chain is two loops of
+// independent compares, numel iterations each.  pre_slot (nullable, LDS): the
+// slot of each route's id when the caller already looked it up.
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ void align_rank_wave(const AlignArgs& a, const int32_t* ids,
+                                                const int32_t* pre_slot = nullptr) {
+  const int lane = lane_id();
+  const int n = a.numel;
+  const int eff = a.num_experts + 1;
+  int e = -1, id = -1;
+  bool idv = false, miss = false;
+  if (lane < n) {
+    e = ids[lane];
+    if (a.slot_for_id) {
+      id = e;
+      idv = e >= 0 && e < a.table_size;
+      const int s = idv ? (pre_slot ? pre_slot[lane] : a.slot_for_id[e]) : -1;
+      if (a.slot_ids) a.slot_ids[lane] = s;
+      if (a.miss_mask) a.miss_mask[lane] = (idv && s < 0) ? 1 : 0;
+      miss = idv && s < 0;
+      e = s;
+    }
+  }
+  const bool valid = lane < n && e >= 0 && e < eff;
+  // (expert << 6 | route): unique per valid route; invalid routes sort last
+  const uint32_t key = valid ? (static_cast<uint32_t>(e) << 6) | static_cast<uint32_t>(lane) : 0xFFFFFFFFu;
+  const uint32_t ex = key >> 6;
+  const uint32_t idk = idv ? static_cast<uint32_t>(id) : 0xFFFFFFFFu;
+  int pos = 0, before = 0, same = 0, dup = 0;
+  for (int j = 0; j < n; ++j) {
+    const uint32_t kj = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), j));
+    const uint32_t xj = kj >> 6;
+    pos += kj < key;
+    before += xj < ex;
+    same += xj == ex;
+    if (a.stats) {
+      const uint32_t ij = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(idk), j));
+      dup += (j < lane) && ij == idk;
+    }
+  }
+  if (valid) a.sorted_ids[pos] = lane;
+  const unsigned long long pmask = __ballot(valid);
+  if (lane == 0) a.ntpp[0] = __popcll(pmask);
+  if (a.seg_expert) {
+    const bool head = valid && e < a.num_experts && (pos - before) % a.seg_cap == 0;
+    const unsigned long long hmask = __ballot(head);
+    int si = 0;
+    for (unsigned long long m = hmask; m; m &= m - 1) {
+      const int j = __ffsll(static_cast<long long>(m)) - 1;
+      si += __builtin_amdgcn_readlane(pos, j) < pos;
+    }
+    if (head) {
+      a.seg_expert[si] = e;
+      a.seg_start[si] = pos;
+      a.seg_count[si] = min(a.seg_cap, same - (pos - before));
+    }
+    if (lane == 0) a.n_seg[0] = __popcll(hmask);
+  }
+  if (a.stats) {
+    unsigned long long t_act = 0, t_miss = 0, t_missed = 0;
+    if (a.slot_for_id) {
+      const bool first = idv && dup == 0;
+      t_act = __popcll(__ballot(first));
+      t_miss = __popcll(__ballot(first && miss));
+      t_missed = __popcll(__ballot(miss));
+    }
+    auto* st = reinterpret_cast<unsigned long long*>(a.stats);
+    if (lane == 0) {
+      if (t_act) atomicAdd(st + 0, t_act);
+      if (t_miss) atomicAdd(st + 1, t_miss);
+      if (t_missed) atomicAdd(st + 3, t_missed);
+      atomicAdd(st + 2, 1ull);
+    }
+  }
+}
+
 // Whether a call qualifies for the one-wave align.
 inline bool align_fits_wave(const AlignArgs& a) {
   return a.numel <= kWave && a.block_size == 1 && a.max_padded == 0 && !a.expert_ids && !a.cum_out &&
