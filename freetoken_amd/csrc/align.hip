@@ -385,7 +385,7 @@ hipError_t launch_align_large(const AlignArgs& a, int32_t* gcount, hipStream_t s
 }
 
 // One-wave align for decode-sized calls (align_wave.h).
-__global__ void __launch_bounds__(kWave) align_wave_kernel(AlignArgs a) { align_wave(a, a.ids); }
+__global__ void __launch_bounds__(kWave) align_wave_kernel(AlignArgs a) { align_small(a, a.ids); }
 
 // ----------------------------------------------------------------------------
 // Decode-form align for banks of many rows (an expert cache of thousands of

@@ -1157,7 +1157,7 @@ route_shared_kernel(RouteArgs r, AlignArgs al, DecodeArgs a) {
       if (lane < r.k) s_ids[wave * r.k + lane] = id;
     }
     __syncthreads();
-    if (wave == 0) align_wave(al, s_ids);
+    if (wave == 0) align_small(al, s_ids);
     return;
   }
   decode_stage_block<FS, FS, 0, kSharedRT, kSharedKS>(a, blockIdx.x - 1, 0, 1, smem);

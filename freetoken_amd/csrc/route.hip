@@ -101,7 +101,7 @@ __global__ void __launch_bounds__(kFrontWaves * kWave) route_align_kernel(RouteA
     if (lane < r.k) s_ids[tok * r.k + lane] = id;
   }
   __syncthreads();
-  if (wave == 0) align_wave(a, s_ids);
+  if (wave == 0) align_small(a, s_ids);
 }
 
 template <int GROUPED, typename T, int PER>
