@@ -103,6 +103,8 @@ SIGNATURES = {
     "ftmoe_cpu_executor_create": (_vp, [_i]),
     "ftmoe_cpu_executor_destroy": (_i, [_vp, _i]),
     "ftmoe_cpu_executor_healthy": (_i, [_vp]),
+    "ftmoe_cpu_executor_set_handshake": (_i, [_vp, _i]),
+    "ftmoe_cpu_executor_handshake": (_i, [_vp]),
     "ftmoe_cpu_executor_set_watchdog": (None, [_vp, _i]),
     "ftmoe_cpu_executor_hold": (None, [_vp, _i]),
     "ftmoe_cpu_executor_isa": (ctypes.c_char_p, [_vp]),

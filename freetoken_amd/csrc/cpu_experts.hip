@@ -22,6 +22,17 @@
 // once, "wait" blocks the stream until the job is done -- so the CPU work
 // overlaps whatever the stream runs between them (the GPU's share of the
 // layer), and both nodes replay in a captured graph.
+//
+// Flag handshake (set_handshake(1), the reference's default where stream
+// memory operations work, moe/cpu_executor.py:32-50): "submit" is a stream
+// write of the job's ready flag (mapped pinned memory), a coordinator thread
+// polls the flags of the armed jobs and hands a ready job to the driver, the
+// driver raises the job's done flag when it ends, and "wait" is a stream wait
+// on that flag followed by its reset -- no host function, so no runtime
+// callback round trip.  The coordinator also runs the watchdog of these jobs
+// (their waits are on the GPU, not in a host function): a job without pool
+// progress for the watchdog period is failed and its done flag raised, so a
+// stream never waits for ever.
 #include <hip/hip_runtime.h>
 #include <immintrin.h>
 #include <pthread.h>
@@ -355,6 +366,10 @@ class Executor;
 
 struct Job {
   Executor* ex;
+  int slot = -1;           // flag handshake: this record's flag slot (fixed for its life)
+  bool flagged = false;    // the current use rides the flag handshake
+  bool armed = false;      // flag handshake: the coordinator watches the ready flag
+  bool started = false;    // flag handshake: handed to the driver, not yet done
   ftmoe_bank bank;  // host pointers
   const bf16* x;    // [M, H]
   const float* w;   // [M, k]
@@ -399,8 +414,84 @@ class Executor {
     cv_work_.notify_all();
     driver_.join();
     for (auto& t : workers_) t.join();
+    if (coord_.joinable()) coord_.join();
+    if (flags_) {
+      // release any wait still enqueued on a stream (callers synchronise first)
+      for (int s = 0; s < kFlagSlots; ++s) flag_store(done_flag(s), 1);
+      (void)hipHostFree(flags_);
+    }
     for (Job* j : jobs_) delete j;
   }
+
+  // ---- flag handshake ------------------------------------------------------
+  static constexpr int kFlagSlots = 256;
+  // Turns the flag handshake on after a functional probe of stream memory
+  // operations on a private stream of the current device (write seen by the
+  // host, wait on a host write, and the same under graph capture); returns 0,
+  // or FTMOE_ERR_UNSUPPORTED with the host-function handshake kept.
+  int enable_flags() {
+    std::lock_guard<std::mutex> g(flag_mu_);
+    if (flags_) return 0;
+    int dev = 0, can = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&can, hipDeviceAttributeCanUseStreamWaitValue, dev) != hipSuccess || !can)
+      return FTMOE_ERR_UNSUPPORTED;
+    void* host = nullptr;
+    const size_t bytes = (2 * kFlagSlots + 16) * sizeof(uint64_t);
+    if (hipHostMalloc(&host, bytes, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
+      return FTMOE_ERR_UNSUPPORTED;
+    std::memset(host, 0, bytes);
+    void* devp = nullptr;
+    if (hipHostGetDevicePointer(&devp, host, 0) != hipSuccess || !devp) {
+      (void)hipHostFree(host);
+      return FTMOE_ERR_UNSUPPORTED;
+    }
+    flags_ = static_cast<uint64_t*>(host);
+    dflags_ = static_cast<uint64_t*>(devp);
+    if (!probe_flags()) {
+      // a probe stream that may still wait is left as it is (never reused)
+      flags_ = nullptr;
+      dflags_ = nullptr;
+      if (!probe_hung_) (void)hipHostFree(host);
+      return FTMOE_ERR_UNSUPPORTED;
+    }
+    slot_job_.assign(kFlagSlots, nullptr);
+    coord_ = std::thread([this] { coordinate(); });
+    return 0;
+  }
+  bool flags_on() const { return flags_ != nullptr && use_flags_; }
+  void use_flags(bool on) { use_flags_ = on; }
+  bool flags_capturable() const { return flags_capturable_; }
+  // Binds a flag slot to the record (kept for its life); false when none is left.
+  bool bind_slot(Job* j) {
+    std::lock_guard<std::mutex> g(m_);
+    if (j->slot >= 0) return true;
+    for (int s = 0; s < kFlagSlots; ++s)
+      if (!slot_job_[s]) {
+        slot_job_[s] = j;
+        j->slot = s;
+        nslots_.store(std::max(nslots_.load(), s + 1));
+        return true;
+      }
+    return false;
+  }
+  // a submit that failed to enqueue: the record goes back unused
+  void disarm(Job* j) {
+    std::lock_guard<std::mutex> g(m_);
+    j->armed = false;
+    j->flagged = false;
+    if (!j->permanent) free_.push_back(j);
+  }
+  // submit side: the record waits for its ready flag (the coordinator polls it)
+  void arm(Job* j) {
+    std::lock_guard<std::mutex> g(m_);
+    j->flagged = true;
+    j->done = false;
+    j->failed = false;
+    j->armed = true;
+  }
+  uint64_t* ready_dev(const Job* j) const { return dflags_ + j->slot; }
+  uint64_t* done_dev(const Job* j) const { return dflags_ + kFlagSlots + j->slot; }
   // Jobs captured into graphs: their records are replayed by the graphs, so
   // the executor must outlive them.
   int captured_jobs() {
@@ -461,6 +552,9 @@ class Executor {
       jobs_.push_back(j);
     }
     j->ex = this;
+    j->flagged = false;
+    j->armed = false;
+    j->started = false;
     j->permanent = permanent;
     if (permanent) ++captured_;
     return j;
@@ -469,17 +563,22 @@ class Executor {
   void start(Job* j) {
     {
       std::lock_guard<std::mutex> g(m_);
-      if (unhealthy_.load()) {
-        j->done = true;
-        j->failed = true;
-      } else {
-        j->done = false;
-        j->failed = false;
-        queue_.push_back(j);
-      }
+      start_locked(j);
     }
     cv_job_.notify_all();
     cv_done_.notify_all();
+  }
+  void start_locked(Job* j) {
+    if (unhealthy_.load()) {
+      j->done = true;
+      j->failed = true;
+      if (j->flagged) flag_store(done_flag(j->slot), 1);
+    } else {
+      j->done = false;
+      j->failed = false;
+      j->started = j->flagged;
+      queue_.push_back(j);
+    }
   }
   // a job record that was never started goes back to the free list
   void discard(Job* j) {
@@ -548,12 +647,177 @@ class Executor {
     else j->abandoned = true;
     j->failed = true;
     j->done = true;
+    j->started = false;
+    if (j->flagged) flag_store(done_flag(j->slot), 1);  // the stream's wait must end
     for (Job* q : queue_) {
       q->failed = true;
       q->done = true;
+      q->started = false;
+      if (q->flagged) flag_store(done_flag(q->slot), 1);
     }
     queue_.clear();
     cv_done_.notify_all();
+  }
+
+  // Bounded wait for a stream's queued work: true when it drained within ms.
+  static bool drained(hipStream_t s, int ms) {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (;;) {
+      const hipError_t e = hipStreamQuery(s);
+      if (e == hipSuccess) return true;
+      if (e != hipErrorNotReady) return false;
+      if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(ms)) return false;
+      std::this_thread::sleep_for(std::chrono::microseconds(200));
+    }
+  }
+  // Polls a host flag for a value (true when seen within ms).
+  static bool seen(const uint64_t* p, uint64_t v, int ms) {
+    const auto t0 = std::chrono::steady_clock::now();
+    while (flag_load(p) != v) {
+      if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(ms)) return false;
+      std::this_thread::sleep_for(std::chrono::microseconds(100));
+    }
+    return true;
+  }
+  // The functional probe of the flag handshake on a private stream: a stream
+  // write reaches the host; a stream wait holds the stream until the host
+  // writes the value (every wait is released from the host, so none can stay
+  // blocked); and the same write / wait / reset sequence captured in a graph.
+  bool probe_flags() {
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return false;
+    uint64_t* hp = flags_ + 2 * kFlagSlots;
+    uint64_t* dp = dflags_ + 2 * kFlagSlots;
+    // a device-to-host copy enqueued before the write has landed when the
+    // host sees the flag (the CPU share's inputs travel that way)
+    void* dword = nullptr;
+    const uint64_t val = 29;
+    bool ok = hipMalloc(&dword, sizeof(uint64_t)) == hipSuccess &&
+              hipMemcpy(dword, &val, sizeof(val), hipMemcpyHostToDevice) == hipSuccess &&
+              hipMemcpyAsync(hp + 8, dword, sizeof(uint64_t), hipMemcpyDeviceToHost, s) == hipSuccess &&
+              hipStreamWriteValue64(s, dp, 5, 0) == hipSuccess && seen(hp, 5, 2000) && flag_load(hp + 8) == val &&
+              drained(s, 2000);
+    if (dword) (void)hipFree(dword);
+    if (ok) {
+      const bool q = hipStreamWaitValue64(s, dp + 1, 7, hipStreamWaitValueEq, ~0ull) == hipSuccess &&
+                     hipStreamWriteValue64(s, dp + 2, 9, 0) == hipSuccess;
+      std::this_thread::sleep_for(std::chrono::milliseconds(2));
+      const bool held = flag_load(hp + 2) == 0;
+      flag_store(hp + 1, 7);  // releases the wait
+      if (!drained(s, 2000)) {
+        probe_hung_ = true;  // the stream is left waiting: never destroyed or reused
+        return false;
+      }
+      ok = q && held && flag_load(hp + 2) == 9;
+    }
+    if (ok) flags_capturable_ = probe_capture(s, hp + 3, dp + 3);
+    if (!probe_hung_) (void)hipStreamDestroy(s);
+    return ok;
+  }
+  // The captured sequence also copies a device word to the host before the
+  // ready write (as the CPU share's inputs are copied out), which the host must
+  // see when it sees the flag, and a host word to the device and back after
+  // the wait (as the CPU share's result is copied back), which must see the
+  // host's write made before it released the wait.
+  bool probe_capture(hipStream_t s, uint64_t* hp, uint64_t* dp) {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    void* dword = nullptr;
+    if (hipMalloc(&dword, 2 * sizeof(uint64_t)) != hipSuccess) return false;
+    const uint64_t init[2] = {0, 23};
+    if (hipMemcpy(dword, init, sizeof(init), hipMemcpyHostToDevice) != hipSuccess ||
+        hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+      (void)hipFree(dword);
+      return false;
+    }
+    const bool q = hipMemcpyAsync(hp + 5, static_cast<uint64_t*>(dword) + 1, sizeof(uint64_t), hipMemcpyDeviceToHost,
+                                  s) == hipSuccess &&
+                   hipStreamWriteValue64(s, dp, 11, 0) == hipSuccess &&
+                   hipStreamWaitValue64(s, dp + 1, 13, hipStreamWaitValueEq, ~0ull) == hipSuccess &&
+                   hipStreamWriteValue64(s, dp + 1, 0, 0) == hipSuccess &&
+                   hipStreamWriteValue64(s, dp + 2, 17, 0) == hipSuccess &&
+                   hipMemcpyAsync(dword, hp + 3, sizeof(uint64_t), hipMemcpyHostToDevice, s) == hipSuccess &&
+                   hipMemcpyAsync(hp + 4, dword, sizeof(uint64_t), hipMemcpyDeviceToHost, s) == hipSuccess;
+    const bool ended = hipStreamEndCapture(s, &graph) == hipSuccess && graph;
+    bool ok = q && ended && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess;
+    if (ok && hipGraphLaunch(exec, s) == hipSuccess) {
+      ok = seen(hp, 11, 2000) && flag_load(hp + 5) == 23;  // the copy before the flag has landed
+      std::this_thread::sleep_for(std::chrono::milliseconds(2));
+      ok = ok && flag_load(hp + 2) == 0;  // the wait holds the replay
+      flag_store(hp + 3, 19);  // the host's data, written before the release
+      flag_store(hp + 1, 13);  // releases the wait whatever happened
+      if (!drained(s, 2000)) {
+        probe_hung_ = true;
+        ok = false;
+      } else {
+        // the writes and the copies after the wait ran after it
+        ok = ok && flag_load(hp + 1) == 0 && flag_load(hp + 2) == 17 && flag_load(hp + 4) == 19;
+      }
+    } else {
+      ok = false;
+    }
+    if (exec && !probe_hung_) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (!probe_hung_) (void)hipFree(dword);
+    return ok;
+  }
+  // The coordinator of the flag handshake: hands each armed job whose ready
+  // flag the stream raised to the driver, returns eager records to the free
+  // list once the stream has consumed their done flag, and runs the watchdog
+  // of the flag jobs (their waits are stream waits, not host functions).
+  // Busy-polls only while a submitted job waits for its ready flag; while the
+  // pool computes, or nothing is submitted, it sleeps between sweeps, so that
+  // it does not take a CPU from the pool.
+  void coordinate() {
+    int idle = 0;
+    uint64_t seen_progress = progress_.load(std::memory_order_relaxed);
+    auto since = std::chrono::steady_clock::now();
+    while (!stop_.load(std::memory_order_relaxed)) {
+      bool any = false, waiting = false, awaiting_ready = false;
+      {
+        std::lock_guard<std::mutex> g(m_);
+        const int n = nslots_.load();
+        for (int s = 0; s < n; ++s) {
+          Job* j = slot_job_[s];
+          if (!j || !j->armed) continue;
+          if (flag_load(ready_flag(s)) == 1) {
+            flag_store(ready_flag(s), 0);
+            start_locked(j);
+            any = true;
+          } else if (!j->permanent && j->done && !j->started && flag_load(done_flag(s)) == 0) {
+            j->armed = false;  // the stream consumed the done flag: the record is free again
+            if (!j->abandoned) free_.push_back(j);
+          }
+          waiting |= j->started && !j->done;
+          awaiting_ready |= !j->permanent && j->armed && !j->started && !j->done;
+        }
+        if (waiting && watchdog_ms_ > 0) {
+          const uint64_t p = progress_.load(std::memory_order_relaxed);
+          const auto now = std::chrono::steady_clock::now();
+          if (p != seen_progress) {
+            seen_progress = p;
+            since = now;
+          } else if (now - since >= std::chrono::milliseconds(watchdog_ms_)) {
+            for (int s = 0; s < n; ++s) {
+              Job* j = slot_job_[s];
+              if (j && j->armed && j->started && !j->done) poison(j);
+            }
+          }
+        } else {
+          seen_progress = progress_.load(std::memory_order_relaxed);
+          since = std::chrono::steady_clock::now();
+        }
+      }
+      if (any) {
+        cv_job_.notify_all();
+        cv_done_.notify_all();
+        idle = 0;
+      } else if (!awaiting_ready || ++idle > (1 << 16)) {
+        std::this_thread::sleep_for(std::chrono::microseconds(20));
+      } else {
+        _mm_pause();
+      }
+    }
   }
   void worker() {
     constexpr int kSpin = 4096;  // pauses before sleeping (~0.1 ms)
@@ -595,7 +859,10 @@ class Executor {
       progress_.fetch_add(1, std::memory_order_relaxed);
       {
         std::lock_guard<std::mutex> g(m_);
+        const bool already = j->done;  // poisoned while computed: its flag was raised then
         j->done = true;
+        j->started = false;
+        if (j->flagged && !already) flag_store(done_flag(j->slot), 1);
         busy_ = false;
       }
       cv_done_.notify_all();
@@ -732,6 +999,21 @@ class Executor {
   bool hold_ = false;  // the driver takes no new job
   std::atomic<bool> stall_{false};  // the driver stalls inside its job (tests of a wedged pool)
   int captured_ = 0;   // permanent (graph-captured) job records
+  // flag handshake: pinned host flags (ready [kFlagSlots], done [kFlagSlots],
+  // probe words) and their device addresses; the record bound to each slot
+  std::mutex flag_mu_;
+  uint64_t* flags_ = nullptr;
+  uint64_t* dflags_ = nullptr;
+  bool flags_capturable_ = false;
+  bool probe_hung_ = false;
+  bool use_flags_ = false;
+  std::vector<Job*> slot_job_;
+  std::atomic<int> nslots_{0};
+  std::thread coord_;
+  uint64_t* ready_flag(int s) { return flags_ + s; }
+  uint64_t* done_flag(int s) { return flags_ + kFlagSlots + s; }
+  static void flag_store(uint64_t* p, uint64_t v) { __atomic_store_n(p, v, __ATOMIC_RELEASE); }
+  static uint64_t flag_load(const uint64_t* p) { return __atomic_load_n(p, __ATOMIC_ACQUIRE); }
   int watchdog_ms_ = 10000;
   std::atomic<uint64_t> progress_{0};  // work units and jobs completed
   std::atomic<bool> unhealthy_{false};
@@ -817,6 +1099,26 @@ void ftmoe_cpu_executor_set_watchdog(ftmoe_cpu_executor* ex, int ms) {
   if (ex) reinterpret_cast<ftmoe_cpu::Executor*>(ex)->set_watchdog_ms(ms);
 }
 
+int ftmoe_cpu_executor_set_handshake(ftmoe_cpu_executor* ex, int mode) {
+  if (!ex || mode < 0 || mode > 1) return ftmoe::report_error(FTMOE_ERR_INVALID, "cpu_executor_set_handshake: mode");
+  auto* e = reinterpret_cast<ftmoe_cpu::Executor*>(ex);
+  if (mode == 0) {
+    e->use_flags(false);
+    return FTMOE_OK;
+  }
+  const int rc = e->enable_flags();
+  if (rc) return ftmoe::report_error(rc, "cpu_executor_set_handshake: stream memory operations failed their probe "
+                                         "on this device; the host-function handshake stays");
+  e->use_flags(true);
+  return FTMOE_OK;
+}
+
+int ftmoe_cpu_executor_handshake(ftmoe_cpu_executor* ex) {
+  if (!ex) return -1;
+  auto* e = reinterpret_cast<ftmoe_cpu::Executor*>(ex);
+  return e->flags_on() ? (e->flags_capturable() ? 2 : 1) : 0;
+}
+
 void ftmoe_cpu_executor_hold(ftmoe_cpu_executor* ex, int hold) {
   if (ex) reinterpret_cast<ftmoe_cpu::Executor*>(ex)->hold(hold);
 }
@@ -850,9 +1152,20 @@ int ftmoe_cpu_experts_submit(ftmoe_cpu_executor* ex, const ftmoe_bank* bank, con
   if (stream && hipStreamIsCapturing(stream, &cs) != hipSuccess)
     return ftmoe::report_error(FTMOE_ERR_HIP, "cpu_experts_submit: stream query failed");
   auto* e = reinterpret_cast<ftmoe_cpu::Executor*>(ex);
+  const bool capturing = cs != hipStreamCaptureStatusNone;
   // a job captured into a graph is replayed with the same record: never recycled
-  ftmoe_cpu::Job* j = e->new_job(cs != hipStreamCaptureStatusNone);
+  ftmoe_cpu::Job* j = e->new_job(capturing);
   ftmoe_cpu::fill(j, bank, x, w, ids, M, k, activation, y);
+  if (e->flags_on() && (!capturing || e->flags_capturable()) && e->bind_slot(j)) {
+    // flag handshake: the stream raises the job's ready flag
+    e->arm(j);
+    if (hipStreamWriteValue64(stream, e->ready_dev(j), 1, 0) != hipSuccess) {
+      e->disarm(j);
+      return ftmoe::report_error(FTMOE_ERR_HIP, "cpu_experts_submit: hipStreamWriteValue64 failed");
+    }
+    *job = j;
+    return FTMOE_OK;
+  }
   if (hipLaunchHostFunc(stream, ftmoe_cpu::host_start, j) != hipSuccess) {
     e->discard(j);
     return ftmoe::report_error(FTMOE_ERR_HIP, "cpu_experts_submit: hipLaunchHostFunc failed");
@@ -863,6 +1176,15 @@ int ftmoe_cpu_experts_submit(ftmoe_cpu_executor* ex, const ftmoe_bank* bank, con
 
 int ftmoe_cpu_experts_wait(ftmoe_cpu_executor* ex, void* job, ftmoe_stream_t stream) {
   if (!ex || !job) return ftmoe::report_error(FTMOE_ERR_INVALID, "cpu_experts_wait: NULL executor or job");
+  auto* j = static_cast<ftmoe_cpu::Job*>(job);
+  if (j->flagged) {
+    // flag handshake: wait for the job's done flag, then reset it for the next use
+    auto* e = reinterpret_cast<ftmoe_cpu::Executor*>(ex);
+    if (hipStreamWaitValue64(stream, e->done_dev(j), 1, hipStreamWaitValueEq, ~0ull) != hipSuccess ||
+        hipStreamWriteValue64(stream, e->done_dev(j), 0, 0) != hipSuccess)
+      return ftmoe::report_error(FTMOE_ERR_HIP, "cpu_experts_wait: stream memory operation failed");
+    return FTMOE_OK;
+  }
   if (hipLaunchHostFunc(stream, ftmoe_cpu::host_finish, job) != hipSuccess)
     return ftmoe::report_error(FTMOE_ERR_HIP, "cpu_experts_wait: hipLaunchHostFunc failed");
   return FTMOE_OK;

@@ -13,6 +13,8 @@ allocates that size's pinned buffers).
 
 from __future__ import annotations
 
+import os
+
 import torch
 
 from .. import ops
@@ -32,14 +34,23 @@ def hybrid_fetch_fraction(pcie_gbs: float, cpu_gbs: float, overlapped: bool = Tr
 
 
 class CpuMoeDecoder:
+    """``handshake``: ``"flags"`` (the default, as the reference's
+    ``FREETOKEN_CPU_MOE_FLAG_SYNC``; ``FTMOE_CPU_FLAG_SYNC=0`` opts out) rides
+    stream memory operations where their probe passes, else host functions;
+    ``"host"`` keeps host functions."""
+
     def __init__(self, cache: ExpertSlotCache, top_k: int, threads: int = 0, activation: str = "silu",
-                 watchdog_s: float | None = None, swiglu_limit: float | None = None):
+                 watchdog_s: float | None = None, swiglu_limit: float | None = None, handshake: str | None = None):
         assert cache.sources, "the CPU share reads the cache's host sources: set_bank_sources first"
         self.cache = cache
         self.top_k = top_k
         self.activation = activation
         self.swiglu_limit = swiglu_limit  # the layers' ds_fp4 SwiGLU clamp (cpu_moe_ext.cpp:1769-1781)
         self.executor = ops.CpuExecutor(threads, watchdog_s=watchdog_s)
+        if handshake is None:
+            handshake = "host" if os.environ.get("FTMOE_CPU_FLAG_SYNC", "1") == "0" else "flags"
+        if handshake == "flags" and torch.cuda.is_available():
+            self.executor.set_handshake("flags")
         self._io: dict[int, dict[str, torch.Tensor]] = {}
         self._banks: dict[int, ops.ExpertBank] = {}
 

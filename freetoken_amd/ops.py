@@ -613,6 +613,23 @@ class CpuExecutor:
         wedged pool would (tests of the watchdog and of ``close``)."""
         lib().ftmoe_cpu_executor_hold(self._h, 2 if on else 0)
 
+    def set_handshake(self, mode: str) -> bool:
+        """``"flags"``: stream memory operations (a ready flag the stream raises,
+        a done flag it waits on; no host-function round trip), taken when a
+        functional probe on this device passes; ``"host"``: host functions.
+        Returns whether the flags are in use."""
+        if mode not in ("flags", "host"):
+            raise ValueError(f"unknown handshake {mode!r}")
+        rc = lib().ftmoe_cpu_executor_set_handshake(self._h, 1 if mode == "flags" else 0)
+        if rc not in (_lib.FTMOE_OK, _lib.FTMOE_ERR_UNSUPPORTED):
+            check(rc, "cpu_executor_set_handshake")
+        return rc == _lib.FTMOE_OK and mode == "flags"
+
+    @property
+    def handshake(self) -> str:
+        """"host", "flags" (eager calls) or "flags+graphs" (captured calls too)."""
+        return {0: "host", 1: "flags", 2: "flags+graphs"}[lib().ftmoe_cpu_executor_handshake(self._h)]
+
     @property
     def healthy(self) -> bool:
         return lib().ftmoe_cpu_executor_healthy(self._h) == _lib.FTMOE_OK

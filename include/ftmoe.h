@@ -367,6 +367,22 @@ const char* ftmoe_cpu_executor_isa(ftmoe_cpu_executor* ex);
  * stall inside it until hold 0 (maintenance; tests force a stalled or wedged
  * pool with them). */
 int ftmoe_cpu_executor_healthy(ftmoe_cpu_executor* ex);
+/* Handshake of the stream-ordered entry points (_submit / _wait): mode 0 (the
+ * default) host functions; mode 1 stream memory operations -- _submit
+ * enqueues hipStreamWriteValue64 of the job's "ready" flag (mapped pinned
+ * memory), a coordinator thread of the executor polls the flags and hands a
+ * ready job to the pool, the pool raises the job's "done" flag, and _wait
+ * enqueues hipStreamWaitValue64 on it plus its reset: no host-function round
+ * trip per call (replaces the flag handshake of moe/cpu_executor.py:32-50,
+ * cpu_moe_ext.cpp:560-657).  Mode 1 is taken after a functional probe on a
+ * private stream of the current device; FTMOE_ERR_UNSUPPORTED (host functions
+ * kept) when it fails.  Under graph capture the flags are used only when the
+ * probe also captured and replayed them.  The watchdog covers flag jobs too:
+ * a job without pool progress for the period is failed and its done flag
+ * raised, so no stream waits for ever.  ftmoe_cpu_executor_handshake returns
+ * 0 (host functions), 1 (flags, eager calls) or 2 (flags, also captured). */
+int ftmoe_cpu_executor_set_handshake(ftmoe_cpu_executor* ex, int mode);
+int ftmoe_cpu_executor_handshake(ftmoe_cpu_executor* ex);
 void ftmoe_cpu_executor_set_watchdog(ftmoe_cpu_executor* ex, int ms);
 void ftmoe_cpu_executor_hold(ftmoe_cpu_executor* ex, int hold);
 /* Synchronous run on the calling thread's behalf (FTMOE_ERR_TIMEOUT when the

@@ -60,7 +60,7 @@ def _pinned(bank):
     return [torch.from_numpy(np.ascontiguousarray(a)).pin_memory() for a in arrays]
 
 
-def _hybrid_setup(dev, fmt, L, E, Sz, H, I, k, rng, decode_target="hybrid", **kw):
+def _hybrid_setup(dev, fmt, L, E, Sz, H, I, k, rng, decode_target="hybrid", handshake="host", **kw):
     banks = [synth.make_bank(fmt, E, H, I, rng) for _ in range(L)]
     qfmt = {"fp8": "fp8_block", "mxfp4": "ds_fp4"}[fmt]
     cache = ExpertSlotCache(L, E, Sz, qfmt, device=dev, decode_target=decode_target, **kw)
@@ -72,7 +72,10 @@ def _hybrid_setup(dev, fmt, L, E, Sz, H, I, k, rng, decode_target="hybrid", **kw
     per_layer = [_pinned(b) for b in banks]
     cache.set_bank_sources({n: [per_layer[l][j] for l in range(L)] for j, n in enumerate(names)})
     cache.reset()
-    cache.set_cpu_executor(CpuMoeDecoder(cache, k, threads=8))
+    dec = CpuMoeDecoder(cache, k, threads=8, handshake=handshake)
+    if handshake == "flags":  # the stream memory operations passed their probe on this device
+        assert dec.executor.handshake.startswith("flags"), dec.executor.handshake
+    cache.set_cpu_executor(dec)
     layers = [OffloadMoELayer(l, E, k, H, I, device=dev) for l in range(L)]
     for lay in layers:
         lay.offload_cache = cache
@@ -93,16 +96,18 @@ def _expected(st, layer, x, w, ids, bank, E, max_fetch, frac_q16, capacity, shar
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("handshake", ["host", "flags"])
 @pytest.mark.parametrize("fmt,max_fetch,frac,with_shared", [("fp8", 1, 0.0, False), ("mxfp4", 2, 0.0, False),
                                                             ("fp8", 8, 0.4, False), ("fp8", 1, 0.0, True)])
-def test_hybrid_layer_matches_oracle(dev, fmt, max_fetch, frac, with_shared):
+def test_hybrid_layer_matches_oracle(dev, fmt, max_fetch, frac, with_shared, handshake):
     """Two layers share 6 slots over 16 experts; every step fetches at most the
     cap of its misses and the CPU computes the rest (with a shared expert: on
-    the GPU, in the GPU partial)."""
+    the GPU, in the GPU partial).  Both handshakes of the CPU share: host
+    functions, and the stream memory operations' flags."""
     rng = np.random.default_rng(71 + max_fetch)
     L, E, Sz, H, I, k, M = 2, 16, 6, 512, 256, 4, 3
     banks, cache, layers = _hybrid_setup(dev, fmt, L, E, Sz, H, I, k, rng, hybrid_max_fetch=max_fetch,
-                                         hybrid_fetch_fraction=frac)
+                                         hybrid_fetch_fraction=frac, handshake=handshake)
     shared = synth.make_bank(fmt, 1, H, I, rng) if with_shared else None
     if shared is not None:
         for lay in layers:
@@ -156,13 +161,17 @@ def test_cpu_layer_matches_oracle(dev, with_shared):
 
 
 @pytest.mark.gpu
-def test_hybrid_replays_in_a_graph(dev):
+@pytest.mark.parametrize("handshake", ["host", "flags"])
+def test_hybrid_replays_in_a_graph(dev, handshake):
     """Admission, CPU submit, gather, GPU experts and CPU wait captured once and
     replayed with a new routing each time, with eager work between replays:
-    every replay matches the oracle step (the host nodes carry the CPU share)."""
+    every replay matches the oracle step (host nodes, or stream memory
+    operations where they capture, carry the CPU share)."""
     rng = np.random.default_rng(89)
     L, E, Sz, H, I, k, M = 1, 16, 4, 512, 256, 4, 2
-    banks, cache, layers = _hybrid_setup(dev, "fp8", L, E, Sz, H, I, k, rng, hybrid_max_fetch=1)
+    banks, cache, layers = _hybrid_setup(dev, "fp8", L, E, Sz, H, I, k, rng, hybrid_max_fetch=1,
+                                         handshake=handshake)
+    print("handshake:", cache.cpu_executor.executor.handshake, flush=True)
     layer = layers[0]
     x_buf = torch.zeros((M, H), dtype=torch.bfloat16, device=dev)
     w_buf = torch.zeros((M, k), dtype=torch.float32, device=dev)
@@ -236,5 +245,47 @@ def test_stream_wait_unblocks_on_watchdog(dev):
     assert float(marker.item()) == 1.0 and not ex.healthy
     with pytest.raises(RuntimeError, match="watchdog fired"):
         ex.raise_if_unhealthy()
+    ex.hold(False)
+    ex.close()
+
+
+@pytest.mark.gpu
+def test_flag_wait_unblocks_on_watchdog(dev):
+    """The flag handshake with a stalled pool (held from the host): the
+    executor's coordinator fails the job after the watchdog period and raises
+    its done flag, so the stream's wait ends, later stream work runs, and the
+    executor reports the failure; a healthy executor's flag jobs replay a
+    second time on the same records."""
+    import time
+
+    from freetoken_amd import ops
+
+    rng = np.random.default_rng(101)
+    E, H, I, M, k = 4, 256, 128, 2, 2
+    bank = synth.make_bank("bf16", E, H, I, rng)
+    hb = to_device_bank(bank, "cpu")
+    x = torch.from_numpy(synth.activations(rng, M, H)).to(torch.bfloat16).pin_memory()
+    w = torch.full((M, k), 0.5, dtype=torch.float32).pin_memory()
+    ids = torch.tensor([[0, 1], [2, 3]], dtype=torch.int32).pin_memory()
+    y = torch.zeros((M, H), dtype=torch.bfloat16).pin_memory()
+    ex = ops.CpuExecutor(threads=2, watchdog_s=0.3)
+    assert ex.set_handshake("flags"), "stream memory operations failed their probe"
+    # a working pool first: two jobs in a row through the flags, against the synchronous run
+    y_ref = ex.run(hb, x, w, ids)
+    for _ in range(2):
+        y.zero_()
+        job = ex.submit(hb, x, w, ids, y, device=dev)
+        ex.wait(job, device=dev)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref)
+    ex.hold(True)
+    marker = torch.zeros(1, device=dev)
+    t0 = time.monotonic()
+    job = ex.submit(hb, x, w, ids, y, device=dev)
+    ex.wait(job, device=dev)
+    marker += 1  # stream work after the wait
+    torch.cuda.synchronize()
+    assert 0.25 <= time.monotonic() - t0 < 10.0
+    assert float(marker.item()) == 1.0 and not ex.healthy
     ex.hold(False)
     ex.close()
