@@ -123,6 +123,15 @@ int ftmoe_align(const int32_t* topk_ids, int numel, int num_experts, int block_s
 int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_id, int num_experts,
                    int32_t* slot_ids, uint8_t* miss_mask, int64_t* stats, ftmoe_stream_t stream);
 
+/* Routing histogram of one layer's decode step: freq[e] += the number of
+ * entries of topk_ids equal to e, ids outside [0, num_experts) skipped
+ * (int64 freq [num_experts], accumulated, never cleared here); replaces the
+ * opt-in decode_freq scatter of OffloadMoeCache.ensure_experts
+ * (moe/offload_cache.py:234-236,803-807), run on the raw expert ids before
+ * they are rewritten to slots.  Device-side and graph-capturable, so the
+ * histogram also accumulates in replayed decode steps.  num_experts <= 16384. */
+int ftmoe_route_histogram(const int32_t* topk_ids, int numel, int num_experts, int64_t* freq, ftmoe_stream_t stream);
+
 /* Expert-cache admission (the miss path of OffloadMoeCache.ensure_experts):
  * replaces lru_ensure / ensure_experts (moe/offload_kernels.py:19-40) and the
  * capped admission of ensure_experts_hybrid with the "lowest_id" or
@@ -156,15 +165,6 @@ int ftmoe_slot_map(const int32_t* topk_ids, int numel, const int32_t* slot_for_i
  *   slot (or staging entry) could take -- nonzero means the cache is smaller
  *   than a call's distinct experts.
  * num_experts, cache_size <= 8192. */
-/* Routing histogram of one layer's decode step: freq[e] += the number of
- * entries of topk_ids equal to e, ids outside [0, num_experts) skipped
- * (int64 freq [num_experts], accumulated, never cleared here); replaces the
- * opt-in decode_freq scatter of OffloadMoeCache.ensure_experts
- * (moe/offload_cache.py:234-236,803-807), run on the raw expert ids before
- * they are rewritten to slots.  Device-side and graph-capturable, so the
- * histogram also accumulates in replayed decode steps.  num_experts <= 16384. */
-int ftmoe_route_histogram(const int32_t* topk_ids, int numel, int num_experts, int64_t* freq, ftmoe_stream_t stream);
-
 int ftmoe_lru_ensure(int32_t* expert_ids, int numel, int layer_id, int num_layers, int num_experts,
                      int32_t* slot_for_id, int32_t* id_of_slot, int64_t* usage, int64_t* step, int cache_size,
                      int64_t* recency, int max_fetch, int fetch_frac_q16, int32_t* evict_slots,
