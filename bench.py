@@ -924,7 +924,7 @@ def main() -> int:
 
     sweep = {}
     if not args.no_sweep:
-        for M in (1, 2, 4, 8, 16, 32, 128, 256):
+        for M in (1, 2, 4, 8, 16, 32, 128, 192, 256):
             log(f"[bench] sweep C4 decode batch {M}")
             sweep[f"{C4['name']}_b{M}"] = run_decode(c4, M, 20, 3, gen, stage_timing=True)
     cpu = None

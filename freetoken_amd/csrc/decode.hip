@@ -1326,9 +1326,10 @@ static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared
       // wide segments (FP8 calls from kWideMinTokens tokens): no K split (as
       // below) and four-chunk passes, so an expert with up to 64 routes is
       // read once (with 32-route segments about half of C4 b=256's experts
-      // were read twice): C4 b=256 637 -> 594-597 us; at b=128-192, where
-      // most experts have fewer than 32 routes, the wide passes were equal or
-      // slower (b=128 498 -> 549 us)
+      // were read twice): C4 b=256 637 -> 594-597 us.  From 144 tokens:
+      // against the 32-route kernels, interleaved A/B, C4 b=144 515 -> 507 us,
+      // b=160 521 -> 508, b=192 560 -> 531, b=224 595 -> 545, b=255 624 ->
+      // 565; b=96-128 equal
       if (stage == 0) {
         constexpr auto kw = decode_stage_kernel<FR, FS, 0, 1, 1, 1>;
         return launch_one<kw>(dim3((imax + 63) / 64, gy), a, stream);

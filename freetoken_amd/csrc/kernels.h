@@ -42,7 +42,7 @@ constexpr int kDecodeSegCap = 32;
 // FP8 decode calls of at least kWideMinTokens tokens cut segments at 64
 // routes (the wide kernels read an expert once for up to 64 routes).
 constexpr int kDecodeSegCapWide = 64;
-constexpr int kWideMinTokens = 256;
+constexpr int kWideMinTokens = 144;
 inline int decode_seg_cap(int M, bool fp8) { return fp8 && M >= kWideMinTokens ? kDecodeSegCapWide : kDecodeSegCap; }
 inline int decode_max_segments(int numel, int num_experts, int seg_cap = kDecodeSegCap) {
   const int bound = num_experts + numel / seg_cap;

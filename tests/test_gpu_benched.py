@@ -152,7 +152,7 @@ def _oracle_routing(layer, logits: np.ndarray):
 # and the shared expert's gate_up in one launch; 64 is the headline; 256 the
 # wide segments), C2 (128 FP8 experts, softmax router) and C3 (160 MXFP4
 # experts, bf16 shared expert) at their smallest and largest benched batches
-DECODE_POINTS = [("c4", 1), ("c4", 2), ("c4", 8), ("c4", 32), ("c4", 64), ("c4", 128), ("c4", 256),
+DECODE_POINTS = [("c4", 1), ("c4", 2), ("c4", 8), ("c4", 32), ("c4", 64), ("c4", 128), ("c4", 192), ("c4", 256),
                  ("c2", 1), ("c2", 64), ("c3", 1), ("c3", 64)]
 
 
