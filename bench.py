@@ -28,6 +28,7 @@ import os
 import statistics
 import sys
 import time
+import zlib
 
 import torch
 
@@ -162,11 +163,11 @@ class DecodeLayer:
 
     def shared_in_router(self, M: int) -> bool:
         """Whether the shared expert's gate_up runs in the router's launch (the
-        library's route_shared_fits: grouped router, shared expert, at most two
+        library's route_shared_fits: grouped router, shared expert, at most four
         tokens and 64 routes, at most 256 experts); its bytes then belong to
         that launch, not to the gate_up stage."""
         c = self.cfg
-        return (c["router"] == "sigmoid" and bool(c["shared"]) and M <= 2 and M * c["k"] <= 64
+        return (c["router"] == "sigmoid" and bool(c["shared"]) and M <= 4 and M * c["k"] <= 64
                 and c["E"] <= 256)
 
     def step_bytes(self, ids: torch.Tensor, M: int) -> tuple[int, int, int]:
@@ -922,11 +923,16 @@ def main() -> int:
                 "avg_launch_us": round(gu_us, 2),
                 "algorithmic_bytes_per_launch": int(head["gate_up_bytes_per_launch"])}
 
+    def seeded(tag: str) -> torch.Generator:
+        # each sweep line draws from its own seed, so that adding or removing a
+        # line leaves the others' inputs (routings, weights) unchanged
+        return torch.Generator(device=dev).manual_seed(zlib.crc32(tag.encode()) & 0x7FFFFFFF)
+
     sweep = {}
     if not args.no_sweep:
         for M in (1, 2, 4, 8, 16, 32, 128, 192, 256):
             log(f"[bench] sweep C4 decode batch {M}")
-            sweep[f"{C4['name']}_b{M}"] = run_decode(c4, M, 20, 3, gen, stage_timing=True)
+            sweep[f"{C4['name']}_b{M}"] = run_decode(c4, M, 20, 3, seeded(f"{C4['name']}_b{M}"), stage_timing=True)
     cpu = None
     if not args.no_cpu:
         log("[bench] CPU baseline")
@@ -936,22 +942,23 @@ def main() -> int:
     if not args.no_sweep:
         for cfg in (C2, C3):
             log(f"[bench] sweep {cfg['name']}")
-            layer = DecodeLayer(cfg, dev, gen)
+            layer = DecodeLayer(cfg, dev, seeded(cfg["name"]))
             for M in (1, 8, 32, 64):
-                sweep[f"{cfg['name']}_b{M}"] = run_decode(layer, M, 20, 3, gen, stage_timing=True)
+                sweep[f"{cfg['name']}_b{M}"] = run_decode(layer, M, 20, 3, seeded(f"{cfg['name']}_b{M}"),
+                                                          stage_timing=True)
             del layer
             torch.cuda.empty_cache()
         for fmt in ("fp8_block", "mxfp4"):
             log(f"[bench] sweep C5 prefill {fmt}")
-            sweep[f"c5_prefill_8192_{fmt}"] = run_prefill(fmt, 10, 3, gen, dev)
+            sweep[f"c5_prefill_8192_{fmt}"] = run_prefill(fmt, 10, 3, seeded(f"c5_prefill_8192_{fmt}"), dev)
         log("[bench] sweep C4 miss path (admission + PCIe gather of 8 experts per step)")
-        sweep["c4_miss_fetch_8_experts"] = run_miss_fetch(gen, dev)
+        sweep["c4_miss_fetch_8_experts"] = run_miss_fetch(seeded("c4_miss_fetch_8_experts"), dev)
         log("[bench] sweep C4 prefill movement (3 layers x 32 host-resident experts, 8192 tokens)")
-        sweep["c4_prefill_offload_3x32_experts"] = run_prefill_offload(gen, dev)
+        sweep["c4_prefill_offload_3x32_experts"] = run_prefill_offload(seeded("c4_prefill_offload_3x32_experts"), dev)
         log("[bench] sweep C4 hybrid decode (1 expert fetched per step, the other misses on the CPU)")
-        sweep["c4_hybrid_b1"] = run_hybrid(gen, dev, M=1)
+        sweep["c4_hybrid_b1"] = run_hybrid(seeded("c4_hybrid_b1"), dev, M=1)
         log("[bench] sweep C4 expert-parallel share (EP-8: 32 experts on this GPU, 64 tokens per GPU)")
-        sweep["c4_ep8_share_b64_per_gpu"] = run_ep_share(gen, dev)
+        sweep["c4_ep8_share_b64_per_gpu"] = run_ep_share(seeded("c4_ep8_share_b64_per_gpu"), dev)
         # the reference's benched rules (moe/bench_profile.py:156-191): the fetch share from the measured
         # PCIe and CPU rates, pcie / cpu for rates taken under DRAM contention, pcie / (pcie + cpu) for
         # rates of transfers that overlap without contending; both from this run's standalone rates
@@ -961,7 +968,8 @@ def main() -> int:
         for rule, overlapped in (("contention", False), ("overlap", True)):
             frac = hybrid_fetch_fraction(pcie, cpu_rate, overlapped=overlapped)
             log(f"[bench] sweep C4 hybrid decode, measured fetch fraction {frac} ({rule} rule)")
-            sweep[f"c4_hybrid_b1_fraction_{rule}_rule"] = run_hybrid(gen, dev, M=1, fetch_fraction=frac)
+            sweep[f"c4_hybrid_b1_fraction_{rule}_rule"] = run_hybrid(seeded(f"c4_hybrid_b1_fraction_{rule}_rule"), dev, M=1,
+                                                                     fetch_fraction=frac)
 
     def rnd(d):
         return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}

@@ -1133,10 +1133,12 @@ __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves
 // router's dependent chains keep one CU busy.  One 16-row tile per wave gives
 // the piece enough workgroups to finish under the router (two tiles per wave
 // outlasted it).  Measured: C3 (bf16 shared beside MXFP4) b=1 60.6 -> 53.8 us,
-// b=2 69.3 -> 67.3 us; C4 b=1 -1%; from 4 tokens no gain, so those keep the
-// separate launches.
+// b=2 69.3 -> 67.3 us; C4 b=1 -1%.  Up to 4 tokens (one per wave of the
+// routing workgroup), against the separate launches with the current
+// kernels: C4 b=3 144.6 -> 142.9 us, b=4 163.8 -> 160.2 us, C3 b=4 equal.
 constexpr int kSharedRT = 1, kSharedKS = 4;
-constexpr int kRouteSharedTokens = 2;
+constexpr int kRouteSharedTokens = 4;
+static_assert(kRouteSharedTokens <= kDecWaves, "the routing workgroup routes one token per wave");
 
 template <int PER, int FS>
 __global__ void __launch_bounds__(kDecWaves * kWave) __attribute__((amdgpu_waves_per_eu(2)))
@@ -1311,7 +1313,7 @@ static hipError_t launch_one(dim3 g, const DecodeArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-constexpr int kGateUpSharedMinM = 128;
+constexpr int kGateUpSharedMinM = 80;
 
 // Bytes per weight times two (bf16 4, FP8 2, MXFP4 1).
 static int bytes_per_weight_x2(int fmt) { return fmt == FMT_BF16 ? 4 : fmt == FMT_FP8 ? 2 : 1; }
@@ -1346,7 +1348,9 @@ static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared
       // share the activation chunks through LDS (half the activation reads
       // per weight byte of the RT = 2 K-split grid); measured C4 b=128 326 ->
       // 302 us, b=16-64 unchanged, b=8 slower (its grid no longer fills the
-      // GPU); MXFP4 (one chunk per pass) slower at b=8-64
+      // GPU); MXFP4 (one chunk per pass) slower at b=8-64.  From 80 tokens
+      // (interleaved A/B against the K split): C4 b=80 471 -> 464 us, b=96
+      // 480 -> 470, b=112 498 -> 478; b=32-64 equal within 2 us
       constexpr auto ks = decode_stage_kernel<FR, FS, 0, 1, 1>;
       return launch_one<ks>(dim3((imax + 63) / 64, gy), a, stream);
     }

@@ -45,12 +45,12 @@ def test_softmax_routed_matches_separate_calls(dev, M, logit_dtype):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M", [1, 2, 4, 8, 16, 33])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16, 33])
 @pytest.mark.parametrize("fmts", [("fp8", "fp8"), ("mxfp4", "bf16")])
 def test_grouped_routed_cached_matches_separate_calls(dev, M, fmts):
     """C4-shaped router (256 experts, 8 groups, top-4 groups, k 8) over a
     64-slot table with misses, with a shared expert (FP8 beside FP8, bf16 beside
-    MXFP4 as in C3).  Up to 2 tokens the shared expert's gate_up runs in the
+    MXFP4 as in C3).  Up to 4 tokens the shared expert's gate_up runs in the
     router's launch; the outputs must still equal the separate calls bit for
     bit."""
     rng = np.random.default_rng(100 + M)
@@ -88,12 +88,13 @@ def test_grouped_routed_cached_matches_separate_calls(dev, M, fmts):
 
 # ----------------------------------------------------------------- front-end routers under ties
 # The decode front ends (router + permutation in one launch: up to 16 tokens
-# and 64 routes; with a grouped router and a shared expert up to 2 tokens
-# beside the shared gate_up) rank the candidates by counting instead of the
-# standalone routers' argmax rounds.  On logits full of exact ties (copied
-# values, whole rows equal, tied groups, -0.0 against +0.0, a bias that flips
-# the choice) their ids must equal the oracle's and their weights the
-# standalone router's bit for bit, with the permutation after them.
+# and 64 routes; with a grouped router and a shared expert up to 4 tokens
+# beside the shared gate_up) select each token's experts in a wave of their
+# own launch, and align up to 16 routes by counting ranks instead of sorting.
+# On logits full of exact ties (copied values, whole rows equal, tied groups,
+# -0.0 against +0.0, a bias that flips the choice) their ids must equal the
+# oracle's and their weights the standalone router's bit for bit, with the
+# permutation after them.
 
 
 def _tie_rows(rng, M, E, bf16):
@@ -131,13 +132,13 @@ def test_front_end_softmax_ties(dev, M, E, k, renorm, bf16):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M", [1, 2, 3, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 16])
 @pytest.mark.parametrize("E,ng,tg,k", [(256, 8, 4, 8), (64, 8, 4, 4), (160, 1, 1, 8), (96, 8, 4, 4), (256, 16, 4, 2)])
 @pytest.mark.parametrize("shared", [False, True])
 def test_front_end_grouped_ties(dev, M, E, ng, tg, k, shared):
     """Grouped router front ends (lane-block group scores, and the LDS scan for
     groups of 12), with and without a slot table, and with a shared expert (its
-    gate_up in the router's launch at 1 and 2 tokens)."""
+    gate_up in the router's launch up to 4 tokens)."""
     rng = np.random.default_rng(E * 3 + M + ng)
     k = min(k, 64 // M)
     H, I, S = 128, 128, E // 2
