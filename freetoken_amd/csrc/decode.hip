@@ -1355,14 +1355,16 @@ static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared
       return launch_one<ks>(dim3((imax + 63) / 64, gy), a, stream);
     }
     const dim3 g1((imax + 15) / 16, gy), g2((imax + 31) / 32, gy);
-    // FP8 calls of one or two tokens, or whose RT = 2 grid is a single round
+    // FP8 calls of up to four tokens, or whose RT = 2 grid is a single round
     // of resident workgroups: few experts, many of the grid's segments empty
     // (routes to experts outside the slot bank), and the RT = 1 grid's twice
     // as many, half as long workgroups end together more evenly (C4 b=1
-    // 72.5-72.8 -> 69.6-70.6 us, b=2 115.4-116.1 -> 109.7-109.8 us; b=4-8
-    // equal; MXFP4 at C3 b=1 0.8 us slower, so it keeps RT = 2)
+    // 72.5-72.8 -> 69.6-70.6 us, b=2 115.4-116.1 -> 109.7-109.8 us; b=4
+    // 160.1 -> 156.7 and 176.9 -> 175.7 us on two boxes, b=3 equal; up to 8
+    // tokens C2 b=8 was 5% slower; MXFP4 at C3 b=1 0.8 us slower, so it
+    // keeps RT = 2)
     if (FR == FMT_FP8 &&
-        (a.M <= 2 ||
+        (a.M <= 4 ||
          static_cast<long long>(g2.x) * g2.y <= static_cast<long long>(cu_count()) * resident_per_cu<k2>()))
       return launch_one<k1>(g1, a, stream);
     // MXFP4 up to 8 tokens keeps two row tiles per wave (C3 b=2 66.0-66.5 ->
