@@ -477,7 +477,7 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillGemmArgs
 //
 // Schedule (map_tile_q): the active workgroups are laid out XCD-major
 // (workgroup b runs on XCD b % 8), so each XCD works through a contiguous range
-// of the logical order, in which chunks of kQChunk M blocks of one expert sweep
+// of the logical order, in which chunks of q_chunk() M blocks of one expert sweep
 // its N tiles: the workgroups an XCD runs at once read several weight tiles and
 // share the activations of a few M blocks.
 // ----------------------------------------------------------------------------
@@ -485,7 +485,16 @@ constexpr int kQBM = 256;     // routes per tile (align block size of the quanti
 constexpr int kQRows = 256;   // weight rows per workgroup
 constexpr int kQThreads = 512;
 constexpr int kXcds = 8;
-constexpr int kQChunk = 4;
+// M blocks per chunk of the schedule (see map_tile_q): [FP8, MXFP4][gate_up, down].
+// Measured on C5 (interleaved A/B, ms): FP8 gate_up 4 -> 2.23-2.24, 8 -> 2.19-2.20,
+// 16 -> 2.22, 2 -> 2.32; FP8 down 4 -> 1.25-1.26, 2 -> 1.20, 1 -> 1.22; MXFP4
+// gate_up 4 -> 1.79 (2 and 8 slower by 4-7%); MXFP4 down 4 -> 1.04-1.06, 2 ->
+// 1.02-1.04, 8 -> 1.09-1.10.
+constexpr int kQChunkSel[2][2] = {{8, 2}, {4, 2}};
+template <int FMT, int GATE_UP>
+constexpr int q_chunk() {
+  return kQChunkSel[FMT == FMT_FP8 ? 0 : 1][GATE_UP ? 0 : 1];
+}
 constexpr int kFoldLag = 3;  // FP8: MFMAs between an MFMA and the fold of its result
 
 template <int FMT>
@@ -513,6 +522,7 @@ __device__ __forceinline__ int xcd_major(int b, int n) {
 
 // (M block, N tile) of position `local` in a group of nb M blocks x ntiles:
 // chunks of kQChunk M blocks, each chunk sweeping all N tiles.
+template <int kQChunk>
 __device__ __forceinline__ void chunked(int local, int nb, int ntiles, int& m, int& ntile) {
   const int full = nb / kQChunk, rem = nb - full * kQChunk;
   const int span = kQChunk * ntiles;
@@ -531,6 +541,7 @@ __device__ __forceinline__ void chunked(int local, int nb, int ntiles, int& m, i
 // active workgroups -- routed blocks of the real experts, then the shared
 // expert's blocks -- take part; they are laid out XCD-major over their own
 // count, so every XCD gets the same share.  Returns false for idle ones.
+template <int kQChunk>
 __device__ __forceinline__ bool map_tile_q(const PrefillGemmArgs& a, int b, bool& shared, int& expert, int& mblock,
                                            int& ntile) {
   const int routed = (a.cum[a.num_experts] / kQBM) * a.ntiles;
@@ -546,13 +557,13 @@ __device__ __forceinline__ bool map_tile_q(const PrefillGemmArgs& a, int b, bool
     const int b0 = a.cum[lo] / kQBM;
     const int nb = a.cum[lo + 1] / kQBM - b0;
     int m;
-    chunked(wg - b0 * a.ntiles, nb, a.ntiles, m, ntile);
+    chunked<kQChunk>(wg - b0 * a.ntiles, nb, a.ntiles, m, ntile);
     shared = false;
     expert = lo;
     mblock = b0 + m;
     return true;
   }
-  chunked(wg - routed, a.shared_blocks, a.ntiles, mblock, ntile);
+  chunked<kQChunk>(wg - routed, a.shared_blocks, a.ntiles, mblock, ntile);
   shared = true;
   expert = 0;
   return true;
@@ -572,8 +583,9 @@ struct QTile {
   int expert, mblock, ntile;
 };
 
+template <int kQChunk>
 __device__ __forceinline__ bool map_tile_q(const PrefillGemmArgs& a, int b, QTile& t) {
-  return map_tile_q(a, b, t.shared, t.expert, t.mblock, t.ntile);
+  return map_tile_q<kQChunk>(a, b, t.shared, t.expert, t.mblock, t.ntile);
 }
 
 // s_barrier without the memory fence of __syncthreads (which would wait for
@@ -628,7 +640,8 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
 
   int v = blockIdx.x;
   QTile cur;
-  if (!map_tile_q(a, v, cur)) return;
+  constexpr int kChunk = q_chunk<FMT, GATE_UP>();
+  if (!map_tile_q<kChunk>(a, v, cur)) return;
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -1046,7 +1059,7 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
         if (d < nkb) issue(d, (g0 + d) % S);
     }
     QTile nxt;
-    const bool has_next = map_tile_q(a, v + static_cast<int>(gridDim.x), nxt);
+    const bool has_next = map_tile_q<kChunk>(a, v + static_cast<int>(gridDim.x), nxt);
     const bool cross = has_next && nkb > D;  // the next tile's first steps ride in this tile's last D steps
     // (pinned: a known-zero accumulator would let the compiler schedule the
     // first step, which it peels, apart from the others, at a register cost)
