@@ -185,8 +185,12 @@ class DecodeLayer:
         return u * eb + sh + io, gu, u
 
 
-def run_decode(layer: DecodeLayer, M: int, steps: int, warmup: int, gen, graphs: int = 8, stage_timing=False):
-    """Times `steps` graph replays (rotating over `graphs` routings); returns a dict."""
+def run_decode(layer: DecodeLayer, M: int, steps: int, warmup: int, gen, graphs: int = 8, stage_timing=False,
+               min_ms: float = 0.0):
+    """Times `steps` graph replays (rotating over `graphs` routings); returns a dict.  With
+    `min_ms` > 0 the warm-up and the timed region each last at least that long (more replays
+    than `warmup` / `steps` for short steps, whose first replays after an idle stretch run at
+    lower clocks and whose timed region would otherwise be a millisecond or two)."""
     c, dev = layer.cfg, layer.dev
     G = max(1, min(graphs, steps))
     logits = [torch.randn((M, c["E"]), generator=gen, device=dev) for _ in range(G)]
@@ -208,6 +212,18 @@ def run_decode(layer: DecodeLayer, M: int, steps: int, warmup: int, gen, graphs:
         graphs_[i % G].replay()
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if min_ms > 0:
+        t0.record()
+        for i in range(G):
+            graphs_[i % G].replay()
+        t1.record()
+        torch.cuda.synchronize()
+        est = max(t0.elapsed_time(t1) / G, 1e-3)
+        n = min(4000, math.ceil(min_ms / est))
+        for i in range(n):
+            graphs_[i % G].replay()
+        torch.cuda.synchronize()
+        steps = max(steps, n)
     t0.record()
     for i in range(steps):
         graphs_[i % G].replay()
@@ -230,7 +246,7 @@ def run_decode(layer: DecodeLayer, M: int, steps: int, warmup: int, gen, graphs:
         # instrumented eager pass over the same inputs: per-kernel durations
         L = _lib.lib()
         L.ftmoe_stage_timing_begin()
-        for i in range(steps):
+        for i in range(min(steps, 64)):
             layer.step(logits[i % G], xs[i % G], outs[i % G])
         torch.cuda.synchronize()
         import ctypes
@@ -932,7 +948,8 @@ def main() -> int:
     if not args.no_sweep:
         for M in (1, 2, 4, 8, 16, 32, 128, 192, 256):
             log(f"[bench] sweep C4 decode batch {M}")
-            sweep[f"{C4['name']}_b{M}"] = run_decode(c4, M, 20, 3, seeded(f"{C4['name']}_b{M}"), stage_timing=True)
+            sweep[f"{C4['name']}_b{M}"] = run_decode(c4, M, 20, 3, seeded(f"{C4['name']}_b{M}"), stage_timing=True,
+                                                     min_ms=20.0)
     cpu = None
     if not args.no_cpu:
         log("[bench] CPU baseline")
@@ -945,7 +962,7 @@ def main() -> int:
             layer = DecodeLayer(cfg, dev, seeded(cfg["name"]))
             for M in (1, 8, 32, 64):
                 sweep[f"{cfg['name']}_b{M}"] = run_decode(layer, M, 20, 3, seeded(f"{cfg['name']}_b{M}"),
-                                                          stage_timing=True)
+                                                          stage_timing=True, min_ms=20.0)
             del layer
             torch.cuda.empty_cache()
         for fmt in ("fp8_block", "mxfp4"):
