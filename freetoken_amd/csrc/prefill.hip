@@ -827,8 +827,11 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
       xs = *reinterpret_cast<const uint32_t*>(x_sc + 64 * i);
     };
     // The next column tile's LDS reads are issued before this tile's MFMAs.
-    // FP8: pin() keeps each scale fold after the MFMA two places later in the
-    // stream, so the VALU work runs while the matrix core is busy.
+    // FP8: each scale fold is written kFoldLag MFMAs after its own MFMA (its
+    // result register stays live that long), so the compiler can place the
+    // fold's VALU work while the matrix core runs later MFMAs instead of
+    // waiting out the MFMA result latency; pin() keeps the accumulator updates
+    // in that order.
     i32x8 xf[2];
     uint32_t xs[2];
     if constexpr (FMT == FMT_FP8) {
@@ -847,7 +850,7 @@ __global__ void __launch_bounds__(kQThreads) prefill_qgemm_kernel(PrefillGemmArg
       for (int j = 0; j < 4; ++j) read_w(j);
       read_x(0, xf[0], xs[0]);
     }
-    // FP8: two MFMA results in flight (tq, with their fold factors fq)
+    // FP8: kFoldLag MFMA results in flight (tq, with their fold factors fq)
     constexpr int P = kFoldLag;
     f32x4 tq[P];
     float fq[P];
