@@ -1382,6 +1382,13 @@ static hipError_t launch_stage_t(int stage, const DecodeArgs& a, bool has_shared
   // on the routed segments fill the GPU and one tile per wave is slower)
   const bool heavy_shared = has_shared && bytes_per_weight_x2(FS) >= 4 * bytes_per_weight_x2(FR);
   if (heavy_shared && a.M <= 2) return launch_one<k1>(g1, a, stream);
+  // one FP8 token: K split two ways (half the rows per workgroup's row group
+  // walk, twice the workgroups); interleaved A/B: C4 b=1 69.6 -> 68.9 us, C2
+  // b=1 30.2 -> 29.3 us; from two tokens equal or slower
+  if (FR == FMT_FP8 && a.M == 1) {
+    constexpr auto kh = decode_stage_kernel<FR, FS, 1, 2, 2>;
+    return launch_one<kh>(dim3(a.H / 64, gy), a, stream);
+  }
   if (fill_of<k2>(g2) >= fill_of<k1>(g1) - kSlack) return launch_one<k2>(g2, a, stream);
   return launch_one<k1>(g1, a, stream);
 }
