@@ -348,8 +348,10 @@ ftmoe_cpu_executor* ftmoe_cpu_executor_create(int threads);
  * run their host functions against the freed executor.  Also refused, at
  * once, when the watchdog abandoned a job that the pool is still computing
  * (a wedged pool: its threads cannot be joined); the caller keeps the handle
- * for the life of the process.  Host functions still queued on a stream must
- * have run (synchronise the stream first). */
+ * for the life of the process.  The stream work of the executor's calls
+ * (host functions, or the flag handshake's stream writes and waits on its
+ * pinned flag words, which are freed here) must have completed: synchronise
+ * the streams first. */
 int ftmoe_cpu_executor_destroy(ftmoe_cpu_executor* ex, int graphs_released);
 const char* ftmoe_cpu_executor_isa(ftmoe_cpu_executor* ex);
 /* Watchdog (replaces the flag watchdog of moe/cpu_executor.py:602-656): a
