@@ -58,6 +58,11 @@ PREFILL_CASES = [
     ("mxfp4_shared", "mxfp4", 32, 1024, 256, 512, 8, True),
     ("fp8_noshared_small", "fp8", 16, 512, 384, 37, 8, False),
     ("bf16", "bf16", 16, 512, 256, 300, 2, False),
+    # every token on 8 of 16 experts: experts of up to 10 M blocks, so the
+    # tile schedule's chunks of 8 (FP8 gate_up) and 2 (down) run full and
+    # with a remainder
+    ("fp8_hot_experts", "fp8", 16, 512, 256, 2560, 8, True),
+    ("mxfp4_hot_experts", "mxfp4", 16, 512, 256, 2560, 8, False),
 ]
 
 
