@@ -344,6 +344,56 @@ def run_prefill(fmt: str, steps: int, warmup: int, gen, dev, M: int = 8192):
     return res
 
 
+def run_dense_fp8_library(dev, steps: int = 10, warmup: int = 3) -> list[dict]:
+    """A library reference point for the prefill GEMMs, not part of the path:
+    ``torch._scaled_mm`` (hipBLASLt) on dense FP8 GEMMs of C5's shapes.  The
+    C5 gate_up and down GEMMs as single dense problems (all routes + shared
+    rows in one M), and one expert's gate_up at C5's mean routes per expert
+    (256), with per-tensor and per-row/column float scales.  Block scales of
+    128 x 128 (the path's format) are tried as well and reported unsupported
+    if the library refuses them."""
+    c = C4
+    H, I = c["H"], c["I"]
+    Mall = 8192 * c["k"] + 8192  # C5: routes + shared-expert rows
+    shapes = [("gate_up_dense", Mall, H, 2 * I), ("down_dense", Mall, I, H), ("gate_up_one_expert", 256, H, 2 * I)]
+    f8 = torch.float8_e4m3fn
+    g = torch.Generator(device=dev).manual_seed(77)
+    out = []
+    for name, M, K, N in shapes:
+        a = (torch.randn((M, K), generator=g, device=dev) * 0.5).to(f8)
+        w = (torch.randn((N, K), generator=g, device=dev) * 0.5).to(f8)
+        b = w.t()  # column-major [K, N], as the library wants its second operand
+        scales = {
+            "tensorwise": (torch.tensor(0.01, device=dev), torch.tensor(0.02, device=dev)),
+            "rowwise": (torch.full((M, 1), 0.01, device=dev), torch.full((1, N), 0.02, device=dev)),
+            "blockwise_1x128_128x128": (torch.full((M, K // 128), 0.01, device=dev),
+                                        torch.full((K // 128, N // 128), 0.02, device=dev)),
+        }
+        for kind, (sa, sb) in scales.items():
+            rec = dict(gemm=name, M=M, K=K, N=N, scales=kind)
+            try:
+                for _ in range(warmup):
+                    y = torch._scaled_mm(a, b, scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+                torch.cuda.synchronize()
+                reps = steps if M > 1024 else 50 * steps
+                t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                t0.record()
+                for _ in range(reps):
+                    y = torch._scaled_mm(a, b, scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+                t1.record()
+                torch.cuda.synchronize()
+                us = t0.elapsed_time(t1) / reps * 1e3
+                tf = 2.0 * M * K * N / (us * 1e-6) / 1e12
+                rec.update(us=round(us, 2), tflops=round(tf, 1), frac_of_fp8_peak=round(tf / PEAK_TFLOPS["fp8"], 4))
+                del y
+            except Exception as e:  # the library refuses this scale layout
+                rec["unsupported"] = f"{type(e).__name__}: {str(e).splitlines()[0][:160]}"
+            out.append(rec)
+        del a, w, b, scales
+        torch.cuda.empty_cache()
+    return out
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 
@@ -874,6 +924,8 @@ def main() -> int:
                     help="time the expert cache's prefill movement (materialize vs double buffer) alone")
     ap.add_argument("--prefill-only", choices=("fp8_block", "mxfp4"), default=None,
                     help="profiling aid: run only the C5 prefill of this format and print its result")
+    ap.add_argument("--dense-fp8-library", action="store_true",
+                    help="reference point only: time hipBLASLt (torch._scaled_mm) on dense FP8 GEMMs of C5's shapes")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
@@ -912,6 +964,11 @@ def main() -> int:
         for M in (1, 4):
             res = run_hybrid(gen, dev, M=M)
             print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}), flush=True)
+        return 0
+
+    if args.dense_fp8_library:
+        for rec in run_dense_fp8_library(dev):
+            print(json.dumps(rec), flush=True)
         return 0
 
     if args.prefill_only:
