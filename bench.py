@@ -497,6 +497,19 @@ def run_ep_share(gen, dev, ep: int = 8, per_gpu_batch: int = 64, steps: int = 20
     t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
+    # instrumented eager pass over the same inputs: per-kernel durations
+    import ctypes
+
+    L = _lib.lib()
+    L.ftmoe_stage_timing_begin()
+    for i in range(min(steps, 64)):
+        ops.experts_decode(xs[i % G], ws[i % G], ids_loc[i % G], bank, out=outs[i % G])
+    torch.cuda.synchronize()
+    arr = (ctypes.c_double * 8)()
+    ns, nc = ctypes.c_int(), ctypes.c_int()
+    _lib.check(L.ftmoe_stage_timing_end(arr, 8, ctypes.byref(ns), ctypes.byref(nc)), "stage timing")
+    names = ["align", "gate_up", "down", "combine"]
+    stage_us = {names[j]: arr[j] / max(1, nc.value) * 1e3 for j in range(min(ns.value, 4))}
     eb = expert_bytes("fp8_block", H, I)
     us = [int(torch.unique(t[t >= 0]).numel()) for t in ids_loc]
     routes = [int((t >= 0).sum()) for t in ids_loc]
@@ -506,7 +519,7 @@ def run_ep_share(gen, dev, ep: int = 8, per_gpu_batch: int = 64, steps: int = 20
                 received_tokens_per_step=statistics.mean(tokens),
                 local_routes_per_step=statistics.mean(routes), local_experts_per_step=statistics.mean(us),
                 ms_per_step=ms, gbs=step_bytes / (ms * 1e-3) / 1e9, hbm_frac=step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                global_tok_s_bound=B / (ms * 1e-3))
+                global_tok_s_bound=B / (ms * 1e-3), stage_us=stage_us)
 
 
 def run_hybrid(gen, dev, M: int = 1, n_sets: int = 4, slots: int = 8, max_fetch: int = 1, steps: int = 8,
