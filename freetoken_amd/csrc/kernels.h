@@ -115,7 +115,7 @@ hipError_t launch_decode_stage(int stage, int fmt_r, int fmt_s, const DecodeArgs
                                bool shared_pieces = true);
 // Router + permutation (as launch_route_align) and, in the same launch, the
 // shared expert's gate_up; hipErrorNotSupported when the call does not
-// qualify (grouped router, shared expert, at most 2 tokens, the one-wave
+// qualify (grouped router, shared expert, at most 4 tokens, the one-wave
 // align, at most 256 experts).
 hipError_t launch_route_shared(const RouteArgs& r, const AlignArgs& al, int fmt_s, const DecodeArgs& a,
                                hipStream_t stream);

@@ -1,6 +1,7 @@
 """Decode calls captured in HIP graphs and replayed: the router + shared
-expert launch (grouped router, up to four tokens), and the wide FP8 segments
-of calls from 144 tokens.  Every replay, with new inputs written into the
+expert launch (grouped router, up to four tokens), the router and the
+permutation in separate launches (40 and 96 tokens), and the wide FP8
+segments of calls from 144 tokens.  Every replay, with new inputs written into the
 captured buffers and an eager call of the same layer between replays, must
 equal the eager call bit for bit (the decode path is fixed-shape and free of
 host synchronisation, as the reference's captured decode requires,
@@ -20,7 +21,8 @@ from _helpers import bf16_dev, code_bank, to_device_bank
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,fmts", [(1, ("fp8", "fp8")), (2, ("mxfp4", "bf16")), (4, ("fp8", "fp8")),
-                                    (160, ("fp8", "fp8")), (256, ("fp8", "fp8"))])
+                                    (40, ("mxfp4", "bf16")), (96, ("fp8", "fp8")), (160, ("fp8", "fp8")),
+                                    (256, ("fp8", "fp8"))])
 def test_routed_decode_graph_replays_equal_eager(dev, M, fmts):
     rng = np.random.default_rng(900 + M)
     E, S, H, I, k = 256, 64, 512, 256, 8

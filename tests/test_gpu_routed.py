@@ -45,14 +45,16 @@ def test_softmax_routed_matches_separate_calls(dev, M, logit_dtype):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16, 33])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16, 33, 96, 160])
 @pytest.mark.parametrize("fmts", [("fp8", "fp8"), ("mxfp4", "bf16")])
 def test_grouped_routed_cached_matches_separate_calls(dev, M, fmts):
     """C4-shaped router (256 experts, 8 groups, top-4 groups, k 8) over a
     64-slot table with misses, with a shared expert (FP8 beside FP8, bf16 beside
     MXFP4 as in C3).  Up to 4 tokens the shared expert's gate_up runs in the
-    router's launch; the outputs must still equal the separate calls bit for
-    bit."""
+    router's launch; from 17 tokens the router and the permutation run in
+    separate launches (M = 33: the gate_up K split four ways; 96: the FP8
+    K-unsplit kernel; 160: the FP8 wide kernel).  The outputs must equal the
+    separate calls bit for bit."""
     rng = np.random.default_rng(100 + M)
     E, S, H, I, k = 256, 64, 512, 256, 8
     bank = to_device_bank(code_bank(fmts[0], S, H, I, rng), dev)
