@@ -148,12 +148,13 @@ def _oracle_routing(layer, logits: np.ndarray):
                                                True, c["scale"])
 
 
-# (layer, batch): C4 at every batch the bench times (1 and 2 run the router
-# and the shared expert's gate_up in one launch; 64 is the headline; 256 the
-# wide segments), C2 (128 FP8 experts, softmax router) and C3 (160 MXFP4
-# experts, bf16 shared expert) at their smallest and largest benched batches
-DECODE_POINTS = [("c4", 1), ("c4", 2), ("c4", 8), ("c4", 32), ("c4", 64), ("c4", 128), ("c4", 192), ("c4", 256),
-                 ("c2", 1), ("c2", 64), ("c3", 1), ("c3", 64)]
+# (layer, batch): every batch the bench times.  C4 (1-4 run the router and
+# the shared expert's gate_up in one launch; 64 is the headline; 192 and 256
+# the wide segments), C2 (128 FP8 experts, softmax router) and C3 (160 MXFP4
+# experts, bf16 shared expert)
+DECODE_POINTS = [("c4", 1), ("c4", 2), ("c4", 4), ("c4", 8), ("c4", 16), ("c4", 32), ("c4", 64), ("c4", 128),
+                 ("c4", 192), ("c4", 256), ("c2", 1), ("c2", 8), ("c2", 32), ("c2", 64), ("c3", 1), ("c3", 8),
+                 ("c3", 32), ("c3", 64)]
 
 
 @pytest.mark.parametrize("name,M", DECODE_POINTS, ids=[f"{n}_b{m}" for n, m in DECODE_POINTS])
